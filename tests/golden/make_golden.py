@@ -1,0 +1,310 @@
+"""Write the golden input/output vectors under ``tests/golden/``.
+
+Run once in the build container (the reference is not available on the GPU
+box):  ``python tests/golden/make_golden.py /root/reference``.
+
+Only reference modules that import without ASE are loaded:
+``rune.mobius.{descriptor,force,layers,message,equivariant}`` and
+``rune.nep.{descriptor,force}``.  ``rune/mobius/model.py`` and ``zbl.py``
+import ``ase.data`` (absent here), so the model-level sequencing of
+``model.py:256-305`` (input projection, residual blocks, direction encoder,
+message blocks, readout) is restated below around the reference's own
+classes, and ZBL (``zbl.py:92-141``) is restated from its closed form.
+Forces and virials of the composed energy come from full autograd through
+positions and a homogeneous strain, as in the reference's own test
+``tests/test_mobius_equivariant.py:111-121``.
+
+Inputs are seeded and small; edges come from the oracle's canonical
+neighbour builder.  Every array is stored in float64.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import math
+import sys
+from pathlib import Path
+
+import numpy as np
+import torch
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parents[1]
+sys.path.insert(0, str(ROOT))
+
+from oracle import neighbors as NB  # noqa: E402
+from rune_amd import workloads as W  # noqa: E402
+from rune_amd.elements import ATOMIC_NUMBERS  # noqa: E402
+
+
+def _import_reference(path):
+    sys.path.insert(0, str(path))
+    from rune.mobius import descriptor as md, force as mf, layers as ml  # noqa
+    from rune.mobius import message as mm, equivariant as me  # noqa
+    from rune.nep import descriptor as nd  # noqa
+    return md, mf, ml, mm, me, nd
+
+
+def _structures():
+    rng = np.random.Generator(np.random.PCG64(20261201))
+    out = {}
+    # FeCFeC triclinic cell, rune tests/test_mobius_gpumd.py:192-195
+    cell = np.array([[4.1, .1, .2], [.0, 4.3, .1], [.1, .0, 4.5]])
+    frac = np.array([[.10, .13, .22], [.82, .21, .37], [.30, .75, .19], [.68, .63, .81]])
+    out["fec4"] = W.Structure(frac @ cell, np.array([26, 6, 26, 6]), cell)
+    s = W.si_diamond(seed=11, reps=1)
+    out["si8"] = s
+    s = W.fcc_alloy(seed=12, reps=2)
+    out["fcc32"] = s
+    length = (96 / 0.08) ** (1 / 3)
+    species = ("O", "Zr", "Ta", "Au", "Cs")
+    pos = W._rsa_cubic(rng, 96, length, 1.8, batch=512)
+    num = np.array([ATOMIC_NUMBERS[species[t]] for t in rng.integers(0, 5, 96)])
+    out["amo96"] = W.Structure(pos, num, np.eye(3) * length)
+    return out
+
+
+def _edges(struct, rc_r, rc_a):
+    nl = NB.build(struct.positions, struct.cell, struct.pbc, rc_r, rc_a)
+    sp = NB.split(nl)
+    return nl, sp
+
+
+def _t(x, dtype=torch.float64):
+    return torch.as_tensor(np.asarray(x), dtype=dtype)
+
+
+def _load(name):
+    ck = torch.load(ROOT / f"rune_amd/assets/models/mobius-oam-{name}/model.pt",
+                    weights_only=True, map_location="cpu")
+    return ck["model_params"], ck["model_state_dict"]
+
+
+def _zbl(vec, center, neighbor, types, n, numbers, inner, outer):
+    """Universal ZBL, restated from ``rune/mobius/zbl.py:92-141``."""
+    e = vec.new_zeros(n)
+    if center.numel() == 0:
+        return e
+    d = torch.clamp(torch.linalg.norm(vec, dim=-1), min=1e-12)
+    zi, zj = numbers[types[center]], numbers[types[neighbor]]
+    a_inv = (zi.pow(0.23) + zj.pow(0.23)) * 2.134563
+    co = vec.new_tensor([[0.18175, 3.1998], [0.50986, 0.94229], [0.28022, 0.4029],
+                         [0.02817, 0.20162]]).float().to(vec.dtype)
+    screened = 14.399645 * zi * zj * torch.sum(
+        co[:, 0] * torch.exp(-co[:, 1] * (d * a_inv).unsqueeze(-1)), -1) / d
+    cut = torch.where(d < inner, torch.ones_like(d), torch.where(
+        d < outer, 0.5 * torch.cos(torch.pi * (d - inner) / (outer - inner)) + 0.5,
+        torch.zeros_like(d)))
+    e.scatter_add_(0, center, 0.5 * screened * cut)
+    return e
+
+
+class Composed(torch.nn.Module):
+    """Reference classes assembled in the order of ``model.py:256-305``."""
+
+    def __init__(self, mods, params, state):
+        super().__init__()
+        md, mf, ml, mm, me, _ = mods
+        p = dict(params)
+        self.p = p
+        self.descriptor = md.Descriptor(dict(p))
+        n_in = p["n_desc_radial"] + p["n_desc_angular"] * self.descriptor.angular.num_L
+        H = p["hidden_dim"]
+        self.register_buffer("q_scaler", torch.ones(n_in))
+        self.input_projection = torch.nn.Linear(n_in, H)
+        self.element_embedding = torch.nn.Embedding(len(p["elements"]), H)
+        self.residual_blocks = torch.nn.ModuleList(
+            ml.ResidualBlock(H, p["ffn_dim"], p["activation"], norm_eps=p["norm_eps"])
+            for _ in range(p["blocks"]))
+        self.output_norm = ml.RMSNorm(H, eps=p["norm_eps"])
+        self.energy_heads = ml.ElementwiseLinearHead(len(p["elements"]), H)
+        kw = dict(hidden_dim=H, message_dim=p["message_dim"], pair_dim=p["pair_dim"],
+                  message_groups=p["message_groups"], n_elements=len(p["elements"]),
+                  basis_size=p["message_basis_size"], cutoff=p["message_cutoff"],
+                  activation=p["activation"], norm_eps=p["norm_eps"])
+        self.eq = p.get("message_mode", "scalar") == "equivariant"
+        if self.eq:
+            self.direction_encoder = me.DirectionEncoder(
+                p["n_desc_angular"], p["equivariant_channels"], p["equivariant_l_max"])
+            self.message_blocks = torch.nn.ModuleList(
+                me.EquivariantBlock(**kw, equivariant_channels=p["equivariant_channels"],
+                                    l_max=p["equivariant_l_max"])
+                for _ in range(p["message_layers"]))
+        else:
+            self.message_blocks = torch.nn.ModuleList(
+                mm.MessageBlock(**kw, vector_channels=p["vector_channels"])
+                for _ in range(p["message_layers"]))
+        self.register_buffer("zbl_numbers", state["zbl.atomic_numbers"].clone())
+        mine = {k: v for k, v in state.items() if not k.startswith("zbl.")}
+        missing, unexpected = self.load_state_dict(mine, strict=False)
+        assert not unexpected, unexpected
+        assert all(k == "zbl_numbers" for k in missing), missing
+
+    def energies(self, batch):
+        st = self.descriptor.compute_state(batch, track_geometry=True)
+        edge = st.radial
+        types = batch["types"]
+        h = self.input_projection(st.values * self.q_scaler) + self.element_embedding(types)
+        for blk in self.residual_blocks:
+            h = blk(h)
+        if self.eq:
+            ang = self.descriptor.angular
+            lq = self.p["equivariant_l_max"]
+            direction = self.direction_encoder(ang.normalized_moments(st.angular.moments, lq))
+            harm = ang.normalized_basis(edge.vectors, lq)
+            for mb in self.message_blocks:
+                h, direction = mb(h, direction, types, edge.center, edge.neighbor,
+                                  edge.vectors, harm)
+        else:
+            for mb in self.message_blocks:
+                h = mb(h, types, edge.center, edge.neighbor, edge.vectors)
+        e = self.energy_heads(self.output_norm(h), types)
+        zbl = self.p.get("zbl")
+        if zbl is not None:
+            e = e + _zbl(edge.vectors, edge.center, edge.neighbor, types, len(types),
+                         self.zbl_numbers.to(e.dtype), float(zbl[0]), float(zbl[1]))
+        return e
+
+
+def _padded(sp, n, kind):
+    c, j, o = sp[kind]
+    cap = max(1, int(np.bincount(c, minlength=n).max(initial=0)) if len(c) else 1)
+    return NB.pack(c, j, o, n, cap)
+
+
+def _batch(struct, types, sp, dtype):
+    n = len(struct)
+    rn, ro = _padded(sp, n, "radial")
+    an, ao = _padded(sp, n, "angular")
+    return {"positions": _t(struct.positions, dtype), "types": torch.as_tensor(types),
+            "radial_neighbors": torch.as_tensor(rn), "radial_offsets": _t(ro, dtype),
+            "angular_neighbors": torch.as_tensor(an), "angular_offsets": _t(ao, dtype),
+            "n_atoms_per_structure": torch.tensor([n])}
+
+
+def _geometry(model, batch):
+    pos = batch["positions"].detach().clone().requires_grad_(True)
+    strain = pos.new_zeros((3, 3), requires_grad=True)
+    deform = torch.eye(3, dtype=pos.dtype) + strain
+    moved = dict(batch)
+    moved["positions"] = pos @ deform.T
+    moved["radial_offsets"] = batch["radial_offsets"] @ deform.T
+    moved["angular_offsets"] = batch["angular_offsets"] @ deform.T
+    e = model.energies(moved)
+    gp, gs = torch.autograd.grad(e.sum(), (pos, strain))
+    return e.detach(), -gp, -gs.reshape(9)
+
+
+def _edge_arrays(sp):
+    out = {}
+    for kind in ("radial", "angular"):
+        c, j, o = sp[kind]
+        out[f"{kind}_center"] = c
+        out[f"{kind}_neighbor"] = j
+        out[f"{kind}_offset"] = o
+    return out
+
+
+def main(reference):
+    mods = _import_reference(reference)
+    md, mf, ml, mm, me, nd = mods
+    structs = _structures()
+    out_files = []
+    for mname in ("loc", "mp", "eq"):
+        params, state = _load(mname)
+        el = params["elements"]
+        for sname, st in structs.items():
+            if mname != "loc" and sname == "si8":
+                continue
+            types = np.array([el.index({v: k for k, v in ATOMIC_NUMBERS.items()}[z])
+                              for z in st.numbers])
+            nl, sp = _edges(st, params["rcut_radial"], params["rcut_angular"])
+            rec = {"positions": st.positions, "cell": st.cell, "types": types,
+                   **_edge_arrays(sp)}
+            for dname, dtype in (("f64", torch.float64), ("f32", torch.float32)):
+                model = Composed(mods, params, state).to(dtype)
+                batch = _batch(st, types, sp, dtype)
+                e, f, v = _geometry(model, batch)
+                rec[f"energies_{dname}"] = e.numpy()
+                rec[f"forces_{dname}"] = f.numpy()
+                rec[f"virial_{dname}"] = v.numpy()
+                if dname == "f64":
+                    state_d = model.descriptor.compute_state(batch)
+                    rec["q"] = state_d.values.detach().numpy()
+                    rec["moments"] = state_d.angular.moments.detach().numpy()
+                    g = torch.Generator().manual_seed(7)
+                    dq = torch.randn(state_d.values.shape, generator=g, dtype=dtype)
+                    dm = torch.randn(state_d.angular.moments.shape, generator=g, dtype=dtype)
+                    fc, vc = mf.contract_forces(model.descriptor, dq, state_d,
+                                                compute_virial=True, moment_gradient=dm)
+                    rec["contract_dq"] = dq.numpy()
+                    rec["contract_dmom"] = dm.numpy()
+                    rec["contract_forces"] = fc.detach().numpy()
+                    rec["contract_atom_virial"] = vc.detach().numpy()
+            path = HERE / f"mobius_{mname}_{sname}.npz"
+            np.savez_compressed(path, **rec)
+            out_files.append(path)
+    # message / equivariant block vectors on the amorphous cell
+    st = structs["amo96"]
+    for mname in ("mp", "eq"):
+        params, state = _load(mname)
+        el = params["elements"]
+        types = np.array([el.index({v: k for k, v in ATOMIC_NUMBERS.items()}[z])
+                          for z in st.numbers])
+        nl, sp = _edges(st, params["rcut_radial"], params["rcut_angular"])
+        model = Composed(mods, params, state).double()
+        blk = model.message_blocks[1]
+        c, j, o = sp["radial"]
+        pos = _t(st.positions)
+        vec = pos[j] + _t(o) - pos[c]
+        g = torch.Generator().manual_seed(9)
+        H = params["hidden_dim"]
+        h = torch.randn((len(st), H), generator=g, dtype=torch.float64)
+        rec = {"positions": st.positions, "types": types, "hidden": h.numpy(),
+               **_edge_arrays(sp)}
+        tt = torch.as_tensor(types)
+        ct, jt = torch.as_tensor(c), torch.as_tensor(j)
+        if mname == "eq":
+            C, lq = params["equivariant_channels"], params["equivariant_l_max"]
+            direction = torch.randn((len(st), C, lq * (lq + 2)), generator=g, dtype=torch.float64)
+            harm = model.descriptor.angular.normalized_basis(vec, lq)
+            hn, dn = blk(h, direction, tt, ct, jt, vec, harm)
+            rec.update(direction=direction.numpy(), harmonics=harm.numpy(),
+                       out_hidden=hn.detach().numpy(), out_direction=dn.detach().numpy())
+            mom = torch.randn((len(st), params["n_desc_angular"], 24), generator=g,
+                              dtype=torch.float64)
+            enc = model.direction_encoder(model.descriptor.angular.normalized_moments(mom, lq))
+            rec.update(enc_moments=mom.numpy(), enc_out=enc.detach().numpy())
+        else:
+            hn = blk(h, tt, ct, jt, vec)
+            rec.update(out_hidden=hn.detach().numpy())
+        path = HERE / f"block_{mname}_amo96.npz"
+        np.savez_compressed(path, **rec)
+        out_files.append(path)
+    # NEP descriptor with seeded coefficient tables (C2 shapes)
+    p = {"n_types": 2, "n_desc_radial": 5, "n_desc_angular": 5, "k_max_radial": 9,
+         "k_max_angular": 9, "rcut_radial": 6.0, "rcut_angular": 4.0, "l_max": 4,
+         "l_max_4body": 2, "l_max_5body": 0}
+    torch.manual_seed(2)
+    desc = nd.Descriptor(dict(p)).double()
+    st = W.rocksalt(seed=13, reps=2)
+    types = (st.numbers == ATOMIC_NUMBERS["Te"]).astype(np.int64)
+    nl, sp = _edges(st, 6.0, 4.0)
+    batch = _batch(st, types, sp, torch.float64)
+    sd = desc.compute_state(batch)
+    rec = {"positions": st.positions, "cell": st.cell, "types": types,
+           "c_radial": desc.radial.c_table.detach().numpy(),
+           "c_angular": desc.angular.c_table.detach().numpy(),
+           "q": sd.values.detach().numpy(), **_edge_arrays(sp)}
+    path = HERE / "nep_desc_pbte64.npz"
+    np.savez_compressed(path, **rec)
+    out_files.append(path)
+    with open(HERE / "MANIFEST.txt", "w") as fh:
+        fh.write("# sha256  file  (written by make_golden.py)\n")
+        for f in out_files:
+            fh.write(f"{hashlib.sha256(f.read_bytes()).hexdigest()}  {f.name}\n")
+    print("\n".join(str(f) for f in out_files))
+
+
+if __name__ == "__main__":
+    main(Path(sys.argv[1] if len(sys.argv) > 1 else "/root/reference"))
