@@ -1,0 +1,536 @@
+// K2 / K3: descriptor forward and its geometry reverse pass (+ ZBL).
+//
+// One 64-lane wavefront per centre atom.  The forward kernel evaluates the
+// Chebyshev radial basis and the real angular polynomials per edge and
+// reduces them into q (rune/mobius/descriptor.py:822-911) in a fixed order;
+// the reverse kernel forms dE/ds from dE/dq (force.py:28-133), contracts it
+// with the per-edge basis Jacobians (force.py:165-243) and adds the ZBL pair
+// term (zbl.py:92-141).  No atomics: every output has one writer.
+#include <cmath>
+
+#include "kernels.hpp"
+
+namespace rune {
+namespace {
+
+constexpr int kWave = 64;
+constexpr float kPi = 3.14159265358979323846f;
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// f_k(r) of descriptor.py:377-414, k < k_max.
+template <int KMAX>
+__device__ inline void chebyshev(float r, float rc, int k_max, float *f) {
+    float rcinv = 1.0f / rc;
+    float arg = kPi * r * rcinv;
+    float fc = 0.5f * cosf(arg) + 0.5f;
+    float rs = r * rcinv - 1.0f;
+    float x = 2.0f * rs * rs - 1.0f;
+    f[0] = fc;
+    float t2 = 1.0f, t1 = x;
+#pragma unroll
+    for (int k = 1; k < KMAX; ++k) {
+        if (k >= k_max) break;
+        float t = (k == 1) ? x : 2.0f * x * t1 - t2;
+        if (k > 1) {
+            t2 = t1;
+            t1 = t;
+        }
+        f[k] = 0.5f * (t + 1.0f) * fc;
+    }
+}
+
+// f_k(r) and d f_k / d r.
+template <int KMAX>
+__device__ inline void chebyshev_d(float r, float rc, int k_max, float *f, float *fp) {
+    float rcinv = 1.0f / rc;
+    float arg = kPi * r * rcinv;
+    float fc = 0.5f * cosf(arg) + 0.5f;
+    float fcp = -0.5f * kPi * rcinv * sinf(arg);
+    float rs = r * rcinv - 1.0f;
+    float x = 2.0f * rs * rs - 1.0f;
+    float dxdr = 4.0f * rs * rcinv;
+    f[0] = fc;
+    fp[0] = fcp;
+    float t2 = 1.0f, t1 = x;      // T_{k-2}, T_{k-1}
+    float u2 = 1.0f, u1 = 2.0f * x;  // U_{k-2}, U_{k-1}
+#pragma unroll
+    for (int k = 1; k < KMAX; ++k) {
+        if (k >= k_max) break;
+        if (k == 1) {
+            float core = 0.5f * (x + 1.0f);
+            f[1] = core * fc;
+            fp[1] = 0.5f * dxdr * fc + core * fcp;
+        } else {
+            float tn = 2.0f * x * t1 - t2;
+            float un = 2.0f * x * u1 - u2;
+            float core = 0.5f * (tn + 1.0f);
+            f[k] = core * fc;
+            fp[k] = 0.5f * float(k) * u1 * dxdr * fc + core * fcp;
+            t2 = t1;
+            t1 = tn;
+            u2 = u1;
+            u1 = un;
+        }
+    }
+}
+
+struct Powers {
+    float zp[kMaxL + 1];
+    float wr[kMaxL + 1];
+    float wi[kMaxL + 1];
+};
+
+__device__ inline void powers(float x, float y, float z, int l_max, Powers &p) {
+    p.zp[0] = 1.0f;
+    p.wr[0] = 1.0f;
+    p.wi[0] = 0.0f;
+#pragma unroll
+    for (int k = 1; k <= kMaxL; ++k) {
+        if (k > l_max) break;
+        p.zp[k] = p.zp[k - 1] * z;
+        p.wr[k] = p.wr[k - 1] * x - p.wi[k - 1] * y;
+        p.wi[k] = p.wr[k - 1] * y + p.wi[k - 1] * x;
+    }
+}
+
+// z-polynomial of order L, |m| = n1 (descriptor.py:601-613) and d/dz.
+__device__ inline void zpoly(const DescTables &t, int L, int n1, const Powers &p, float &zf,
+                             float &zfp) {
+    const float *Z = t.z + t.z_off[L] + n1 * (L + 1);
+    zf = 0.0f;
+    zfp = 0.0f;
+    for (int q = ((L + n1) & 1); q <= L - n1; q += 2) {
+        zf += Z[q] * p.zp[q];
+        if (q > 0) zfp += float(q) * Z[q] * p.zp[q - 1];
+    }
+}
+
+__device__ inline float dot_cubic(const DescTables &t, int which, const float *s) {
+    float r = 0.0f;
+    const float *co = t.cubic_coef + which * kMaxCubic;
+    const int *ix = t.cubic_idx + which * kMaxCubic * 3;
+    for (int k = 0; k < t.cubic_n[which]; ++k)
+        r = r + co[k] * ((s[ix[3 * k]] * s[ix[3 * k + 1]]) * s[ix[3 * k + 2]]);
+    return r;
+}
+
+// q of one angular channel from its moments s[0..nlm) (descriptor.py:650-725).
+__device__ void invariants_of(const DescTables &t, const float *s, float *out, int stride) {
+    int idx = 0;
+    for (int L = 1; L <= t.l_max; ++L) {
+        int st = L * L - 1;
+        float q = t.c3b[st] * s[st] * s[st];
+        float acc = 0.0f;
+        for (int c = 1; c <= 2 * L; ++c) acc += t.c3b[st + c] * s[st + c] * s[st + c];
+        out[stride * idx++] = q + 2.0f * acc;
+    }
+    if (t.has_q[0]) {
+        const float *c = t.c4b;
+        float s3 = s[3], s4 = s[4], s5 = s[5], s6 = s[6], s7 = s[7];
+        out[stride * idx++] = c[0] * s3 * s3 * s3 + c[1] * s3 * (s4 * s4 + s5 * s5) +
+                              c[2] * s3 * (s6 * s6 + s7 * s7) + c[3] * s6 * (s5 * s5 - s4 * s4) +
+                              c[4] * s4 * s5 * s7;
+    }
+    if (t.has_q[1]) {
+        const float *c = t.c5b;
+        float a = s[0] * s[0], b = s[1] * s[1] + s[2] * s[2];
+        out[stride * idx++] = c[0] * a * a + c[1] * a * b + c[2] * b * b;
+    }
+    if (t.has_q[2]) {
+        const float *c = t.c4b2;
+        float a = s[0], b = s[1], cc = s[2], d = s[3], e = s[4], f = s[5], g = s[6], h = s[7];
+        out[stride * idx++] = c[0] * a * a * d + c[1] * a * (b * e + cc * f) +
+                              c[2] * d * (b * b + cc * cc) + c[3] * g * (b * b - cc * cc) +
+                              c[4] * b * cc * h;
+    }
+    for (int w = 0; w < 3; ++w)
+        if (t.has_q[3 + w]) out[stride * idx++] = dot_cubic(t, w, s);
+}
+
+// dE/ds of one channel: W[c] += sum_L dq_L * dq_L/ds_c  (force.py:28-133).
+__device__ void invariant_gradient(const DescTables &t, const float *s, const float *dq,
+                                   int stride, float *W) {
+    int idx = 0;
+    for (int L = 1; L <= t.l_max; ++L) {
+        int st = L * L - 1;
+        float g = dq[stride * idx++];
+        for (int c = 0; c <= 2 * L; ++c)
+            W[st + c] += g * ((c == 0 ? 2.0f : 4.0f) * t.c3b[st + c] * s[st + c]);
+    }
+    if (t.has_q[0]) {
+        const float *c = t.c4b;
+        float g = dq[stride * idx++];
+        float s20 = s[3], s21r = s[4], s21i = s[5], s22r = s[6], s22i = s[7];
+        W[3] += g * (3.0f * c[0] * s20 * s20 + c[1] * (s21r * s21r + s21i * s21i) +
+                     c[2] * (s22r * s22r + s22i * s22i));
+        W[4] += g * (2.0f * c[1] * s20 * s21r - 2.0f * c[3] * s22r * s21r + c[4] * s21i * s22i);
+        W[5] += g * (2.0f * c[1] * s20 * s21i + 2.0f * c[3] * s22r * s21i + c[4] * s21r * s22i);
+        W[6] += g * (2.0f * c[2] * s20 * s22r + c[3] * (s21i * s21i - s21r * s21r));
+        W[7] += g * (2.0f * c[2] * s20 * s22i + c[4] * s21r * s21i);
+    }
+    if (t.has_q[1]) {
+        const float *c = t.c5b;
+        float g = dq[stride * idx++];
+        float s0 = s[0], s1 = s[1], s2 = s[2];
+        float a = s0 * s0, b = s1 * s1 + s2 * s2;
+        float factor = c[1] * a + 2.0f * c[2] * b;
+        W[0] += g * (2.0f * s0 * (2.0f * c[0] * a + c[1] * b));
+        W[1] += g * 2.0f * s1 * factor;
+        W[2] += g * 2.0f * s2 * factor;
+    }
+    if (t.has_q[2]) {
+        const float *c = t.c4b2;
+        float g = dq[stride * idx++];
+        float a = s[0], b = s[1], cc = s[2], d = s[3], e = s[4], f = s[5], gg = s[6], h = s[7];
+        W[0] += g * (2.0f * c[0] * a * d + c[1] * (b * e + cc * f));
+        W[1] += g * (c[1] * a * e + 2.0f * c[2] * d * b + 2.0f * c[3] * gg * b + c[4] * cc * h);
+        W[2] += g * (c[1] * a * f + 2.0f * c[2] * d * cc - 2.0f * c[3] * gg * cc + c[4] * b * h);
+        W[3] += g * (c[0] * a * a + c[2] * (b * b + cc * cc));
+        W[4] += g * c[1] * a * b;
+        W[5] += g * c[1] * a * cc;
+        W[6] += g * c[3] * (b * b - cc * cc);
+        W[7] += g * c[4] * b * cc;
+    }
+    for (int w = 0; w < 3; ++w) {
+        if (!t.has_q[3 + w]) continue;
+        float g = dq[stride * idx++];
+        const float *co = t.cubic_coef + w * kMaxCubic;
+        const int *ix = t.cubic_idx + w * kMaxCubic * 3;
+        for (int k = 0; k < t.cubic_n[w]; ++k) {
+            int a = ix[3 * k], b = ix[3 * k + 1], c = ix[3 * k + 2];
+            float gc = g * co[k];
+            W[a] += gc * (s[b] * s[c]);
+            W[b] += gc * (s[a] * s[c]);
+            W[c] += gc * (s[a] * s[b]);
+        }
+    }
+}
+
+__global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Records r,
+                                                              const int32_t *types, float *q,
+                                                              int ldq, float *moments) {
+    extern __shared__ float lds[];
+    const int nlm = t.nlm, na = t.na, nout = na * nlm;
+    float *gnL = lds;                          // [64][na+1]
+    float *bL = gnL + kWave * (na + 1);        // [64][nlm+1]
+    float *sL = bL + kWave * (nlm + 1);        // [na*nlm]
+    const int i = blockIdx.x;
+    const int lane = threadIdx.x;
+    const int ti = types[i];
+    const int rb = r.view[4 * i], re = r.view[4 * i + 1];
+    const int ab = r.view[4 * i + 2], ae = r.view[4 * i + 3];
+
+    // radial channels
+    float qr[kMaxNr];
+#pragma unroll
+    for (int n = 0; n < kMaxNr; ++n) qr[n] = 0.0f;
+    for (int e = rb + lane; e < re; e += kWave) {
+        float4 v = r.vec[e];
+        int tj = types[r.nbr[e]];
+        float f[kMaxKr];
+        chebyshev<kMaxKr>(v.w, t.rc_r, t.kr, f);
+        const float *row = t.c_radial + size_t(ti * t.n_types + tj) * t.nr * t.kr;
+#pragma unroll
+        for (int n = 0; n < kMaxNr; ++n) {
+            if (n >= t.nr) break;
+            float a = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kMaxKr; ++k) {
+                if (k >= t.kr) break;
+                a += row[n * t.kr + k] * f[k];
+            }
+            qr[n] += a;
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < kMaxNr; ++n) {
+        if (n >= t.nr) break;
+        float v = wave_sum(qr[n]);
+        if (lane == 0) q[size_t(i) * ldq + n] = v;
+    }
+
+    // angular moments s[n][lm] = sum_e gn[e][n] b[e][lm]
+    constexpr int kMaxOut = (kMaxNa * kMaxLm + kWave - 1) / kWave;
+    float acc[kMaxOut];
+#pragma unroll
+    for (int j = 0; j < kMaxOut; ++j) acc[j] = 0.0f;
+    for (int base = ab; base < ae; base += kWave) {
+        int e = base + lane;
+        float *gl = gnL + lane * (na + 1);
+        float *bl = bL + lane * (nlm + 1);
+        if (e < ae) {
+            float4 v = r.vec[e];
+            int tj = types[r.nbr[e]];
+            float f[kMaxKa];
+            chebyshev<kMaxKa>(v.w, t.rc_a, t.ka, f);
+            const float *row = t.c_angular + size_t(ti * t.n_types + tj) * t.na * t.ka;
+            for (int n = 0; n < na; ++n) {
+                float a = 0.0f;
+#pragma unroll
+                for (int k = 0; k < kMaxKa; ++k) {
+                    if (k >= t.ka) break;
+                    a += row[n * t.ka + k] * f[k];
+                }
+                gl[n] = a;
+            }
+            float inv = 1.0f / fmaxf(v.w, 1.0e-12f);
+            Powers p;
+            powers(v.x * inv, v.y * inv, v.z * inv, t.l_max, p);
+            int idx = 0;
+            for (int L = 1; L <= t.l_max; ++L) {
+                for (int n1 = 0; n1 <= L; ++n1) {
+                    float zf, zfp;
+                    zpoly(t, L, n1, p, zf, zfp);
+                    if (n1 == 0) {
+                        bl[idx++] = zf;
+                    } else {
+                        bl[idx++] = zf * p.wr[n1];
+                        bl[idx++] = zf * p.wi[n1];
+                    }
+                }
+            }
+        } else {
+            for (int n = 0; n < na; ++n) gl[n] = 0.0f;
+            for (int c = 0; c < nlm; ++c) bl[c] = 0.0f;
+        }
+        __syncthreads();
+        int cnt = min(kWave, ae - base);
+#pragma unroll
+        for (int j = 0; j < kMaxOut; ++j) {
+            int o = lane + kWave * j;
+            if (o >= nout) break;
+            int n = o / nlm, c = o - n * nlm;
+            float a = 0.0f;
+            for (int k = 0; k < cnt; ++k) a += gnL[k * (na + 1) + n] * bL[k * (nlm + 1) + c];
+            acc[j] += a;
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < kMaxOut; ++j) {
+        int o = lane + kWave * j;
+        if (o >= nout) break;
+        sL[o] = acc[j];
+        moments[size_t(i) * nout + o] = acc[j];
+    }
+    __syncthreads();
+    if (lane < na) invariants_of(t, sL + lane * nlm, q + size_t(i) * ldq + t.nr + lane, na);
+}
+
+__device__ inline void zbl_pair(const ZblTables &z, int ti, int tj, float d, float &e,
+                                float &de) {
+    const float K = 14.399645f;
+    float zi = z.z[ti], zj = z.z[tj];
+    float a_inv = (z.zpow[ti] + z.zpow[tj]) * 2.134563f;
+    float rin = z.rc_inner, rout = z.rc_outer;
+    float co[8];
+    for (int k = 0; k < 8; ++k) co[k] = z.universal[k];
+    if (z.mode == RUNE_ZBL_FLEXIBLE) {
+        int lo = min(ti, tj), hi = max(ti, tj);
+        const float *p = z.pairs + size_t(lo * z.n_types - lo * (lo - 1) / 2 + hi - lo) * 10;
+        rin = p[0];
+        rout = p[1];
+        for (int k = 0; k < 8; ++k) co[k] = p[2 + k];
+    }
+    float x = d * a_inv;
+    float phi = 0.0f, dphi = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        float ex = co[2 * k] * expf(-co[2 * k + 1] * x);
+        phi += ex;
+        dphi += -co[2 * k + 1] * a_inv * ex;
+    }
+    float pref = K * zi * zj;
+    float scr = pref * phi / d;
+    float dscr = pref * (dphi / d - phi / (d * d));
+    float w = fmaxf(rout - rin, 1.0e-12f);
+    float cut, dcut;
+    if (d < rin) {
+        cut = 1.0f;
+        dcut = 0.0f;
+    } else if (d < rout) {
+        float a = kPi * (d - rin) / w;
+        cut = 0.5f * cosf(a) + 0.5f;
+        dcut = -0.5f * kPi / w * sinf(a);
+    } else {
+        cut = 0.0f;
+        dcut = 0.0f;
+    }
+    e = 0.5f * scr * cut;
+    de = 0.5f * (dscr * cut + scr * dcut);
+}
+
+__global__ void __launch_bounds__(kWave) k_descriptor_reverse(
+    DescTables t, ZblTables z, Records r, const int32_t *types, const float *dq, int ldq,
+    const float *moments, const float *dmom, const float4 *g_direct, float *energies,
+    float4 *g, int want_grad) {
+    extern __shared__ float lds[];
+    const int nlm = t.nlm, na = t.na, nout = na * nlm;
+    float *dqL = lds;              // [Q]
+    float *sL = dqL + t.Q;         // [na*nlm]
+    float *WL = sL + nout;         // [na*nlm]
+    const int i = blockIdx.x;
+    const int lane = threadIdx.x;
+    const int ti = types[i];
+    const int rb = r.view[4 * i], re = r.view[4 * i + 1];
+    const int ab = r.view[4 * i + 2], ae = r.view[4 * i + 3];
+    const int eb = r.ptr[i], ee = r.ptr[i + 1];
+    if (want_grad) {
+        for (int k = lane; k < t.Q; k += kWave) dqL[k] = dq[size_t(i) * ldq + k];
+        for (int o = lane; o < nout; o += kWave) {
+            sL[o] = moments[size_t(i) * nout + o];
+            WL[o] = dmom ? dmom[size_t(i) * nout + o] : 0.0f;
+        }
+        __syncthreads();
+        if (lane < na)
+            invariant_gradient(t, sL + lane * nlm, dqL + t.nr + lane, na, WL + lane * nlm);
+        __syncthreads();
+    }
+    float zsum = 0.0f;
+    for (int e = eb + lane; e < ee; e += kWave) {
+        float4 v = r.vec[e];
+        float d = v.w;
+        float inv = 1.0f / fmaxf(d, 1.0e-12f);
+        float ux = v.x * inv, uy = v.y * inv, uz = v.z * inv;
+        int tj = types[r.nbr[e]];
+        float gx = 0.0f, gy = 0.0f, gz = 0.0f;
+        bool in_r = e >= rb && e < re;
+        bool in_a = e >= ab && e < ae;
+        if (want_grad && in_r) {
+            float f[kMaxKr], fp[kMaxKr];
+            chebyshev_d<kMaxKr>(d, t.rc_r, t.kr, f, fp);
+            const float *row = t.c_radial + size_t(ti * t.n_types + tj) * t.nr * t.kr;
+            float gs = 0.0f;
+            for (int n = 0; n < t.nr; ++n) {
+                float a = 0.0f;
+#pragma unroll
+                for (int k = 0; k < kMaxKr; ++k) {
+                    if (k >= t.kr) break;
+                    a += row[n * t.kr + k] * fp[k];
+                }
+                gs += dqL[n] * a;
+            }
+            gx += gs * ux;
+            gy += gs * uy;
+            gz += gs * uz;
+        }
+        if (want_grad && in_a) {
+            float f[kMaxKa], fp[kMaxKa];
+            chebyshev_d<kMaxKa>(d, t.rc_a, t.ka, f, fp);
+            const float *row = t.c_angular + size_t(ti * t.n_types + tj) * t.na * t.ka;
+            float gn[kMaxNa], gnp[kMaxNa];
+#pragma unroll
+            for (int n = 0; n < kMaxNa; ++n) {
+                float a = 0.0f, b = 0.0f;
+                if (n < na) {
+#pragma unroll
+                    for (int k = 0; k < kMaxKa; ++k) {
+                        if (k >= t.ka) break;
+                        float c = row[n * t.ka + k];
+                        a += c * f[k];
+                        b += c * fp[k];
+                    }
+                }
+                gn[n] = a;
+                gnp[n] = b;
+            }
+            Powers p;
+            powers(ux, uy, uz, t.l_max, p);
+            float rs = 0.0f, dx = 0.0f, dy = 0.0f, dz = 0.0f, proj = 0.0f;
+            int c = 0;
+            for (int L = 1; L <= t.l_max; ++L) {
+                for (int n1 = 0; n1 <= L; ++n1) {
+                    float zf, zfp;
+                    zpoly(t, L, n1, p, zf, zfp);
+                    for (int part = 0; part < (n1 == 0 ? 1 : 2); ++part, ++c) {
+                        float b, bx, by, bz;
+                        if (n1 == 0) {
+                            b = zf;
+                            bx = 0.0f;
+                            by = 0.0f;
+                            bz = zfp;
+                        } else if (part == 0) {
+                            b = zf * p.wr[n1];
+                            bx = zf * float(n1) * p.wr[n1 - 1];
+                            by = -zf * float(n1) * p.wi[n1 - 1];
+                            bz = zfp * p.wr[n1];
+                        } else {
+                            b = zf * p.wi[n1];
+                            bx = zf * float(n1) * p.wi[n1 - 1];
+                            by = zf * float(n1) * p.wr[n1 - 1];
+                            bz = zfp * p.wi[n1];
+                        }
+                        float wr = 0.0f, wrp = 0.0f;
+#pragma unroll
+                        for (int n = 0; n < kMaxNa; ++n) {
+                            if (n >= na) break;
+                            float w = WL[n * nlm + c];
+                            wr += w * gn[n];
+                            wrp += w * gnp[n];
+                        }
+                        rs += wrp * b;
+                        dx += wr * bx;
+                        dy += wr * by;
+                        dz += wr * bz;
+                        proj += wr * (ux * bx + uy * by + uz * bz);
+                    }
+                }
+            }
+            gx += rs * ux + (dx - proj * ux) * inv;
+            gy += rs * uy + (dy - proj * uy) * inv;
+            gz += rs * uz + (dz - proj * uz) * inv;
+        }
+        bool in_z = z.mode != RUNE_ZBL_NONE && (z.on_angular ? in_a : in_r);
+        if (in_z) {
+            float ez, dez;
+            zbl_pair(z, ti, tj, fmaxf(d, 1.0e-12f), ez, dez);
+            zsum += ez;
+            gx += dez * ux;
+            gy += dez * uy;
+            gz += dez * uz;
+        }
+        if (want_grad) {
+            if (g_direct) {
+                float4 gd = g_direct[e];
+                gx += gd.x;
+                gy += gd.y;
+                gz += gd.z;
+            }
+            g[e] = make_float4(gx, gy, gz, 0.0f);
+        }
+    }
+    if (z.mode != RUNE_ZBL_NONE) {
+        float s = wave_sum(zsum);
+        if (lane == 0) energies[i] += s;
+    }
+}
+
+}  // namespace
+
+void descriptor_forward(const DescTables &t, const Records &r, const int32_t *types, float *q,
+                        int ldq, float *moments, hipStream_t s) {
+    if (r.n_atoms == 0) return;
+    size_t lds = sizeof(float) * (kWave * (t.na + 1) + kWave * (t.nlm + 1) + t.na * t.nlm);
+    hipLaunchKernelGGL(k_descriptor_forward, dim3(r.n_atoms), dim3(kWave), lds, s, t, r, types,
+                       q, ldq, moments);
+    RUNE_HIP_CHECK(hipGetLastError());
+}
+
+void descriptor_reverse(const DescTables &t, const ZblTables &z, const Records &r,
+                        const int32_t *types, const float *dq, int ldq, const float *moments,
+                        const float *dmom, const float4 *g_direct, float *energies, float4 *g,
+                        int want_grad, hipStream_t s) {
+    if (r.n_atoms == 0) return;
+    if (!want_grad && z.mode == RUNE_ZBL_NONE) return;
+    size_t lds = sizeof(float) * (t.Q + 2 * t.na * t.nlm);
+    hipLaunchKernelGGL(k_descriptor_reverse, dim3(r.n_atoms), dim3(kWave), lds, s, t, z, r,
+                       types, dq, ldq, moments, dmom, g_direct, energies, g, want_grad);
+    RUNE_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace rune

@@ -1,0 +1,109 @@
+// Device-side descriptions of packed model data and kernel launchers.
+#pragma once
+
+#include "common.hpp"
+
+namespace rune {
+
+constexpr int kMaxNr = 16;    // radial descriptor channels  (n_max_radial + 1)
+constexpr int kMaxKr = 24;    // radial basis size           (basis_size_radial + 1)
+constexpr int kMaxNa = 16;    // angular descriptor channels
+constexpr int kMaxKa = 24;    // angular basis size
+constexpr int kMaxL = 8;      // l_max
+constexpr int kMaxLm = kMaxL * (kMaxL + 2);
+constexpr int kMaxCubic = 64; // terms of one cubic invariant
+
+// Descriptor constants and coefficient tables (device pointers).
+struct DescTables {
+    int n_types;
+    int nr, kr, na, ka, l_max, nlm;
+    int num_L, Q;                 // angular invariants per channel, q width
+    int has_q[6];                 // q222 q1111 q112 q123 q233 q134
+    float rc_r, rc_a;
+    const float *c_radial;        // [T,T,nr,kr]
+    const float *c_angular;       // [T,T,na,ka]
+    const float *z;               // Z_L[n1][p] flattened, offsets z_off[L]
+    int z_off[kMaxL + 2];
+    const float *c3b;             // [80]
+    const float *c4b;             // [5]
+    const float *c5b;             // [3]
+    const float *c4b2;            // [5]
+    const float *cubic_coef;      // [3][kMaxCubic]  q123, q233, q134
+    const int *cubic_idx;         // [3][kMaxCubic][3]
+    int cubic_n[3];
+};
+
+// ZBL (rune/mobius/zbl.py:92-141).
+struct ZblTables {
+    int mode;                     // RUNE_ZBL_*
+    int n_types;
+    float rc_inner, rc_outer;
+    const float *z;               // atomic numbers [T]
+    const float *zpow;            // z^0.23 [T]
+    const float *pairs;           // flexible: [T(T+1)/2, 10]
+    const float *universal;       // universal (a_k, b_k) pairs [4, 2]
+    int on_angular;               // 1: evaluate on the angular list (NEP)
+};
+
+// Records of a neighbour list as the kernels see them.
+struct Records {
+    int n_atoms;
+    const int32_t *ptr;           // [N+1]
+    const int32_t *view;          // [N,4] rb re ab ae
+    const int32_t *nbr;           // [E]
+    const float4 *vec;            // [E] {x, y, z, |r|}
+    const int32_t *tptr;          // [N+1]
+    const int32_t *tidx;          // [E]
+    const int32_t *sptr;          // [B+1]
+    int n_structures;
+};
+
+// ---- descriptor (descriptor.hip) ----
+void descriptor_forward(const DescTables &t, const Records &r, const int32_t *types, float *q,
+                        int ldq, float *moments, hipStream_t s);
+// dq: [N, ldq]; dmom: [N, na*nlm] or null; g_direct: [E] or null (added);
+// energies: ZBL energies added when zbl.mode != NONE; g: [E] output.
+void descriptor_reverse(const DescTables &t, const ZblTables &z, const Records &r,
+                        const int32_t *types, const float *dq, int ldq, const float *moments,
+                        const float *dmom, const float4 *g_direct, float *energies, float4 *g,
+                        int want_grad, hipStream_t s);
+
+// ---- dense layers (dense.hip) ----
+struct Epilogue {
+    const float *row_scale = nullptr;   // [M]  v = row_scale[m] * acc
+    const float *bias = nullptr;        // [N]
+    const float *emb = nullptr;         // [T, ld_emb] added at types[m]
+    const int32_t *types = nullptr;
+    int ld_emb = 0;
+    const float *residual = nullptr;    // [M, ldr]
+    int ldr = 0;
+    float *pre = nullptr;               // store pre-activation [M, ldp]
+    int ldp = 0;
+    int act = -1;                       // RUNE_ACT_* applied to the output, -1 none
+    const float *dact_from = nullptr;   // v *= act'(U[m, n]) with U [M, ldu]
+    int ldu = 0;
+    int dact = -1;                      // activation whose derivative is used
+};
+// C[M,N] = A[M,K] B[K,N] (+ epilogue); row-major with leading dimensions.
+void gemm(int M, int N, int K, const float *A, int lda, const float *B, int ldb, float *C,
+          int ldc, const Epilogue &ep, hipStream_t s);
+// inv_rms[m] = rsqrt(mean_n x[m,n]^2 + eps)
+void row_inv_rms(int M, int N, const float *x, int ldx, float eps, float *inv_rms, hipStream_t s);
+// dh[m] = base[m] + r*dz[m] - r^3/N (dz[m].h[m]) h[m]   (RMSNorm backward + residual)
+void rms_backward(int M, int N, const float *h, int ldh, const float *inv_rms, const float *dz,
+                  int ldz, const float *base, int ldb, float *dh, int ldd, hipStream_t s);
+// Möbius readout (layers.py:70-89 on RMSNorm): E = r*(h.hw[t]) + hb[t]; dh = dE/dh.
+void readout(int M, int H, const float *h, int ldh, const int32_t *types, const float *hw,
+             const float *hb, float eps, float *energies, float *dh, int ldd, hipStream_t s);
+// NEP per-element MLP (rune/nep/model.py:157-170): energies and dE/dq.
+void nep_mlp(int M, int Q, int Hn, const float *q, int ldq, const int32_t *types,
+             const float *w0, const float *b0, const float *w1, float shared_bias,
+             float *energies, float *dq, int want_grad, hipStream_t s);
+
+// ---- forces (force.hip) ----
+void forces_and_virial(const Records &r, const float4 *g, float *forces, float *atom_virial,
+                       hipStream_t s);
+// out[b, c] = sum over atoms of structure b of x[m, c] (fixed order, fp64 accumulation)
+void structure_sum(const Records &r, const float *x, int ncol, float *out, hipStream_t s);
+
+}  // namespace rune

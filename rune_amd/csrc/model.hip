@@ -1,0 +1,614 @@
+// Model handle: weight packing and the forward / reverse schedule.
+//
+// Schedule of one call (Mobius.forward, rune/mobius/model.py:307-393):
+//   K2 descriptor forward          q, moments
+//   input projection + residual    h_0 .. h_B            (MFMA GEMMs)
+//   message blocks (MP / EQ)       h, angular states
+//   readout                        E_i and dE/dh
+//   reverse of the above           dE/dq (+ dE/dmoments, direct dE/dr_ij)
+//   K3 descriptor reverse + ZBL    g_e = dE/dr_e per record
+//   K7 forces, per-atom virials, structure totals
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <sstream>
+
+#include "model.hpp"
+
+namespace rune {
+
+namespace {
+thread_local std::string g_last_error;
+
+struct CubicTerm {
+    int coef, sign, a, b, c;
+};
+// Cubic invariant term lists (coefficient index into C4B_123/233/134, sign,
+// component indices), in the order of rune/mobius/descriptor.py:141-196.
+const CubicTerm kQ123[] = {
+    {6, 1, 12, 2, 4}, {6, -1, 11, 2, 5}, {6, 1, 1, 11, 4}, {6, 1, 1, 12, 5}, {5, 1, 0, 11, 6},
+    {5, 1, 0, 12, 7}, {3, 1, 14, 2, 6}, {3, -1, 13, 2, 7}, {3, 1, 1, 13, 6}, {3, 1, 1, 14, 7},
+    {4, 1, 10, 0, 5}, {4, 1, 0, 4, 9},  {1, 1, 10, 2, 3}, {1, 1, 0, 3, 8},  {1, 1, 1, 3, 9},
+    {0, 1, 10, 2, 6}, {0, -1, 10, 1, 7}, {0, -1, 2, 7, 9}, {0, -1, 1, 6, 9}, {2, -1, 2, 5, 8},
+    {2, -1, 1, 4, 8}};
+const CubicTerm kQ233[] = {
+    {0, 1, 3, 8, 8},    {1, 1, 10, 10, 3},  {1, 1, 3, 9, 9},    {2, -1, 10, 10, 6},
+    {2, 1, 6, 9, 9},    {3, 1, 4, 8, 9},    {3, 1, 10, 5, 8},   {4, -1, 13, 13, 3},
+    {4, -1, 14, 14, 3}, {5, -1, 14, 7, 9},  {5, -1, 13, 6, 9},  {5, -1, 10, 14, 6},
+    {5, 1, 10, 13, 7},  {6, 1, 10, 7, 9},   {7, -1, 11, 6, 8},  {7, -1, 12, 7, 8},
+    {8, 1, 11, 4, 9},   {8, 1, 12, 5, 9},   {8, 1, 10, 12, 4},  {8, -1, 10, 11, 5},
+    {9, 1, 12, 14, 4},  {9, 1, 11, 14, 5},  {9, 1, 13, 11, 4},  {9, -1, 13, 12, 5}};
+const CubicTerm kQ134[] = {
+    {0, -1, 10, 15, 2}, {0, -1, 1, 15, 9},  {1, 1, 0, 15, 8},   {2, -1, 1, 13, 18},
+    {2, -1, 1, 14, 19}, {2, -1, 2, 14, 18}, {2, 1, 2, 13, 19},  {3, -1, 10, 18, 2},
+    {3, 1, 1, 10, 19},  {3, 1, 1, 18, 9},   {3, 1, 2, 19, 9},   {4, 1, 1, 16, 8},
+    {4, 1, 2, 17, 8},   {5, 1, 0, 10, 17},  {5, 1, 0, 16, 9},   {5, -1, 1, 11, 16},
+    {5, -1, 1, 12, 17}, {5, -1, 2, 12, 16}, {5, 1, 2, 11, 17},  {6, 1, 1, 13, 22},
+    {6, 1, 1, 14, 23},  {6, -1, 2, 14, 22}, {6, 1, 2, 13, 23},  {7, 1, 0, 11, 18},
+    {7, 1, 0, 12, 19},  {8, 1, 0, 13, 20},  {8, 1, 0, 14, 21},  {9, 1, 1, 11, 20},
+    {9, 1, 1, 12, 21},  {9, -1, 2, 12, 20}, {9, 1, 2, 11, 21}};
+// C4B_123 / C4B_233 / C4B_134 (rune/mobius/descriptor.py:107-139).
+const double kC123[] = {-0.008418146349617, -0.016836292699234, -0.033672585398469,
+                        -0.042090731748086, -0.067345170796937, -0.084181463496172,
+                        -0.168362926992344};
+const double kC233[] = {0.008572620635186, 0.009644198214584, 0.019288396429168,
+                        0.025717861905558, 0.026789439484956, 0.032147327381947,
+                        0.038576792858337, 0.128589309527790, 0.192883964291685,
+                        0.321473273819474};
+const double kC134[] = {0.003645164295772, 0.004860219061029, 0.006075273826286,
+                        0.018225821478859, 0.024301095305146, 0.036451642957719,
+                        0.042526916784005, 0.072903285915437, 0.085053833568010,
+                        0.255161500704030};
+
+std::string str(const char *p) { return p ? std::string(p) : std::string(); }
+}  // namespace
+
+void set_last_error(const std::string &msg) { g_last_error = msg; }
+
+const char *g_last_error_ptr() { return g_last_error.c_str(); }
+
+// ---------------------------------------------------------------------------
+// expected state_dict entries
+// ---------------------------------------------------------------------------
+
+static void expect(ModelImpl &m, const std::string &name, int64_t n) { m.expected[name] = n; }
+
+static void define_expected(ModelImpl &m) {
+    const rune_model_config &c = m.cfg;
+    const int64_t T = c.n_types;
+    expect(m, "q_scaler", m.Q);
+    expect(m, "descriptor.radial.c_table", T * T * c.n_desc_radial * c.k_radial);
+    expect(m, "descriptor.angular.c_table", T * T * c.n_desc_angular * c.k_angular);
+    expect(m, "descriptor.angular.C3B", 80);
+    expect(m, "descriptor.angular.C4B", 5);
+    expect(m, "descriptor.angular.C5B", 3);
+    expect(m, "descriptor.angular.C4B2", 5);
+    for (int L = 1; L <= 8; ++L) expect(m, "descriptor.angular.Z" + std::to_string(L), (L + 1) * (L + 1));
+    if (c.zbl_mode != RUNE_ZBL_NONE) {
+        expect(m, "zbl.atomic_numbers", T);
+        expect(m, "zbl.universal_coefficients", 8);
+        expect(m, "zbl.pair_parameters", c.zbl_mode == RUNE_ZBL_FLEXIBLE ? T * (T + 1) / 2 * 10 : 0);
+    }
+    if (c.family == RUNE_FAMILY_NEP) {
+        for (int t = 0; t < T; ++t) {
+            std::string p = "element_mlps." + m.elements[t] + ".";
+            expect(m, p + "0.weight", int64_t(c.nep_hidden) * m.Q);
+            expect(m, p + "0.bias", c.nep_hidden);
+            expect(m, p + "2.weight", c.nep_hidden);
+        }
+        expect(m, "shared_bias", 1);
+        return;
+    }
+    const int64_t H = c.hidden_dim, F = c.ffn_dim;
+    expect(m, "input_projection.weight", H * m.Q);
+    expect(m, "input_projection.bias", H);
+    expect(m, "element_embedding.weight", T * H);
+    for (int b = 0; b < c.blocks; ++b) {
+        std::string p = "residual_blocks." + std::to_string(b) + ".";
+        expect(m, p + "norm.weight", H);
+        expect(m, p + "ffn.0.weight", F * H);
+        expect(m, p + "ffn.0.bias", F);
+        expect(m, p + "ffn.2.weight", H * F);
+        expect(m, p + "ffn.2.bias", H);
+    }
+    expect(m, "output_norm.weight", H);
+    expect(m, "energy_heads.weight", T * H);
+    expect(m, "energy_heads.bias", T);
+    define_expected_messages(m);
+}
+
+// ---------------------------------------------------------------------------
+// packing
+// ---------------------------------------------------------------------------
+
+size_t Packer::put(const float *p, size_t n) {
+    size_t off = data.size();
+    data.insert(data.end(), p, p + n);
+    while (data.size() % 64) data.push_back(0.0f);
+    return off;
+}
+
+size_t Packer::put(const std::vector<float> &v) { return put(v.data(), v.size()); }
+
+const std::vector<float> &ModelImpl::tensor(const std::string &name) const {
+    auto it = host.find(name);
+    if (it == host.end()) throw Error(RUNE_ERR_STATE, "missing tensor " + name);
+    return it->second;
+}
+
+// W [rows, cols] -> W^T [cols, rows]
+std::vector<float> transpose(const std::vector<float> &w, int rows, int cols) {
+    std::vector<float> t(size_t(rows) * cols);
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c) t[size_t(c) * rows + r] = w[size_t(r) * cols + c];
+    return t;
+}
+
+static void pack_descriptor(ModelImpl &m, Packer &pk, std::map<std::string, size_t> &off) {
+    const rune_model_config &c = m.cfg;
+    off["c_radial"] = pk.put(m.tensor("descriptor.radial.c_table"));
+    off["c_angular"] = pk.put(m.tensor("descriptor.angular.c_table"));
+    std::vector<float> z;
+    int zo = 0;
+    for (int L = 1; L <= 8; ++L) {
+        m.desc.z_off[L] = zo;
+        const auto &t = m.tensor("descriptor.angular.Z" + std::to_string(L));
+        z.insert(z.end(), t.begin(), t.end());
+        zo += int(t.size());
+    }
+    off["z"] = pk.put(z);
+    off["c3b"] = pk.put(m.tensor("descriptor.angular.C3B"));
+    off["c4b"] = pk.put(m.tensor("descriptor.angular.C4B"));
+    off["c5b"] = pk.put(m.tensor("descriptor.angular.C5B"));
+    off["c4b2"] = pk.put(m.tensor("descriptor.angular.C4B2"));
+    std::vector<float> coef(3 * kMaxCubic, 0.0f);
+    std::vector<float> idxf(3 * kMaxCubic * 3, 0.0f);  // stored as int bits
+    const CubicTerm *lists[3] = {kQ123, kQ233, kQ134};
+    const int counts[3] = {int(sizeof(kQ123) / sizeof(CubicTerm)),
+                           int(sizeof(kQ233) / sizeof(CubicTerm)),
+                           int(sizeof(kQ134) / sizeof(CubicTerm))};
+    const double *cvals[3] = {kC123, kC233, kC134};
+    for (int w = 0; w < 3; ++w) {
+        m.desc.cubic_n[w] = counts[w];
+        for (int k = 0; k < counts[w]; ++k) {
+            const CubicTerm &t = lists[w][k];
+            coef[w * kMaxCubic + k] = float(double(t.sign) * cvals[w][t.coef]);
+            int ids[3] = {t.a, t.b, t.c};
+            for (int q = 0; q < 3; ++q)
+                std::memcpy(&idxf[(w * kMaxCubic + k) * 3 + q], &ids[q], sizeof(int));
+        }
+    }
+    off["cubic_coef"] = pk.put(coef);
+    off["cubic_idx"] = pk.put(idxf);
+    if (c.zbl_mode != RUNE_ZBL_NONE) {
+        const auto &zn = m.tensor("zbl.atomic_numbers");
+        std::vector<float> zp(zn.size());
+        for (size_t t = 0; t < zn.size(); ++t) zp[t] = std::pow(zn[t], 0.23f);
+        off["zbl_z"] = pk.put(zn);
+        off["zbl_zpow"] = pk.put(zp);
+        off["zbl_universal"] = pk.put(m.tensor("zbl.universal_coefficients"));
+        const auto &pp = m.tensor("zbl.pair_parameters");
+        off["zbl_pairs"] = pk.put(pp.empty() ? std::vector<float>(10, 0.0f) : pp);
+    }
+}
+
+static void pack_local(ModelImpl &m, Packer &pk, std::map<std::string, size_t> &off) {
+    const rune_model_config &c = m.cfg;
+    const int H = c.hidden_dim, F = c.ffn_dim, Q = m.Q, T = c.n_types;
+    const auto &qs = m.tensor("q_scaler");
+    // input projection with the descriptor scaler folded in: W'[h, q] = W[h, q] * s[q]
+    std::vector<float> win = m.tensor("input_projection.weight");
+    for (int h = 0; h < H; ++h)
+        for (int q = 0; q < Q; ++q) win[size_t(h) * Q + q] *= qs[q];
+    off["in_w"] = pk.put(win);                       // [H, Q]  (reverse: B = W')
+    off["in_wT"] = pk.put(transpose(win, H, Q));     // [Q, H]
+    off["in_b"] = pk.put(m.tensor("input_projection.bias"));
+    off["emb"] = pk.put(m.tensor("element_embedding.weight"));
+    for (int b = 0; b < c.blocks; ++b) {
+        std::string p = "residual_blocks." + std::to_string(b) + ".";
+        const auto &wn = m.tensor(p + "norm.weight");
+        std::vector<float> w1 = m.tensor(p + "ffn.0.weight");  // [F, H], fold norm weight
+        for (int f = 0; f < F; ++f)
+            for (int h = 0; h < H; ++h) w1[size_t(f) * H + h] *= wn[h];
+        const auto &w2 = m.tensor(p + "ffn.2.weight");        // [H, F]
+        off[p + "w1"] = pk.put(w1);
+        off[p + "w1T"] = pk.put(transpose(w1, F, H));
+        off[p + "b1"] = pk.put(m.tensor(p + "ffn.0.bias"));
+        off[p + "w2"] = pk.put(w2);
+        off[p + "w2T"] = pk.put(transpose(w2, H, F));
+        off[p + "b2"] = pk.put(m.tensor(p + "ffn.2.bias"));
+    }
+    std::vector<float> hw = m.tensor("energy_heads.weight");  // [T, H] * output_norm.weight
+    const auto &wo = m.tensor("output_norm.weight");
+    for (int t = 0; t < T; ++t)
+        for (int h = 0; h < H; ++h) hw[size_t(t) * H + h] *= wo[h];
+    off["head_w"] = pk.put(hw);
+    off["head_b"] = pk.put(m.tensor("energy_heads.bias"));
+}
+
+static void pack_nep(ModelImpl &m, Packer &pk, std::map<std::string, size_t> &off) {
+    const int T = m.cfg.n_types, Hn = m.cfg.nep_hidden, Q = m.Q;
+    const auto &qs = m.tensor("q_scaler");
+    std::vector<float> w0, b0, w1;
+    for (int t = 0; t < T; ++t) {
+        std::string p = "element_mlps." + m.elements[t] + ".";
+        std::vector<float> w = m.tensor(p + "0.weight");
+        for (int h = 0; h < Hn; ++h)
+            for (int q = 0; q < Q; ++q) w[size_t(h) * Q + q] *= qs[q];
+        w0.insert(w0.end(), w.begin(), w.end());
+        const auto &b = m.tensor(p + "0.bias");
+        b0.insert(b0.end(), b.begin(), b.end());
+        const auto &o = m.tensor(p + "2.weight");
+        w1.insert(w1.end(), o.begin(), o.end());
+    }
+    off["nep_w0"] = pk.put(w0);
+    off["nep_b0"] = pk.put(b0);
+    off["nep_w1"] = pk.put(w1);
+    m.nep_bias = m.tensor("shared_bias")[0];
+}
+
+static void finalize(ModelImpl &m) {
+    for (const auto &kv : m.expected)
+        if (!m.host.count(kv.first))
+            throw Error(RUNE_ERR_STATE, "missing state_dict tensor " + kv.first);
+    Packer pk;
+    std::map<std::string, size_t> off;
+    pack_descriptor(m, pk, off);
+    if (m.cfg.family == RUNE_FAMILY_NEP) {
+        pack_nep(m, pk, off);
+    } else {
+        pack_local(m, pk, off);
+        pack_messages(m, pk, off);
+    }
+    m.weights.reserve(pk.data.size() * sizeof(float));
+    RUNE_HIP_CHECK(hipMemcpy(m.weights.ptr, pk.data.data(), pk.data.size() * sizeof(float),
+                             hipMemcpyHostToDevice));
+    const float *base = m.weights.as<float>();
+    auto P = [&](const std::string &k) -> const float * {
+        auto it = off.find(k);
+        if (it == off.end()) throw Error(RUNE_ERR_STATE, "internal: no packed " + k);
+        return base + it->second;
+    };
+    DescTables &d = m.desc;
+    d.c_radial = P("c_radial");
+    d.c_angular = P("c_angular");
+    d.z = P("z");
+    d.c3b = P("c3b");
+    d.c4b = P("c4b");
+    d.c5b = P("c5b");
+    d.c4b2 = P("c4b2");
+    d.cubic_coef = P("cubic_coef");
+    d.cubic_idx = reinterpret_cast<const int *>(P("cubic_idx"));
+    ZblTables &z = m.zbl;
+    if (m.cfg.zbl_mode != RUNE_ZBL_NONE) {
+        z.z = P("zbl_z");
+        z.zpow = P("zbl_zpow");
+        z.universal = P("zbl_universal");
+        z.pairs = P("zbl_pairs");
+    }
+    if (m.cfg.family == RUNE_FAMILY_NEP) {
+        m.nep_w0 = P("nep_w0");
+        m.nep_b0 = P("nep_b0");
+        m.nep_w1 = P("nep_w1");
+    } else {
+        m.in_w = P("in_w");
+        m.in_wT = P("in_wT");
+        m.in_b = P("in_b");
+        m.emb = P("emb");
+        m.res.resize(m.cfg.blocks);
+        for (int b = 0; b < m.cfg.blocks; ++b) {
+            std::string p = "residual_blocks." + std::to_string(b) + ".";
+            m.res[b] = {P(p + "w1"), P(p + "w1T"), P(p + "b1"), P(p + "w2"), P(p + "w2T"),
+                        P(p + "b2")};
+        }
+        m.head_w = P("head_w");
+        m.head_b = P("head_b");
+        bind_messages(m, P);
+    }
+    m.host.clear();
+    m.finalized = true;
+}
+
+// ---------------------------------------------------------------------------
+// compute
+// ---------------------------------------------------------------------------
+
+__global__ void k_check_types(int n, const int32_t *types, int n_types, int32_t *flag) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n && (types[i] < 0 || types[i] >= n_types)) atomicOr(flag, 1);
+}
+
+static Records records_of(const rune_nlist *nl) {
+    Records r;
+    r.n_atoms = int(nl->n_atoms);
+    r.ptr = nl->ptr.as<int32_t>();
+    r.view = nl->view.as<int32_t>();
+    r.nbr = nl->nbr.as<int32_t>();
+    r.vec = nl->vec.as<float4>();
+    r.tptr = nl->tptr.as<int32_t>();
+    r.tidx = nl->tidx.as<int32_t>();
+    r.sptr = nl->sptr.as<int32_t>();
+    r.n_structures = nl->n_structures;
+    return r;
+}
+
+static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, int want_f,
+                    int want_w, float *d_energies, float *d_energy, float *d_forces,
+                    float *d_virial, float *d_atom_virial, hipStream_t s) {
+    RUNE_REQUIRE(m.finalized, RUNE_ERR_STATE, "model handle is not finalized");
+    RUNE_REQUIRE(nl, RUNE_ERR_ARGUMENT, "null neighbour list");
+    if (!nl->from_padded) {
+        RUNE_REQUIRE(nl->rc_radial == m.cfg.rc_radial && nl->rc_angular == m.cfg.rc_angular,
+                     RUNE_ERR_STATE, "neighbour list was built with other cutoffs");
+    }
+    const int N = int(nl->n_atoms);
+    const int64_t E = nl->n_records;
+    const int B = nl->n_structures;
+    const bool grad = want_f || want_w;
+    Records r = records_of(nl);
+    const DescTables &d = m.desc;
+    const int ldq = (m.Q + 3) & ~3;
+    const int nmom = d.na * d.nlm;
+    // ---- workspace plan ----
+    Arena ar;
+    size_t o_flag = ar.add(16);
+    size_t o_q = ar.add(4 * size_t(N) * ldq);
+    size_t o_dq = ar.add(4 * size_t(N) * ldq);
+    size_t o_s = ar.add(4 * size_t(N) * nmom);
+    size_t o_e = ar.add(4 * size_t(N));
+    size_t o_g = ar.add(16 * size_t(std::max<int64_t>(E, 1)));
+    size_t o_av = ar.add(4 * size_t(N) * 9);
+    size_t o_f = ar.add(4 * size_t(N) * 3);
+    size_t o_sum = ar.add(4 * size_t(B) * 10);
+    LocalPlan lp = plan_local(m, ar, N);
+    MessagePlan mp = plan_messages(m, ar, N, E);
+    m.work.reserve(ar.total);
+    char *base = m.work.as<char>();
+    int32_t *flag = reinterpret_cast<int32_t *>(base + o_flag);
+    float *q = reinterpret_cast<float *>(base + o_q);
+    float *dq = reinterpret_cast<float *>(base + o_dq);
+    float *mom = reinterpret_cast<float *>(base + o_s);
+    float *energies = d_energies ? d_energies : reinterpret_cast<float *>(base + o_e);
+    float4 *g = reinterpret_cast<float4 *>(base + o_g);
+    float *atom_virial = d_atom_virial ? d_atom_virial : reinterpret_cast<float *>(base + o_av);
+    float *forces = d_forces ? d_forces : reinterpret_cast<float *>(base + o_f);
+    float *sums = reinterpret_cast<float *>(base + o_sum);
+    lp.bind(base);
+    mp.bind(base);
+    // ---- type validation (one small readback) ----
+    RUNE_HIP_CHECK(hipMemsetAsync(flag, 0, 16, s));
+    if (N > 0)
+        hipLaunchKernelGGL(k_check_types, dim3(ceil_div(N, 256)), dim3(256), 0, s, N, types,
+                           m.cfg.n_types, flag);
+    int32_t hflag = 0;
+    RUNE_HIP_CHECK(hipMemcpyAsync(&hflag, flag, 4, hipMemcpyDeviceToHost, s));
+    RUNE_HIP_CHECK(hipStreamSynchronize(s));
+    RUNE_REQUIRE(hflag == 0, RUNE_ERR_TYPE, "atom type outside [0, n_types)");
+    if (N == 0) return;
+    // ---- forward ----
+    descriptor_forward(d, r, types, q, ldq, mom, s);
+    const float4 *g_direct = nullptr;
+    const float *dmom = nullptr;
+    if (m.cfg.family == RUNE_FAMILY_NEP) {
+        nep_mlp(N, m.Q, m.cfg.nep_hidden, q, ldq, types, m.nep_w0, m.nep_b0, m.nep_w1,
+                m.nep_bias, energies, dq, grad ? 1 : 0, s);
+    } else {
+        float *h = local_forward(m, lp, N, q, ldq, types, s);
+        h = messages_forward(m, mp, lp, r, types, mom, h, s, grad);
+        float *dh = grad ? lp.dh_a : nullptr;
+        readout(N, m.cfg.hidden_dim, h, m.cfg.hidden_dim, types, m.head_w, m.head_b,
+                float(m.cfg.norm_eps), energies, dh, m.cfg.hidden_dim, s);
+        if (grad) {
+            dh = messages_backward(m, mp, lp, r, types, mom, dh, s);
+            local_backward(m, lp, N, dh, dq, ldq, s);
+            g_direct = mp.g_direct_used ? mp.g_direct : nullptr;
+            dmom = mp.dmom_used ? mp.dmom : nullptr;
+        }
+    }
+    descriptor_reverse(d, m.zbl, r, types, dq, ldq, mom, dmom, g_direct, energies, g,
+                       grad ? 1 : 0, s);
+    if (d_energy) structure_sum(r, energies, 1, d_energy, s);
+    if (!grad) return;
+    forces_and_virial(r, g, forces, atom_virial, s);
+    if (want_w && d_virial) structure_sum(r, atom_virial, 9, d_virial, s);
+}
+
+// ---- local (descriptor network) part ----
+
+LocalPlan plan_local(ModelImpl &m, Arena &ar, int N) {
+    LocalPlan p;
+    if (m.cfg.family == RUNE_FAMILY_NEP) return p;
+    const int H = m.cfg.hidden_dim, F = m.cfg.ffn_dim, nb = m.cfg.blocks;
+    p.o_h = ar.add(4 * size_t(N) * H * (nb + 1));
+    p.o_r = ar.add(4 * size_t(N) * std::max(nb, 1));
+    p.o_u = ar.add(4 * size_t(N) * F * std::max(nb, 1));
+    p.o_a = ar.add(4 * size_t(N) * F);
+    p.o_dha = ar.add(4 * size_t(N) * H);
+    p.o_dhb = ar.add(4 * size_t(N) * H);
+    p.o_dz = ar.add(4 * size_t(N) * H);
+    p.N = N;
+    p.H = H;
+    p.F = F;
+    return p;
+}
+
+void LocalPlan::bind(char *base) {
+    if (!N) return;
+    h = reinterpret_cast<float *>(base + o_h);
+    r = reinterpret_cast<float *>(base + o_r);
+    u = reinterpret_cast<float *>(base + o_u);
+    a = reinterpret_cast<float *>(base + o_a);
+    dh_a = reinterpret_cast<float *>(base + o_dha);
+    dh_b = reinterpret_cast<float *>(base + o_dhb);
+    dz = reinterpret_cast<float *>(base + o_dz);
+}
+
+float *local_forward(ModelImpl &m, LocalPlan &p, int N, const float *q, int ldq,
+                     const int32_t *types, hipStream_t s) {
+    const int H = p.H, F = p.F, nb = m.cfg.blocks, act = m.cfg.activation;
+    Epilogue e0;
+    e0.bias = m.in_b;
+    e0.emb = m.emb;
+    e0.types = types;
+    e0.ld_emb = H;
+    gemm(N, H, m.Q, q, ldq, m.in_wT, H, p.h, H, e0, s);
+    for (int b = 0; b < nb; ++b) {
+        float *hb = p.h + size_t(b) * N * H;
+        float *hn = p.h + size_t(b + 1) * N * H;
+        float *rb = p.r + size_t(b) * N;
+        float *ub = p.u + size_t(b) * N * F;
+        row_inv_rms(N, H, hb, H, float(m.cfg.norm_eps), rb, s);
+        Epilogue e1;
+        e1.row_scale = rb;
+        e1.bias = m.res[b].b1;
+        e1.pre = ub;
+        e1.ldp = F;
+        e1.act = act;
+        gemm(N, F, H, hb, H, m.res[b].w1T, F, p.a, F, e1, s);
+        Epilogue e2;
+        e2.bias = m.res[b].b2;
+        e2.residual = hb;
+        e2.ldr = H;
+        gemm(N, H, F, p.a, F, m.res[b].w2T, H, hn, H, e2, s);
+    }
+    return p.h + size_t(nb) * N * H;
+}
+
+void local_backward(ModelImpl &m, LocalPlan &p, int N, float *dh, float *dq, int ldq,
+                    hipStream_t s) {
+    const int H = p.H, F = p.F, nb = m.cfg.blocks, act = m.cfg.activation;
+    float *cur = dh;
+    float *other = (dh == p.dh_a) ? p.dh_b : p.dh_a;
+    for (int b = nb - 1; b >= 0; --b) {
+        float *hb = p.h + size_t(b) * N * H;
+        float *rb = p.r + size_t(b) * N;
+        float *ub = p.u + size_t(b) * N * F;
+        Epilogue e1;
+        e1.dact_from = ub;
+        e1.ldu = F;
+        e1.dact = act;
+        gemm(N, F, H, cur, H, m.res[b].w2, F, p.a, F, e1, s);       // du
+        Epilogue e2;
+        gemm(N, H, F, p.a, F, m.res[b].w1, H, p.dz, H, e2, s);      // dz
+        rms_backward(N, H, hb, H, rb, p.dz, H, cur, H, other, H, s);
+        std::swap(cur, other);
+    }
+    Epilogue e3;
+    gemm(N, m.Q, H, cur, H, m.in_w, m.Q, dq, ldq, e3, s);
+}
+
+}  // namespace rune
+
+using namespace rune;
+
+struct rune_model : ModelImpl {};
+
+extern "C" const char *rune_last_error(void) { return g_last_error_ptr(); }
+
+extern "C" const char *rune_version(void) { return "rune_hip 0.1.0 (gfx950)"; }
+
+extern "C" int rune_model_create(const rune_model_config *config, rune_model **out) {
+    return guarded([&] {
+        RUNE_REQUIRE(config && out, RUNE_ERR_ARGUMENT, "null argument");
+        const rune_model_config &c = *config;
+        RUNE_REQUIRE(c.n_types >= 1, RUNE_ERR_ARGUMENT, "n_types must be positive");
+        RUNE_REQUIRE(c.n_desc_radial >= 1 && c.n_desc_radial <= kMaxNr, RUNE_ERR_ARGUMENT,
+                     "n_desc_radial outside [1, 16]");
+        RUNE_REQUIRE(c.k_radial >= 1 && c.k_radial <= kMaxKr, RUNE_ERR_ARGUMENT,
+                     "k_radial outside [1, 24]");
+        RUNE_REQUIRE(c.n_desc_angular >= 1 && c.n_desc_angular <= kMaxNa, RUNE_ERR_ARGUMENT,
+                     "n_desc_angular outside [1, 16]");
+        RUNE_REQUIRE(c.k_angular >= 1 && c.k_angular <= kMaxKa, RUNE_ERR_ARGUMENT,
+                     "k_angular outside [1, 24]");
+        RUNE_REQUIRE(c.l_max >= 1 && c.l_max <= kMaxL, RUNE_ERR_ARGUMENT, "l_max outside [1, 8]");
+        RUNE_REQUIRE(c.rc_radial > 0 && c.rc_angular > 0, RUNE_ERR_ARGUMENT, "bad cutoffs");
+        if ((c.has_q[0] || c.has_q[2]) && c.l_max < 2)
+            throw Error(RUNE_ERR_ARGUMENT, "q222 / q112 require l_max >= 2");
+        if ((c.has_q[3] || c.has_q[4]) && c.l_max < 3)
+            throw Error(RUNE_ERR_ARGUMENT, "q_123 and q_233 require l_max >= 3.");
+        if (c.has_q[5] && c.l_max < 4)
+            throw Error(RUNE_ERR_ARGUMENT, "q_134 requires l_max >= 4.");
+        auto *m = new rune_model();
+        m->cfg = c;
+        m->cfg.elements = nullptr;
+        if (c.elements)
+            for (int t = 0; t < c.n_types; ++t) m->elements.push_back(str(c.elements[t]));
+        if (c.family == RUNE_FAMILY_NEP && int(m->elements.size()) != c.n_types) {
+            delete m;
+            throw Error(RUNE_ERR_ARGUMENT, "NEP models need the element symbols");
+        }
+        int num_L = c.l_max;
+        for (int k = 0; k < 6; ++k) num_L += c.has_q[k] ? 1 : 0;
+        m->Q = c.n_desc_radial + c.n_desc_angular * num_L;
+        DescTables &d = m->desc;
+        d.n_types = c.n_types;
+        d.nr = c.n_desc_radial;
+        d.kr = c.k_radial;
+        d.na = c.n_desc_angular;
+        d.ka = c.k_angular;
+        d.l_max = c.l_max;
+        d.nlm = c.l_max * (c.l_max + 2);
+        d.num_L = num_L;
+        d.Q = m->Q;
+        for (int k = 0; k < 6; ++k) d.has_q[k] = c.has_q[k] ? 1 : 0;
+        d.rc_r = float(c.rc_radial);
+        d.rc_a = float(c.rc_angular);
+        ZblTables &z = m->zbl;
+        z.mode = c.zbl_mode;
+        z.n_types = c.n_types;
+        z.rc_inner = float(c.zbl_rc_inner);
+        z.rc_outer = float(c.zbl_rc_outer);
+        z.on_angular = c.family == RUNE_FAMILY_NEP ? 1 : 0;
+        try {
+            validate_messages(*m);
+            define_expected(*m);
+        } catch (...) {
+            delete m;
+            throw;
+        }
+        *out = m;
+    });
+}
+
+extern "C" void rune_model_destroy(rune_model *model) { delete model; }
+
+extern "C" int rune_model_set_tensor(rune_model *model, const char *name, const float *h_data,
+                                     int64_t n_elements) {
+    return guarded([&] {
+        RUNE_REQUIRE(model && name, RUNE_ERR_ARGUMENT, "null argument");
+        RUNE_REQUIRE(!model->finalized, RUNE_ERR_STATE, "model is already finalized");
+        auto it = model->expected.find(name);
+        RUNE_REQUIRE(it != model->expected.end(), RUNE_ERR_ARGUMENT,
+                     std::string("unexpected state_dict key ") + name);
+        if (it->second != n_elements) {
+            std::ostringstream os;
+            os << "size mismatch for " << name << ": expected " << it->second << " values, got "
+               << n_elements;
+            throw Error(RUNE_ERR_ARGUMENT, os.str());
+        }
+        RUNE_REQUIRE(h_data || n_elements == 0, RUNE_ERR_ARGUMENT, "null data");
+        model->host[name].assign(h_data, h_data + n_elements);
+    });
+}
+
+extern "C" int rune_model_finalize(rune_model *model) {
+    return guarded([&] {
+        RUNE_REQUIRE(model, RUNE_ERR_ARGUMENT, "null model");
+        finalize(*model);
+    });
+}
+
+extern "C" int rune_model_compute(rune_model *model, const rune_nlist *nl, const int32_t *d_types,
+                                  int32_t compute_forces, int32_t compute_virial,
+                                  float *d_energies, float *d_energy, float *d_forces,
+                                  float *d_virial, float *d_atom_virial, void *stream) {
+    return guarded([&] {
+        RUNE_REQUIRE(model, RUNE_ERR_ARGUMENT, "null model");
+        compute(*model, nl, d_types, compute_forces, compute_virial, d_energies, d_energy,
+                d_forces, d_virial, d_atom_virial, as_stream(stream));
+    });
+}
+
+extern "C" int64_t rune_model_workspace_bytes(const rune_model *model) {
+    return model ? int64_t(model->work.bytes) : 0;
+}

@@ -1,0 +1,689 @@
+// K1: canonical periodic neighbour lists (cell-list binning, exact fp64 test).
+//
+// Semantics follow rune/mobius/interface/batch.py:42-102: every image pair
+// (i, j, S) with (p_j + S.cell) - p_i shorter than the cutoff, self pairs at
+// S = 0 excluded, radial and angular membership decided in fp64 by
+//     o_d = (S0*c0d + S1*c1d) + S2*c2d,   v = (p_j + o) - p_i,
+//     d2  = (v0*v0 + v1*v1) + v2*v2 < rc*rc
+// with no fused multiply-add, so the edge set is reproducible bit for bit.
+// Binning only proposes candidates; it never decides membership.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <sstream>
+
+#include "nlist.hpp"
+
+#pragma clang fp contract(off)
+
+namespace rune {
+namespace {
+
+constexpr int kThreads = 256;
+
+struct Geo {
+    double cell[9];     // rows = lattice vectors
+    double inv[9];      // inverse of cell (frac = p . inv)
+    int pbc[3];
+    int nb[3];          // bins per direction
+    int m[3];           // stencil reach per direction
+    int bin_offset;     // first global bin of this structure
+    int atom_begin, atom_end;
+};
+
+__device__ inline int find_structure(const int32_t *sptr, int nstruct, int atom) {
+    int lo = 0, hi = nstruct - 1;
+    while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (sptr[mid] <= atom) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+__device__ inline void frac_of(const Geo &g, const double *p, double *f) {
+    for (int d = 0; d < 3; ++d)
+        f[d] = (p[0] * g.inv[0 * 3 + d] + p[1] * g.inv[1 * 3 + d]) + p[2] * g.inv[2 * 3 + d];
+}
+
+__global__ void bin_atoms(int n, const double *pos, const int32_t *sptr, int nstruct,
+                          const Geo *geo, int32_t *atom_bin, int32_t *atom_wrap,
+                          int32_t *atom_cell, int32_t *bin_count) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int s = find_structure(sptr, nstruct, i);
+    const Geo &g = geo[s];
+    double f[3];
+    frac_of(g, pos + 3 * i, f);
+    int b[3], w[3];
+    for (int d = 0; d < 3; ++d) {
+        double fd = f[d];
+        w[d] = 0;
+        if (g.pbc[d]) {
+            double fl = floor(fd);
+            w[d] = int(fl);
+            fd -= fl;
+        }
+        double x = floor(fd * g.nb[d]);
+        x = fmin(fmax(x, 0.0), double(g.nb[d] - 1));
+        b[d] = int(x);
+    }
+    int flat = g.bin_offset + (b[0] * g.nb[1] + b[1]) * g.nb[2] + b[2];
+    atom_bin[i] = flat;
+    atom_wrap[3 * i + 0] = w[0];
+    atom_wrap[3 * i + 1] = w[1];
+    atom_wrap[3 * i + 2] = w[2];
+    atom_cell[3 * i + 0] = b[0];
+    atom_cell[3 * i + 1] = b[1];
+    atom_cell[3 * i + 2] = b[2];
+    atomicAdd(bin_count + flat, 1);
+}
+
+__global__ void fill_bins(int n, const int32_t *atom_bin, const int32_t *bin_start,
+                          int32_t *bin_cursor, int32_t *bin_atoms) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int b = atom_bin[i];
+    int slot = atomicAdd(bin_cursor + b, 1);
+    bin_atoms[bin_start[b] + slot] = i;
+}
+
+// Exact fp64 squared distance of image (j, S) seen from i.
+__device__ inline double pair_d2(const double *pos, const Geo &g, int i, int j, const int *S,
+                                 double *v) {
+    double r2 = 0.0;
+    for (int d = 0; d < 3; ++d) {
+        double o = (double(S[0]) * g.cell[0 * 3 + d] + double(S[1]) * g.cell[1 * 3 + d]) +
+                   double(S[2]) * g.cell[2 * 3 + d];
+        v[d] = (pos[3 * j + d] + o) - pos[3 * i + d];
+    }
+    r2 = (v[0] * v[0] + v[1] * v[1]) + v[2] * v[2];
+    return r2;
+}
+
+// Packs (class, j, S) into an ordered 64-bit key.
+__device__ inline uint64_t make_key(int cls, int j, const int *S) {
+    uint64_t k = uint64_t(cls) << 62;
+    k |= uint64_t(uint32_t(j)) << 24;
+    k |= uint64_t(uint32_t(S[0] + 128) & 0xff) << 16;
+    k |= uint64_t(uint32_t(S[1] + 128) & 0xff) << 8;
+    k |= uint64_t(uint32_t(S[2] + 128) & 0xff);
+    return k;
+}
+
+template <bool kFill>
+__global__ void enumerate_edges(int n, const double *pos, const int32_t *sptr, int nstruct,
+                                const Geo *geo, const int32_t *atom_wrap,
+                                const int32_t *atom_cell, const int32_t *bin_start,
+                                const int32_t *bin_atoms, double rc2_r, double rc2_a,
+                                double rc2_max, int cls1_radial, int max_r, int max_a,
+                                int32_t *cnt_union, int32_t *cnt_r, int32_t *cnt_a,
+                                int32_t *error_flag, const int32_t *ptr, uint64_t *keys) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int s = find_structure(sptr, nstruct, i);
+    const Geo &g = geo[s];
+    int wi[3] = {atom_wrap[3 * i], atom_wrap[3 * i + 1], atom_wrap[3 * i + 2]};
+    int ci[3] = {atom_cell[3 * i], atom_cell[3 * i + 1], atom_cell[3 * i + 2]};
+    int cu = 0, cr = 0, ca = 0;
+    int base = kFill ? ptr[i] : 0;
+    for (int dx = -g.m[0]; dx <= g.m[0]; ++dx) {
+        for (int dy = -g.m[1]; dy <= g.m[1]; ++dy) {
+            for (int dz = -g.m[2]; dz <= g.m[2]; ++dz) {
+                int dd[3] = {dx, dy, dz};
+                int T[3], bb[3];
+                bool ok = true;
+                for (int d = 0; d < 3; ++d) {
+                    int b = ci[d] + dd[d];
+                    if (g.pbc[d]) {
+                        int t = (b >= 0) ? b / g.nb[d] : -((-b + g.nb[d] - 1) / g.nb[d]);
+                        T[d] = t;
+                        bb[d] = b - t * g.nb[d];
+                    } else {
+                        T[d] = 0;
+                        bb[d] = b;
+                        ok = ok && (b >= 0 && b < g.nb[d]);
+                    }
+                }
+                if (!ok) continue;
+                int flat = g.bin_offset + (bb[0] * g.nb[1] + bb[1]) * g.nb[2] + bb[2];
+                int beg = bin_start[flat], end = bin_start[flat + 1];
+                for (int q = beg; q < end; ++q) {
+                    int j = bin_atoms[q];
+                    int S[3];
+                    for (int d = 0; d < 3; ++d)
+                        S[d] = g.pbc[d] ? (T[d] - atom_wrap[3 * j + d] + wi[d]) : 0;
+                    if (j == i && S[0] == 0 && S[1] == 0 && S[2] == 0) continue;
+                    double v[3];
+                    double r2 = pair_d2(pos, g, i, j, S, v);
+                    if (!(r2 < rc2_max)) continue;
+                    bool in_r = r2 < rc2_r, in_a = r2 < rc2_a;
+                    if (kFill) {
+                        // class 0: inside the smaller cutoff (both lists)
+                        int cls = (in_r && in_a) ? 0 : 1;
+                        keys[base + cu] = make_key(cls, j, S);
+                    }
+                    ++cu;
+                    cr += in_r;
+                    ca += in_a;
+                }
+            }
+        }
+    }
+    if (!kFill) {
+        cnt_union[i] = cu;
+        cnt_r[i] = cr;
+        cnt_a[i] = ca;
+        if (cr > max_r || ca > max_a) atomicOr(error_flag, 1);
+        return;
+    }
+    // insertion sort of this centre's keys: (class, j, S) ascending
+    uint64_t *k = keys + base;
+    for (int a = 1; a < cu; ++a) {
+        uint64_t x = k[a];
+        int b = a - 1;
+        while (b >= 0 && k[b] > x) {
+            k[b + 1] = k[b];
+            --b;
+        }
+        k[b + 1] = x;
+    }
+}
+
+__global__ void decode_records(int n, const double *pos, const int32_t *sptr, int nstruct,
+                               const Geo *geo, const int32_t *ptr, const int32_t *cnt_r,
+                               const int32_t *cnt_a, const uint64_t *keys, int32_t *view,
+                               int32_t *nbr, int32_t *shift, float4 *vec) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int s = find_structure(sptr, nstruct, i);
+    const Geo &g = geo[s];
+    int b = ptr[i], e = ptr[i + 1];
+    view[4 * i + 0] = b;
+    view[4 * i + 1] = b + cnt_r[i];
+    view[4 * i + 2] = b;
+    view[4 * i + 3] = b + cnt_a[i];
+    float pi[3] = {float(pos[3 * i]), float(pos[3 * i + 1]), float(pos[3 * i + 2])};
+    for (int r = b; r < e; ++r) {
+        uint64_t key = keys[r];
+        int j = int((key >> 24) & 0x3fffffffffull);
+        int S[3] = {int((key >> 16) & 0xff) - 128, int((key >> 8) & 0xff) - 128,
+                    int(key & 0xff) - 128};
+        float v[3];
+        for (int d = 0; d < 3; ++d) {
+            double o = (double(S[0]) * g.cell[0 * 3 + d] + double(S[1]) * g.cell[1 * 3 + d]) +
+                       double(S[2]) * g.cell[2 * 3 + d];
+            float pj = float(pos[3 * j + d]);
+            v[d] = (pj + float(o)) - pi[d];
+        }
+        nbr[r] = j;
+        shift[3 * r + 0] = S[0];
+        shift[3 * r + 1] = S[1];
+        shift[3 * r + 2] = S[2];
+        float d2 = v[0] * v[0] + v[1] * v[1] + v[2] * v[2];
+        vec[r] = make_float4(v[0], v[1], v[2], sqrtf(d2));
+    }
+}
+
+// ---- records from padded reference batches ----
+
+__global__ void count_padded(int n, const int64_t *rn, int kr, const int64_t *an, int ka,
+                             int32_t *cnt_union, int32_t *cnt_r, int32_t *cnt_a) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int cr = 0, ca = 0;
+    for (int k = 0; k < kr; ++k) cr += rn[int64_t(i) * kr + k] != -1;
+    for (int k = 0; k < ka; ++k) ca += an[int64_t(i) * ka + k] != -1;
+    cnt_r[i] = cr;
+    cnt_a[i] = ca;
+    cnt_union[i] = cr + ca;
+}
+
+__global__ void fill_padded(int n, const float *pos, const int64_t *rn, const float *ro, int kr,
+                            const int64_t *an, const float *ao, int ka, const int32_t *ptr,
+                            const int32_t *cnt_r, const int32_t *cnt_a, int32_t *view,
+                            int32_t *nbr, int32_t *shift, float4 *vec) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int b = ptr[i];
+    view[4 * i + 0] = b;
+    view[4 * i + 1] = b + cnt_r[i];
+    view[4 * i + 2] = b + cnt_r[i];
+    view[4 * i + 3] = b + cnt_r[i] + cnt_a[i];
+    int r = b;
+    for (int pass = 0; pass < 2; ++pass) {
+        const int64_t *nn = pass ? an : rn;
+        const float *oo = pass ? ao : ro;
+        int kk = pass ? ka : kr;
+        for (int k = 0; k < kk; ++k) {
+            int64_t j = nn[int64_t(i) * kk + k];
+            if (j == -1) continue;
+            const float *o = oo + (int64_t(i) * kk + k) * 3;
+            float v[3];
+            for (int d = 0; d < 3; ++d) v[d] = (pos[3 * j + d] + o[d]) - pos[3 * i + d];
+            nbr[r] = int(j);
+            shift[3 * r] = shift[3 * r + 1] = shift[3 * r + 2] = 0;
+            vec[r] = make_float4(v[0], v[1], v[2], sqrtf(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]));
+            ++r;
+        }
+    }
+}
+
+__global__ void check_padded(int n, int64_t total, const int64_t *rn, int kr, const int64_t *an,
+                             int ka, int32_t *error_flag) {
+    int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= total) return;
+    int64_t v = t < int64_t(n) * kr ? rn[t] : an[t - int64_t(n) * kr];
+    if (v < -1 || v >= n) atomicOr(error_flag, 2);
+}
+
+// ---- transpose: records grouped by neighbour, ascending record id ----
+
+__global__ void count_in(int64_t e, const int32_t *nbr, int32_t *indeg) {
+    int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (r < e) atomicAdd(indeg + nbr[r], 1);
+}
+
+__global__ void fill_in(int64_t e, const int32_t *nbr, const int32_t *tptr, int32_t *cursor,
+                        int32_t *tidx) {
+    int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (r >= e) return;
+    int a = nbr[r];
+    int slot = atomicAdd(cursor + a, 1);
+    tidx[tptr[a] + slot] = int(r);
+}
+
+__global__ void sort_in(int n, const int32_t *tptr, int32_t *tidx) {
+    int a = blockIdx.x * blockDim.x + threadIdx.x;
+    if (a >= n) return;
+    int32_t *k = tidx + tptr[a];
+    int c = tptr[a + 1] - tptr[a];
+    for (int p = 1; p < c; ++p) {
+        int32_t x = k[p];
+        int q = p - 1;
+        while (q >= 0 && k[q] > x) {
+            k[q + 1] = k[q];
+            --q;
+        }
+        k[q + 1] = x;
+    }
+}
+
+// ---- host helpers ----
+
+void invert3(const double *c, double *inv) {
+    double det = c[0] * (c[4] * c[8] - c[5] * c[7]) - c[1] * (c[3] * c[8] - c[5] * c[6]) +
+                 c[2] * (c[3] * c[7] - c[4] * c[6]);
+    RUNE_REQUIRE(std::fabs(det) > 1e-12, RUNE_ERR_ARGUMENT, "cell is singular");
+    double id = 1.0 / det;
+    inv[0] = (c[4] * c[8] - c[5] * c[7]) * id;
+    inv[1] = (c[2] * c[7] - c[1] * c[8]) * id;
+    inv[2] = (c[1] * c[5] - c[2] * c[4]) * id;
+    inv[3] = (c[5] * c[6] - c[3] * c[8]) * id;
+    inv[4] = (c[0] * c[8] - c[2] * c[6]) * id;
+    inv[5] = (c[2] * c[3] - c[0] * c[5]) * id;
+    inv[6] = (c[3] * c[7] - c[4] * c[6]) * id;
+    inv[7] = (c[1] * c[6] - c[0] * c[7]) * id;
+    inv[8] = (c[0] * c[4] - c[1] * c[3]) * id;
+}
+
+void cross(const double *a, const double *b, double *o) {
+    o[0] = a[1] * b[2] - a[2] * b[1];
+    o[1] = a[2] * b[0] - a[0] * b[2];
+    o[2] = a[0] * b[1] - a[1] * b[0];
+}
+
+double norm3(const double *a) { return std::sqrt(a[0] * a[0] + a[1] * a[1] + a[2] * a[2]); }
+
+// Geometry of one structure: bins of width >= rc, stencil reach, capped bin count.
+Geo make_geo(const double *cell_in, const int32_t *pbc, double rc, int n_atoms, int bin_offset,
+             int atom_begin) {
+    Geo g{};
+    std::memcpy(g.cell, cell_in, sizeof(g.cell));
+    for (int d = 0; d < 3; ++d) g.pbc[d] = pbc[d] ? 1 : 0;
+    // a degenerate row in a non-periodic direction gets an orthogonal stand-in:
+    // its shift is always 0, so it only shapes the (clamped) binning
+    for (int d = 0; d < 3; ++d) {
+        if (norm3(g.cell + 3 * d) == 0.0) {
+            RUNE_REQUIRE(!g.pbc[d], RUNE_ERR_ARGUMENT,
+                         "a periodic direction has a zero-length cell vector");
+            const double *a = g.cell + 3 * ((d + 1) % 3);
+            const double *b = g.cell + 3 * ((d + 2) % 3);
+            double c[3];
+            cross(a, b, c);
+            double nc = norm3(c);
+            if (nc == 0.0) {
+                for (int k = 0; k < 3; ++k) g.cell[3 * d + k] = (k == d) ? 3.0 * rc : 0.0;
+            } else {
+                for (int k = 0; k < 3; ++k) g.cell[3 * d + k] = c[k] / nc * 3.0 * rc;
+            }
+        }
+    }
+    invert3(g.cell, g.inv);
+    double vol = std::fabs(g.cell[0] * (g.cell[4] * g.cell[8] - g.cell[5] * g.cell[7]) -
+                           g.cell[1] * (g.cell[3] * g.cell[8] - g.cell[5] * g.cell[6]) +
+                           g.cell[2] * (g.cell[3] * g.cell[7] - g.cell[4] * g.cell[6]));
+    double th[3];
+    for (int d = 0; d < 3; ++d) {
+        double c[3];
+        cross(g.cell + 3 * ((d + 1) % 3), g.cell + 3 * ((d + 2) % 3), c);
+        th[d] = vol / norm3(c);
+        double nb = std::floor(th[d] / (rc * (1.0 + 1e-9)));
+        g.nb[d] = int(std::max(1.0, std::min(nb, 1024.0)));
+    }
+    int64_t cap = std::max<int64_t>(64, 4 * int64_t(n_atoms));
+    while (int64_t(g.nb[0]) * g.nb[1] * g.nb[2] > cap) {
+        int d = 0;
+        for (int k = 1; k < 3; ++k)
+            if (g.nb[k] > g.nb[d]) d = k;
+        g.nb[d] = std::max(1, g.nb[d] / 2);
+    }
+    for (int d = 0; d < 3; ++d) {
+        g.m[d] = int(std::floor(rc * g.nb[d] / th[d])) + 1;
+        if (!g.pbc[d]) g.m[d] = std::min(g.m[d], g.nb[d]);
+        RUNE_REQUIRE(g.m[d] <= 60, RUNE_ERR_ARGUMENT,
+                     "cell is too thin for the cutoff (more than 60 images per direction)");
+    }
+    g.bin_offset = bin_offset;
+    g.atom_begin = atom_begin;
+    g.atom_end = atom_begin + n_atoms;
+    return g;
+}
+
+struct Work {
+    int32_t *atom_bin, *atom_wrap, *atom_cell, *bin_count, *bin_start, *bin_cursor, *bin_atoms;
+    int32_t *cnt_union, *cnt_r, *cnt_a, *flag, *scan_tmp, *indeg;
+    Geo *geo;
+};
+
+void build_transpose(rune_nlist *nl, int32_t *indeg, int32_t *scan_tmp, hipStream_t s) {
+    int n = int(nl->n_atoms);
+    int64_t e = nl->n_records;
+    nl->tptr.reserve(sizeof(int32_t) * (n + 1));
+    nl->tidx.reserve(sizeof(int32_t) * std::max<int64_t>(e, 1));
+    RUNE_HIP_CHECK(hipMemsetAsync(indeg, 0, sizeof(int32_t) * (n + 1), s));
+    if (e > 0)
+        hipLaunchKernelGGL(count_in, dim3(ceil_div(e, kThreads)), dim3(kThreads), 0, s, e,
+                           nl->nbr.as<int32_t>(), indeg);
+    exclusive_scan(indeg, nl->tptr.as<int32_t>(), n, scan_tmp, s);
+    RUNE_HIP_CHECK(hipMemsetAsync(indeg, 0, sizeof(int32_t) * (n + 1), s));
+    if (e > 0) {
+        hipLaunchKernelGGL(fill_in, dim3(ceil_div(e, kThreads)), dim3(kThreads), 0, s, e,
+                           nl->nbr.as<int32_t>(), nl->tptr.as<int32_t>(), indeg,
+                           nl->tidx.as<int32_t>());
+        hipLaunchKernelGGL(sort_in, dim3(ceil_div(n, kThreads)), dim3(kThreads), 0, s, n,
+                           nl->tptr.as<int32_t>(), nl->tidx.as<int32_t>());
+    }
+    RUNE_HIP_CHECK(hipGetLastError());
+}
+
+std::string overflow_message(const std::vector<int32_t> &cr, const std::vector<int32_t> &ca,
+                             int max_r, int max_a) {
+    // the reference checks the radial list first (batch.py:83-96, :20-33)
+    for (int pass = 0; pass < 2; ++pass) {
+        const std::vector<int32_t> &c = pass ? ca : cr;
+        int cap = pass ? max_a : max_r;
+        int best = 0, atom = 0;
+        for (size_t i = 0; i < c.size(); ++i)
+            if (c[i] > best) {
+                best = c[i];
+                atom = int(i);
+            }
+        if (best > cap) {
+            std::ostringstream os;
+            os << "Neighbor count " << best << " for atom " << atom
+               << " exceeds max_neighbors=" << cap
+               << ". Increase max_neighbors_radial or max_neighbors_angular.";
+            return os.str();
+        }
+    }
+    return "neighbour capacity exceeded";
+}
+
+}  // namespace
+}  // namespace rune
+
+using namespace rune;
+
+extern "C" int rune_nlist_create(rune_nlist **out) {
+    return guarded([&] {
+        RUNE_REQUIRE(out, RUNE_ERR_ARGUMENT, "null output pointer");
+        *out = new rune_nlist();
+    });
+}
+
+extern "C" void rune_nlist_destroy(rune_nlist *nl) { delete nl; }
+
+extern "C" int64_t rune_nlist_atoms(const rune_nlist *nl) { return nl ? nl->n_atoms : 0; }
+extern "C" int64_t rune_nlist_records(const rune_nlist *nl) { return nl ? nl->n_records : 0; }
+
+static void set_structures(rune_nlist *nl, int64_t n_atoms, int32_t nstruct,
+                           const int64_t *h_sptr, hipStream_t s) {
+    RUNE_REQUIRE(nstruct >= 1 && h_sptr, RUNE_ERR_ARGUMENT, "need at least one structure");
+    RUNE_REQUIRE(h_sptr[0] == 0 && h_sptr[nstruct] == n_atoms, RUNE_ERR_ARGUMENT,
+                 "structure ranges must cover all atoms");
+    for (int b = 0; b < nstruct; ++b)
+        RUNE_REQUIRE(h_sptr[b + 1] >= h_sptr[b], RUNE_ERR_ARGUMENT,
+                     "structure ranges must be non-decreasing");
+    RUNE_REQUIRE(n_atoms < (int64_t(1) << 30), RUNE_ERR_ARGUMENT, "too many atoms");
+    nl->h_struct_ptr.assign(h_sptr, h_sptr + nstruct + 1);
+    std::vector<int32_t> sp(nstruct + 1);
+    for (int b = 0; b <= nstruct; ++b) sp[b] = int32_t(h_sptr[b]);
+    nl->sptr.reserve(sizeof(int32_t) * (nstruct + 1));
+    RUNE_HIP_CHECK(hipMemcpyAsync(nl->sptr.ptr, sp.data(), sizeof(int32_t) * (nstruct + 1),
+                                  hipMemcpyHostToDevice, s));
+    nl->n_structures = nstruct;
+    nl->n_atoms = n_atoms;
+}
+
+extern "C" int rune_nlist_build(rune_nlist *nl, int64_t n_atoms, const double *d_positions,
+                                int32_t n_structures, const int64_t *h_struct_ptr,
+                                const double *h_cells, const int32_t *h_pbc, double rc_radial,
+                                double rc_angular, int32_t max_radial, int32_t max_angular,
+                                void *stream, int64_t *n_records) {
+    return guarded([&] {
+        RUNE_REQUIRE(nl && (d_positions || n_atoms == 0) && h_cells && h_pbc,
+                     RUNE_ERR_ARGUMENT, "null argument");
+        RUNE_REQUIRE(rc_radial > 0 && rc_angular > 0, RUNE_ERR_ARGUMENT,
+                     "radial and angular cutoffs must be positive");
+        RUNE_REQUIRE(max_radial >= 1 && max_angular >= 1, RUNE_ERR_ARGUMENT,
+                     "radial and angular max-neighbor counts must be positive");
+        hipStream_t s = as_stream(stream);
+        set_structures(nl, n_atoms, n_structures, h_struct_ptr, s);
+        nl->rc_radial = rc_radial;
+        nl->rc_angular = rc_angular;
+        nl->from_padded = false;
+        const int n = int(n_atoms);
+        const double rc = std::max(rc_radial, rc_angular);
+        std::vector<Geo> geo(n_structures);
+        int total_bins = 0;
+        for (int b = 0; b < n_structures; ++b) {
+            int na = int(h_struct_ptr[b + 1] - h_struct_ptr[b]);
+            geo[b] = make_geo(h_cells + 9 * b, h_pbc + 3 * b, rc, na, total_bins,
+                              int(h_struct_ptr[b]));
+            total_bins += geo[b].nb[0] * geo[b].nb[1] * geo[b].nb[2];
+        }
+        // working memory
+        Arena ar;
+        size_t o_geo = ar.add(sizeof(Geo) * n_structures);
+        size_t o_abin = ar.add(4 * size_t(n + 1));
+        size_t o_wrap = ar.add(12 * size_t(n + 1));
+        size_t o_cell = ar.add(12 * size_t(n + 1));
+        size_t o_bcnt = ar.add(4 * size_t(total_bins + 1));
+        size_t o_bst = ar.add(4 * size_t(total_bins + 2));
+        size_t o_bcur = ar.add(4 * size_t(total_bins + 1));
+        size_t o_batm = ar.add(4 * size_t(n + 1));
+        size_t o_cu = ar.add(4 * size_t(n + 1));
+        size_t o_cr = ar.add(4 * size_t(n + 1));
+        size_t o_ca = ar.add(4 * size_t(n + 1));
+        size_t o_flag = ar.add(16);
+        size_t o_scan = ar.add(4 * scan_tmp_ints(std::max(n, total_bins) + 1));
+        size_t o_indeg = ar.add(4 * size_t(n + 1));
+        nl->work.reserve(ar.total);
+        char *base = nl->work.as<char>();
+        Work w;
+        w.geo = reinterpret_cast<Geo *>(base + o_geo);
+        w.atom_bin = reinterpret_cast<int32_t *>(base + o_abin);
+        w.atom_wrap = reinterpret_cast<int32_t *>(base + o_wrap);
+        w.atom_cell = reinterpret_cast<int32_t *>(base + o_cell);
+        w.bin_count = reinterpret_cast<int32_t *>(base + o_bcnt);
+        w.bin_start = reinterpret_cast<int32_t *>(base + o_bst);
+        w.bin_cursor = reinterpret_cast<int32_t *>(base + o_bcur);
+        w.bin_atoms = reinterpret_cast<int32_t *>(base + o_batm);
+        w.cnt_union = reinterpret_cast<int32_t *>(base + o_cu);
+        w.cnt_r = reinterpret_cast<int32_t *>(base + o_cr);
+        w.cnt_a = reinterpret_cast<int32_t *>(base + o_ca);
+        w.flag = reinterpret_cast<int32_t *>(base + o_flag);
+        w.scan_tmp = reinterpret_cast<int32_t *>(base + o_scan);
+        w.indeg = reinterpret_cast<int32_t *>(base + o_indeg);
+        RUNE_HIP_CHECK(hipMemcpyAsync(w.geo, geo.data(), sizeof(Geo) * n_structures,
+                                      hipMemcpyHostToDevice, s));
+        RUNE_HIP_CHECK(hipMemsetAsync(w.bin_count, 0, 4 * size_t(total_bins + 1), s));
+        RUNE_HIP_CHECK(hipMemsetAsync(w.bin_cursor, 0, 4 * size_t(total_bins + 1), s));
+        RUNE_HIP_CHECK(hipMemsetAsync(w.flag, 0, 16, s));
+        nl->ptr.reserve(4 * size_t(n + 1));
+        nl->view.reserve(16 * size_t(n + 1));
+        int gb = ceil_div(std::max(n, 1), kThreads);
+        const int32_t *sptr = nl->sptr.as<int32_t>();
+        if (n > 0) {
+            hipLaunchKernelGGL(bin_atoms, dim3(gb), dim3(kThreads), 0, s, n, d_positions, sptr,
+                               n_structures, w.geo, w.atom_bin, w.atom_wrap, w.atom_cell,
+                               w.bin_count);
+        }
+        exclusive_scan(w.bin_count, w.bin_start, total_bins, w.scan_tmp, s);
+        if (n > 0) {
+            hipLaunchKernelGGL(fill_bins, dim3(gb), dim3(kThreads), 0, s, n, w.atom_bin,
+                               w.bin_start, w.bin_cursor, w.bin_atoms);
+            hipLaunchKernelGGL((enumerate_edges<false>), dim3(gb), dim3(kThreads), 0, s, n,
+                               d_positions, sptr, n_structures, w.geo, w.atom_wrap, w.atom_cell,
+                               w.bin_start, w.bin_atoms, rc_radial * rc_radial,
+                               rc_angular * rc_angular, rc * rc, 0, max_radial, max_angular,
+                               w.cnt_union, w.cnt_r, w.cnt_a, w.flag, nullptr, nullptr);
+        }
+        exclusive_scan(w.cnt_union, nl->ptr.as<int32_t>(), n, w.scan_tmp, s);
+        RUNE_HIP_CHECK(hipGetLastError());
+        int32_t host[2] = {0, 0};
+        RUNE_HIP_CHECK(hipMemcpyAsync(&host[0], nl->ptr.as<int32_t>() + n, 4,
+                                      hipMemcpyDeviceToHost, s));
+        RUNE_HIP_CHECK(hipMemcpyAsync(&host[1], w.flag, 4, hipMemcpyDeviceToHost, s));
+        RUNE_HIP_CHECK(hipStreamSynchronize(s));
+        if (host[1]) {
+            std::vector<int32_t> cr(n), ca(n);
+            RUNE_HIP_CHECK(hipMemcpy(cr.data(), w.cnt_r, 4 * size_t(n), hipMemcpyDeviceToHost));
+            RUNE_HIP_CHECK(hipMemcpy(ca.data(), w.cnt_a, 4 * size_t(n), hipMemcpyDeviceToHost));
+            nl->n_records = 0;
+            throw Error(RUNE_ERR_OVERFLOW, overflow_message(cr, ca, max_radial, max_angular));
+        }
+        int64_t e = host[0];
+        nl->n_records = e;
+        size_t ecap = size_t(std::max<int64_t>(e, 1));
+        nl->keys.reserve(8 * ecap);
+        nl->nbr.reserve(4 * ecap);
+        nl->shift.reserve(12 * ecap);
+        nl->vec.reserve(16 * ecap);
+        if (n > 0) {
+            hipLaunchKernelGGL((enumerate_edges<true>), dim3(gb), dim3(kThreads), 0, s, n,
+                               d_positions, sptr, n_structures, w.geo, w.atom_wrap, w.atom_cell,
+                               w.bin_start, w.bin_atoms, rc_radial * rc_radial,
+                               rc_angular * rc_angular, rc * rc, 0, max_radial, max_angular,
+                               w.cnt_union, w.cnt_r, w.cnt_a, w.flag, nl->ptr.as<int32_t>(),
+                               nl->keys.as<uint64_t>());
+            hipLaunchKernelGGL(decode_records, dim3(gb), dim3(kThreads), 0, s, n, d_positions,
+                               sptr, n_structures, w.geo, nl->ptr.as<int32_t>(), w.cnt_r,
+                               w.cnt_a, nl->keys.as<uint64_t>(), nl->view.as<int32_t>(),
+                               nl->nbr.as<int32_t>(), nl->shift.as<int32_t>(),
+                               nl->vec.as<float4>());
+        }
+        RUNE_HIP_CHECK(hipGetLastError());
+        build_transpose(nl, w.indeg, w.scan_tmp, s);
+        if (n_records) *n_records = e;
+    });
+}
+
+extern "C" int rune_nlist_from_padded(rune_nlist *nl, int64_t n_atoms, const float *d_positions,
+                                      const int64_t *d_radial_nbr, const float *d_radial_off,
+                                      int32_t k_radial, const int64_t *d_angular_nbr,
+                                      const float *d_angular_off, int32_t k_angular,
+                                      int32_t n_structures, const int64_t *h_struct_ptr,
+                                      void *stream, int64_t *n_records) {
+    return guarded([&] {
+        RUNE_REQUIRE(nl, RUNE_ERR_ARGUMENT, "null handle");
+        RUNE_REQUIRE(k_radial >= 0 && k_angular >= 0, RUNE_ERR_ARGUMENT, "negative width");
+        hipStream_t s = as_stream(stream);
+        set_structures(nl, n_atoms, n_structures, h_struct_ptr, s);
+        nl->from_padded = true;
+        const int n = int(n_atoms);
+        Arena ar;
+        size_t o_cu = ar.add(4 * size_t(n + 1));
+        size_t o_cr = ar.add(4 * size_t(n + 1));
+        size_t o_ca = ar.add(4 * size_t(n + 1));
+        size_t o_flag = ar.add(16);
+        size_t o_scan = ar.add(4 * scan_tmp_ints(n + 1));
+        size_t o_indeg = ar.add(4 * size_t(n + 1));
+        nl->work.reserve(ar.total);
+        char *base = nl->work.as<char>();
+        int32_t *cu = reinterpret_cast<int32_t *>(base + o_cu);
+        int32_t *cr = reinterpret_cast<int32_t *>(base + o_cr);
+        int32_t *ca = reinterpret_cast<int32_t *>(base + o_ca);
+        int32_t *flag = reinterpret_cast<int32_t *>(base + o_flag);
+        int32_t *scan_tmp = reinterpret_cast<int32_t *>(base + o_scan);
+        int32_t *indeg = reinterpret_cast<int32_t *>(base + o_indeg);
+        RUNE_HIP_CHECK(hipMemsetAsync(flag, 0, 16, s));
+        nl->ptr.reserve(4 * size_t(n + 1));
+        nl->view.reserve(16 * size_t(n + 1));
+        int gb = ceil_div(std::max(n, 1), kThreads);
+        int64_t slots = int64_t(n) * (k_radial + k_angular);
+        if (slots > 0)
+            hipLaunchKernelGGL(check_padded, dim3(ceil_div(slots, kThreads)), dim3(kThreads), 0,
+                               s, n, slots, d_radial_nbr, k_radial, d_angular_nbr, k_angular,
+                               flag);
+        if (n > 0)
+            hipLaunchKernelGGL(count_padded, dim3(gb), dim3(kThreads), 0, s, n, d_radial_nbr,
+                               k_radial, d_angular_nbr, k_angular, cu, cr, ca);
+        exclusive_scan(cu, nl->ptr.as<int32_t>(), n, scan_tmp, s);
+        int32_t host[2] = {0, 0};
+        RUNE_HIP_CHECK(hipMemcpyAsync(&host[0], nl->ptr.as<int32_t>() + n, 4,
+                                      hipMemcpyDeviceToHost, s));
+        RUNE_HIP_CHECK(hipMemcpyAsync(&host[1], flag, 4, hipMemcpyDeviceToHost, s));
+        RUNE_HIP_CHECK(hipStreamSynchronize(s));
+        RUNE_REQUIRE(host[1] == 0, RUNE_ERR_ARGUMENT,
+                     "neighbour index out of range in padded neighbour list");
+        int64_t e = host[0];
+        nl->n_records = e;
+        size_t ecap = size_t(std::max<int64_t>(e, 1));
+        nl->nbr.reserve(4 * ecap);
+        nl->shift.reserve(12 * ecap);
+        nl->vec.reserve(16 * ecap);
+        if (n > 0)
+            hipLaunchKernelGGL(fill_padded, dim3(gb), dim3(kThreads), 0, s, n, d_positions,
+                               d_radial_nbr, d_radial_off, k_radial, d_angular_nbr,
+                               d_angular_off, k_angular, nl->ptr.as<int32_t>(), cr, ca,
+                               nl->view.as<int32_t>(), nl->nbr.as<int32_t>(),
+                               nl->shift.as<int32_t>(), nl->vec.as<float4>());
+        RUNE_HIP_CHECK(hipGetLastError());
+        build_transpose(nl, indeg, scan_tmp, s);
+        if (n_records) *n_records = e;
+    });
+}
+
+extern "C" int rune_nlist_export(const rune_nlist *nl, int32_t *d_ptr, int32_t *d_view,
+                                 int32_t *d_nbr, int32_t *d_shift, float *d_vec, void *stream) {
+    return guarded([&] {
+        RUNE_REQUIRE(nl, RUNE_ERR_ARGUMENT, "null handle");
+        hipStream_t s = as_stream(stream);
+        size_t n = size_t(nl->n_atoms), e = size_t(nl->n_records);
+        if (d_ptr)
+            RUNE_HIP_CHECK(hipMemcpyAsync(d_ptr, nl->ptr.ptr, 4 * (n + 1),
+                                          hipMemcpyDeviceToDevice, s));
+        if (d_view && n)
+            RUNE_HIP_CHECK(hipMemcpyAsync(d_view, nl->view.ptr, 16 * n, hipMemcpyDeviceToDevice, s));
+        if (e) {
+            if (d_nbr)
+                RUNE_HIP_CHECK(hipMemcpyAsync(d_nbr, nl->nbr.ptr, 4 * e, hipMemcpyDeviceToDevice, s));
+            if (d_shift)
+                RUNE_HIP_CHECK(hipMemcpyAsync(d_shift, nl->shift.ptr, 12 * e,
+                                              hipMemcpyDeviceToDevice, s));
+            if (d_vec)
+                RUNE_HIP_CHECK(hipMemcpyAsync(d_vec, nl->vec.ptr, 16 * e, hipMemcpyDeviceToDevice, s));
+        }
+    });
+}

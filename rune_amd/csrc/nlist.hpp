@@ -1,0 +1,35 @@
+// Internal layout of a neighbour-list handle (shared by the model code).
+#pragma once
+
+#include "common.hpp"
+
+struct rune_nlist {
+    int64_t n_atoms = 0;
+    int64_t n_records = 0;
+    int32_t n_structures = 0;
+    double rc_radial = 0.0, rc_angular = 0.0;
+    bool from_padded = false;
+    std::vector<int64_t> h_struct_ptr;   // host copy of structure ranges
+
+    // records (see include/rune_hip.h)
+    rune::DeviceBuffer ptr;      // int32 [N+1]
+    rune::DeviceBuffer view;     // int32 [N,4] {rb, re, ab, ae}
+    rune::DeviceBuffer nbr;      // int32 [E]
+    rune::DeviceBuffer shift;    // int32 [E,3]
+    rune::DeviceBuffer vec;      // float4 [E]
+    // transpose: records whose neighbour is atom a, ascending record id
+    rune::DeviceBuffer tptr;     // int32 [N+1]
+    rune::DeviceBuffer tidx;     // int32 [E]
+    rune::DeviceBuffer sptr;     // int32 [B+1] device copy of structure ranges
+    // working memory of the builder
+    rune::DeviceBuffer work;
+    rune::DeviceBuffer keys;     // uint64 [E]
+    rune::DeviceBuffer pinned_dummy;
+};
+
+namespace rune {
+// Exclusive scan of n int32 values: out[0..n] with out[n] = total.
+// tmp must hold scan_tmp_ints(n) ints.
+size_t scan_tmp_ints(int64_t n);
+void exclusive_scan(const int32_t *in, int32_t *out, int64_t n, int32_t *tmp, hipStream_t s);
+}  // namespace rune
