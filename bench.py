@@ -1,0 +1,254 @@
+"""Benchmark: atom-steps/s of E + F + virial on one MI355X.
+
+One step = one full evaluation of the hot path on one batch: the GPU
+neighbour search (cell list, canonical sorted records, transpose), the
+descriptor, the network with its reverse pass, forces and virials.  Inputs
+(fp64 positions, types) are resident in HBM before the timed region.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C1..C5]
+
+Prints one JSON line.  ``roofline`` describes the phase with the largest
+measured time (HIP events recorded by the library on its launch stream);
+``phases`` lists every phase with its algorithmic traffic or FLOP count.
+``cpu_baseline`` times the CPU oracle (the op-for-op restatement of the
+reference PyTorch path) on the host cores on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK = 8.0e12           # bytes/s, MI355X HBM3E
+FP32_PEAK = 157.3e12        # FLOP/s, MI355X dense fp32 (matrix and vector)
+
+WORKLOADS = {
+    "C1": "Mobius-Local (oam-loc), Si diamond a=5.43 4x4x4 = 512 atoms, sigma 0.05",
+    "C2": "NEP4 seeded (Pb/Te, n_max 4/4, basis 8/8, l_max 4 + q222, rc 6/4, 30 hidden), "
+          "rock salt a=6.46 12^3 = 13824 atoms, sigma 0.05",
+    "C3": "Mobius-MP (oam-mp), 5-element FCC a=3.6 17^3 = 19652 atoms, sigma 0.1",
+    "C4": "Mobius-EQ (oam-eq), 100000-atom amorphous cell, 0.08 /A^3, dmin 1.8, 10 elements",
+    "C5": "Mobius-EQ (oam-eq), 256 small triclinic cells of 8-64 atoms",
+}
+DEFAULT_WORKLOAD = "C2"
+
+
+def build_workload(name, device):
+    import torch
+    from rune_amd import _native as N
+    from rune_amd import workloads as W
+    from rune_amd.api import Evaluator, load_checkpoint
+    if name == "C2":
+        from rune_amd.nep.model import seeded_nep
+        model = seeded_nep(seed=0)
+        params, state, family = model.params, model.state_dict(), N.FAMILY_NEP
+        structures = W.rocksalt()
+    else:
+        kind = {"C1": "loc", "C3": "mp", "C4": "eq", "C5": "eq"}[name]
+        _, params, state = load_checkpoint(ROOT / f"rune_amd/assets/models/mobius-oam-{kind}/model.pt")
+        family = N.FAMILY_MOBIUS
+        structures = {"C1": W.si_diamond, "C3": W.fcc_alloy, "C4": W.amorphous,
+                      "C5": W.small_cells}[name]()
+    ev = Evaluator(params, state, family, device=device)
+    return ev, structures, params, state, family
+
+
+def phase_model(ev, prep, n_records, n_short, params):
+    """Algorithmic bytes (HBM-bound phases) and FLOPs (dense phases) per call.
+
+    Unique compulsory bytes: every per-atom / per-record array the phase must
+    read or write is counted once, weights excluded.  Records: int32 neighbour
+    (4 B), float4 vector (16 B), float4 gradient (16 B).
+    """
+    N = prep.n_atoms
+    E = n_records
+    p = params
+    nr, na = p["n_desc_radial"], p["n_desc_angular"]
+    nlm = p["l_max"] * (p["l_max"] + 2)
+    num_L = p["l_max"] + sum(int(p.get(k, 0)) for k in
+                             ("has_q_222", "has_q_1111", "has_q_112", "has_q_123", "has_q_233",
+                              "has_q_134"))
+    Q = nr + na * num_L
+    mom = 4 * na * nlm
+    out = {}
+    # K2: records (nbr, vec, neighbour type) + atom header (view 16, type 4) + q + moments out
+    out["descriptor"] = ("hbm", E * (4 + 16 + 4) + N * (16 + 4 + 4 * Q + mom))
+    # K3: records in (nbr, vec, type) + g out; atom: view/ptr, type, dq, moments, energy r/w
+    out["reverse"] = ("hbm", E * (4 + 16 + 4 + 16) + N * (20 + 4 + 4 * Q + mom + 8))
+    # K7: g by centre + g via transpose (idx 4 + g 16 + vec 16); forces, atom virial, sums
+    out["forces"] = ("hbm", E * (16 + 4 + 16 + 16) + N * (8 + 12 + 36 + 4 + 36))
+    if ev.family == 0:
+        H, F, nb = p["hidden_dim"], p["ffn_dim"], p["blocks"]
+        fwd = 2 * N * (Q * H + nb * 2 * H * F)
+        out["dense_fwd"] = ("mfma", fwd)
+        out["dense_bwd"] = ("mfma", fwd)
+        out["readout"] = ("hbm", N * (4 * H * 2 + 8))
+    else:
+        Hn = p["hidden_dims"][0]
+        out["readout"] = ("mfma", 2 * N * 2 * Q * Hn)
+    return out
+
+
+def run_gpu(args):
+    import torch
+    device = torch.device("cuda:0")
+    ev, structures, params, state, family = build_workload(args.workload, device)
+    prep = ev.prepare(structures)
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        ev.evaluate(prep)
+    torch.cuda.synchronize()
+    ev.native.timing(True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    nl_ms = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        out = ev.evaluate(prep)
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = start.elapsed_time(stop)
+    phases, calls = ev.native.timing_read()
+    ev.native.timing(False)
+    # neighbour build alone (events around the call, includes its count readback)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(max(3, min(args.steps, 10))):
+        a.record()
+        ev.build_neighbors(prep)
+        b.record()
+        torch.cuda.synchronize()
+        nl_ms.append(a.elapsed_time(b))
+    n_atoms = prep.n_atoms
+    n_records = ev.nlist.n_records
+    ms_per_step = max(gpu_ms, wall * 1e3) / args.steps
+    value = n_atoms * args.steps / (ms_per_step * args.steps / 1e3)
+    model = phase_model(ev, prep, n_records, None, params)
+    per_phase = {}
+    for name, total in phases.items():
+        avg = total / max(calls, 1)
+        entry = {"ms": round(avg, 4)}
+        if name in model and avg > 0:
+            bound, work = model[name]
+            if bound == "hbm":
+                ach = work / (avg / 1e3)
+                entry.update(bound="hbm", bytes=int(work), achieved_GBs=round(ach / 1e9, 1),
+                             frac=round(ach / HBM_PEAK, 4))
+            else:
+                ach = work / (avg / 1e3)
+                entry.update(bound="mfma", flops=int(work), achieved_TFs=round(ach / 1e12, 2),
+                             frac=round(ach / FP32_PEAK, 4))
+        per_phase[name] = entry
+    per_phase["neighbors"] = {"ms": round(statistics.median(nl_ms), 4)}
+    # dominant measured phase that has a work model
+    cands = [(v["ms"], k) for k, v in per_phase.items() if "frac" in v]
+    dom = max(cands)[1]
+    d = per_phase[dom]
+    if d["bound"] == "hbm":
+        roof = {"kernel": dom, "bound": "hbm", "achieved": d["achieved_GBs"],
+                "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": d["frac"], "traffic": None,
+                "algorithmic_bytes": d["bytes"], "avg_ms": d["ms"]}
+    else:
+        roof = {"kernel": dom, "bound": "mfma", "achieved": d["achieved_TFs"],
+                "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s", "frac": d["frac"], "traffic": None,
+                "algorithmic_flops": d["flops"], "avg_ms": d["ms"]}
+    return {
+        "value": value, "ms_per_step": ms_per_step, "n_atoms": n_atoms, "n_records": n_records,
+        "roofline": roof, "phases": per_phase,
+        "energy": float(out["energy"].double().sum().cpu()),
+    }
+
+
+def cpu_baseline(workload, budget_s):
+    """Oracle (op-for-op CPU restatement of the reference path) on the host cores."""
+    import torch
+    from oracle import model as OM
+    from oracle import neighbors as ONB
+    from rune_amd import workloads as W
+    from rune_amd.api import load_checkpoint
+    from rune_amd.elements import ATOMIC_NUMBERS
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    if workload == "C2":
+        from rune_amd.nep.model import seeded_nep
+        model = seeded_nep(seed=0)
+        params, state = model.params, model.state_dict()
+        struct = W.rocksalt(reps=6)
+        fwd = OM.nep_forward
+        sample = "rock salt 6^3 = 1728 atoms (same generator), model-only forward+forces+virial"
+    else:
+        kind = {"C1": "loc", "C3": "mp", "C4": "eq", "C5": "eq"}[workload]
+        _, params, state = load_checkpoint(ROOT / f"rune_amd/assets/models/mobius-oam-{kind}/model.pt")
+        fwd = OM.forward
+        if workload == "C1":
+            struct, sample = W.si_diamond(), "the full 512-atom cell"
+        elif workload == "C3":
+            struct, sample = W.fcc_alloy(reps=6), "FCC 6^3 = 864 atoms (same generator)"
+        else:
+            struct, sample = W.amorphous(n_atoms=500), "500-atom amorphous cell (same generator)"
+        sample += ", model-only forward+forces+virial"
+    el = params["elements"]
+    z2t = {ATOMIC_NUMBERS[e]: t for t, e in enumerate(el)}
+    types = torch.as_tensor([z2t[z] for z in struct.numbers], dtype=torch.long)
+    nl = ONB.build(struct.positions, struct.cell, struct.pbc, params["rcut_radial"],
+                   params["rcut_angular"])
+    sp = ONB.split(nl)
+    edges = {k: OM.Edges(torch.as_tensor(v[0]), torch.as_tensor(v[1]),
+                         torch.as_tensor(v[2], dtype=torch.float32)) for k, v in sp.items()}
+    w = {k: (v.float() if v.is_floating_point() else v) for k, v in state.items()}
+    pos = torch.as_tensor(struct.positions, dtype=torch.float32)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        fwd(w, params, pos, types, [len(struct)], edges["radial"], edges["angular"])
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 3 and time.perf_counter() > t_end:
+            break
+    med = statistics.median(times[1:]) if len(times) > 1 else times[0]
+    return {"value": len(struct) / med, "unit": "atom-steps/s", "cores": cores, "kind": "port",
+            "sample": f"{sample}; median of {len(times) - 1} calls after 1 warm-up, "
+                      f"{med * 1e3:.1f} ms/call"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build evaluates on one GPU only; the multi-GPU "
+                          "(spatial decomposition) path is a design, see DESIGN.md"}))
+        sys.exit(2)
+    res = run_gpu(args)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.workload, args.cpu_budget)
+    line = {
+        "metric": "atom-steps/sec (E+F+virial) on 1 MI355X; % HBM/MFMA roofline vs CPU path",
+        "value": round(res["value"], 1), "unit": "atom-steps/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res["ms_per_step"], 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded generator); trained OAM weights / seeded NEP",
+        "config": {"workload": args.workload, "description": WORKLOADS[args.workload],
+                   "n_atoms": res["n_atoms"], "records": res["n_records"]},
+        "roofline": res["roofline"], "cpu_baseline": cpu, "phases": res["phases"],
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

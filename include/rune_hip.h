@@ -177,6 +177,25 @@ int rune_model_compute(rune_model *model, const rune_nlist *nl, const int32_t *d
 /* Bytes of device workspace the handle currently holds. */
 int64_t rune_model_workspace_bytes(const rune_model *model);
 
+/* Phase timing.  When enabled, rune_model_compute records a HIP event on its
+ * stream at every phase boundary (no synchronisation inside the call; the last
+ * 256 calls are kept).  rune_model_timing_read waits for those events and
+ * returns the summed milliseconds per phase and the number of calls.
+ * (No counterpart in the reference; it feeds the roofline measurement.) */
+enum {
+    RUNE_PHASE_DESCRIPTOR = 0,   /* K2 descriptor forward                       */
+    RUNE_PHASE_DENSE_FWD = 1,    /* input projection + residual blocks           */
+    RUNE_PHASE_MESSAGE_FWD = 2,  /* MP / EQ message blocks                       */
+    RUNE_PHASE_READOUT = 3,      /* element heads (or NEP MLP, fwd + bwd)        */
+    RUNE_PHASE_MESSAGE_BWD = 4,
+    RUNE_PHASE_DENSE_BWD = 5,
+    RUNE_PHASE_REVERSE = 6,      /* K3 descriptor reverse + ZBL                  */
+    RUNE_PHASE_FORCES = 7,       /* K7 forces, virials, structure sums           */
+    RUNE_N_PHASES = 8
+};
+int rune_model_timing(rune_model *model, int32_t enable);
+int rune_model_timing_read(rune_model *model, double *ms_per_phase, int64_t *calls);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,78 @@
+"""``nn.Module`` shell shared by the Möbius and NEP drop-in models.
+
+The shell holds parameters and buffers under the reference's state_dict
+names (so ``load_state_dict(strict=True)`` accepts the reference
+checkpoints), and its ``forward(batch)`` evaluates through the HIP library:
+the padded reference batch (``rune/mobius/interface/batch.py:124-166``) is
+converted to records on the device and ``rune_model_compute`` returns
+energies, forces and virials.  There is no PyTorch/CPU evaluation path.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import _native as N
+
+
+class HipPotential(nn.Module):
+    family = N.FAMILY_MOBIUS
+
+    def __init__(self):
+        super().__init__()
+        self._native = None
+        self._native_key = None
+        self._nlist = None
+
+    # the handle is rebuilt whenever a parameter or buffer changed in place
+    def _state_key(self):
+        return tuple((t.data_ptr(), t._version) for t in self.state_dict().values())
+
+    def native(self):
+        key = self._state_key()
+        if self._native is None or key != self._native_key:
+            dtypes = {t.dtype for t in self.state_dict().values() if t.is_floating_point()}
+            if dtypes - {torch.float32}:
+                raise TypeError("the HIP evaluator computes in float32; convert the model "
+                                f"with .float() (found {sorted(map(str, dtypes))})")
+            self._native = N.NativeModel(self.params, self.state_dict(), self.family)
+            self._native_key = key
+        return self._native
+
+    def neighbor_list(self):
+        if self._nlist is None:
+            self._nlist = N.NeighborList()
+        return self._nlist
+
+    def _direct_edge_list(self):
+        return "angular" if self.family == N.FAMILY_NEP else "radial"
+
+    def forward(self, batch):
+        """``Mobius.forward`` / ``NEP.forward`` contract on a padded batch."""
+        compute_forces = bool(batch.get("compute_forces", True))
+        compute_virial = bool(batch.get("compute_virial", True))
+        positions = batch["positions"]
+        N.require_device(positions.device)
+        counts = batch["n_atoms_per_structure"].detach().to("cpu", torch.long)
+        struct_ptr = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)]).numpy()
+        nl = self.neighbor_list().from_padded(
+            positions.detach().to(torch.float32), batch["radial_neighbors"],
+            batch["radial_offsets"], batch["angular_neighbors"], batch["angular_offsets"],
+            struct_ptr)
+        out = self.native().compute(nl, batch["types"], len(struct_ptr) - 1, compute_forces,
+                                    compute_virial)
+        result = {"energies": out["energies"], "energy": out["energy"]}
+        if compute_forces:
+            result["forces"] = out["forces"]
+        if compute_virial:
+            result["virial"] = out["virial"]
+        return result
+
+
+class ParamHolder(nn.Module):
+    """Bare module that only carries named parameters / buffers."""
+
+
+def linear(n_in, n_out, bias=True):
+    return nn.Linear(n_in, n_out, bias=bias)

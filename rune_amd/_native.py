@@ -79,6 +79,8 @@ def library():
         "rune_model_finalize": (C.c_int, [vp]),
         "rune_model_compute": (C.c_int, [vp, vp, vp, i32, i32, vp, vp, vp, vp, vp, vp]),
         "rune_model_workspace_bytes": (i64, [vp]),
+        "rune_model_timing": (C.c_int, [vp, i32]),
+        "rune_model_timing_read": (C.c_int, [vp, C.POINTER(C.c_double), C.POINTER(i64)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -299,6 +301,19 @@ class NativeModel:
 
     def workspace_bytes(self):
         return int(library().rune_model_workspace_bytes(self._h))
+
+    PHASES = ("descriptor", "dense_fwd", "message_fwd", "readout", "message_bwd", "dense_bwd",
+              "reverse", "forces")
+
+    def timing(self, enable=True):
+        check(library().rune_model_timing(self._h, int(enable)))
+
+    def timing_read(self):
+        """Summed milliseconds per phase over the recorded calls, and the call count."""
+        ms = (C.c_double * len(self.PHASES))()
+        calls = C.c_int64()
+        check(library().rune_model_timing_read(self._h, ms, C.byref(calls)))
+        return dict(zip(self.PHASES, list(ms))), calls.value
 
 
 def version():

@@ -343,7 +343,6 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     }
     const int N = int(nl->n_atoms);
     const int64_t E = nl->n_records;
-    const int B = nl->n_structures;
     const bool grad = want_f || want_w;
     Records r = records_of(nl);
     const DescTables &d = m.desc;
@@ -359,7 +358,6 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     size_t o_g = ar.add(16 * size_t(std::max<int64_t>(E, 1)));
     size_t o_av = ar.add(4 * size_t(N) * 9);
     size_t o_f = ar.add(4 * size_t(N) * 3);
-    size_t o_sum = ar.add(4 * size_t(B) * 10);
     LocalPlan lp = plan_local(m, ar, N);
     MessagePlan mp = plan_messages(m, ar, N, E);
     m.work.reserve(ar.total);
@@ -372,7 +370,6 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     float4 *g = reinterpret_cast<float4 *>(base + o_g);
     float *atom_virial = d_atom_virial ? d_atom_virial : reinterpret_cast<float *>(base + o_av);
     float *forces = d_forces ? d_forces : reinterpret_cast<float *>(base + o_f);
-    float *sums = reinterpret_cast<float *>(base + o_sum);
     lp.bind(base);
     mp.bind(base);
     // ---- type validation (one small readback) ----
@@ -385,32 +382,65 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     RUNE_HIP_CHECK(hipStreamSynchronize(s));
     RUNE_REQUIRE(hflag == 0, RUNE_ERR_TYPE, "atom type outside [0, n_types)");
     if (N == 0) return;
+    hipEvent_t *ev = nullptr;
+    if (m.timing) {
+        if (m.events.empty()) {
+            m.events.resize(size_t(kTimingRing) * (RUNE_N_PHASES + 1));
+            for (auto &e : m.events) RUNE_HIP_CHECK(hipEventCreate(&e));
+        }
+        ev = m.events.data() + size_t(m.timed_calls % kTimingRing) * (RUNE_N_PHASES + 1);
+        ++m.timed_calls;
+    }
+    auto mark = [&](int k) {
+        if (ev) RUNE_HIP_CHECK(hipEventRecord(ev[k], s));
+    };
     // ---- forward ----
+    mark(0);
     descriptor_forward(d, r, types, q, ldq, mom, s);
+    mark(1);
     const float4 *g_direct = nullptr;
     const float *dmom = nullptr;
     if (m.cfg.family == RUNE_FAMILY_NEP) {
+        mark(2);
+        mark(3);
         nep_mlp(N, m.Q, m.cfg.nep_hidden, q, ldq, types, m.nep_w0, m.nep_b0, m.nep_w1,
                 m.nep_bias, energies, dq, grad ? 1 : 0, s);
+        mark(4);
+        mark(5);
+        mark(6);
     } else {
         float *h = local_forward(m, lp, N, q, ldq, types, s);
+        mark(2);
         h = messages_forward(m, mp, lp, r, types, mom, h, s, grad);
+        mark(3);
         float *dh = grad ? lp.dh_a : nullptr;
         readout(N, m.cfg.hidden_dim, h, m.cfg.hidden_dim, types, m.head_w, m.head_b,
                 float(m.cfg.norm_eps), energies, dh, m.cfg.hidden_dim, s);
+        mark(4);
         if (grad) {
             dh = messages_backward(m, mp, lp, r, types, mom, dh, s);
+            mark(5);
             local_backward(m, lp, N, dh, dq, ldq, s);
             g_direct = mp.g_direct_used ? mp.g_direct : nullptr;
             dmom = mp.dmom_used ? mp.dmom : nullptr;
+        } else {
+            mark(5);
         }
+        mark(6);
     }
     descriptor_reverse(d, m.zbl, r, types, dq, ldq, mom, dmom, g_direct, energies, g,
                        grad ? 1 : 0, s);
+    mark(7);
     if (d_energy) structure_sum(r, energies, 1, d_energy, s);
-    if (!grad) return;
-    forces_and_virial(r, g, forces, atom_virial, s);
-    if (want_w && d_virial) structure_sum(r, atom_virial, 9, d_virial, s);
+    if (grad) {
+        forces_and_virial(r, g, forces, atom_virial, s);
+        if (want_w && d_virial) structure_sum(r, atom_virial, 9, d_virial, s);
+    }
+    mark(8);
+}
+
+ModelImpl::~ModelImpl() {
+    for (auto &e : events) (void)hipEventDestroy(e);
 }
 
 // ---- local (descriptor network) part ----
@@ -611,4 +641,30 @@ extern "C" int rune_model_compute(rune_model *model, const rune_nlist *nl, const
 
 extern "C" int64_t rune_model_workspace_bytes(const rune_model *model) {
     return model ? int64_t(model->work.bytes) : 0;
+}
+
+extern "C" int rune_model_timing(rune_model *model, int32_t enable) {
+    return guarded([&] {
+        RUNE_REQUIRE(model, RUNE_ERR_ARGUMENT, "null model");
+        model->timing = enable != 0;
+        model->timed_calls = 0;
+    });
+}
+
+extern "C" int rune_model_timing_read(rune_model *model, double *ms, int64_t *calls) {
+    return guarded([&] {
+        RUNE_REQUIRE(model && ms, RUNE_ERR_ARGUMENT, "null argument");
+        for (int k = 0; k < RUNE_N_PHASES; ++k) ms[k] = 0.0;
+        int64_t n = std::min<int64_t>(model->timed_calls, kTimingRing);
+        for (int64_t c = 0; c < n; ++c) {
+            hipEvent_t *ev = model->events.data() + size_t(c) * (RUNE_N_PHASES + 1);
+            RUNE_HIP_CHECK(hipEventSynchronize(ev[RUNE_N_PHASES]));
+            for (int k = 0; k < RUNE_N_PHASES; ++k) {
+                float t = 0.0f;
+                RUNE_HIP_CHECK(hipEventElapsedTime(&t, ev[k], ev[k + 1]));
+                ms[k] += t;
+            }
+        }
+        if (calls) *calls = n;
+    });
 }

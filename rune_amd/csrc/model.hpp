@@ -94,8 +94,15 @@ struct ModelImpl {
     // NEP
     const float *nep_w0 = nullptr, *nep_b0 = nullptr, *nep_w1 = nullptr;
     float nep_bias = 0.0f;
+    // phase timing ring (events recorded on the launch stream)
+    bool timing = false;
+    std::vector<hipEvent_t> events;       // kTimingRing x (RUNE_N_PHASES + 1)
+    int64_t timed_calls = 0;
     const std::vector<float> &tensor(const std::string &name) const;
+    ~ModelImpl();
 };
+
+constexpr int kTimingRing = 256;
 
 using PackedLookup = std::function<const float *(const std::string &)>;
 

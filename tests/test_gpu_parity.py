@@ -121,3 +121,90 @@ def test_local_model_is_deterministic():
     b = ev.evaluate(s)
     for k in ("energies", "energy", "forces", "virial"):
         assert torch.equal(a[k], b[k]), k
+
+
+def _nep_oracle(model, s, dtype):
+    p = model.params
+    w = {k: (v.detach().to(dtype) if v.is_floating_point() else v) for k, v in
+         model.state_dict().items()}
+    types = (s.numbers == 52).astype(np.int64) if "Te" in p["elements"] else None
+    nl = ONB.build(s.positions, s.cell, s.pbc, p["rcut_radial"], p["rcut_angular"])
+    sp = ONB.split(nl)
+    mk = lambda k: OM.Edges(torch.as_tensor(sp[k][0]), torch.as_tensor(sp[k][1]),
+                            torch.as_tensor(sp[k][2], dtype=dtype))
+    return OM.nep_forward(w, p, torch.as_tensor(s.positions, dtype=dtype),
+                          torch.as_tensor(types), [len(s)], mk("radial"), mk("angular"))
+
+
+@pytest.mark.parametrize("reps", [2, 3])
+def test_nep_matches_oracle(reps):
+    from rune_amd import _native as N
+    from rune_amd.api import Evaluator
+    from rune_amd.nep.model import seeded_nep
+    model = seeded_nep(seed=0)
+    ev = Evaluator(model.params, model.state_dict(), N.FAMILY_NEP)
+    s = W.rocksalt(seed=30 + reps, reps=reps)
+    out = ev.evaluate(s)
+    r64 = _nep_oracle(model, s, torch.float64)
+    r32 = _nep_oracle(model, s, torch.float32)
+    gpu = _compare(out, r64, len(s))
+    ref = _compare(r32, r64, len(s))
+    print(f"NEP {len(s)}: HIP {gpu}, reference fp32 {ref}")
+    for g, r, t in zip(gpu, ref, TOL):
+        assert g <= max(t, 2.0 * r)
+
+
+def test_drop_in_model_forward_on_padded_batch():
+    """``Mobius.forward(batch)`` with the reference's padded batch format."""
+    from rune_amd.mobius.plugin import load_model
+    from rune_amd import MODELS
+    model = load_model(MODELS["mobius-oam-loc"], device="cuda").eval()
+    s = W.si_diamond(seed=31, reps=2)
+    p = model.params
+    nl = ONB.build(s.positions, s.cell, s.pbc, p["rcut_radial"], p["rcut_angular"])
+    sp = ONB.split(nl)
+    rn, ro = ONB.pack(*sp["radial"], len(s), 64)
+    an, ao = ONB.pack(*sp["angular"], len(s), 64)
+    dev = torch.device("cuda")
+    batch = {"positions": torch.as_tensor(s.positions, dtype=torch.float32, device=dev),
+             "types": torch.full((len(s),), 13, dtype=torch.long, device=dev),
+             "radial_neighbors": torch.as_tensor(rn, device=dev),
+             "radial_offsets": torch.as_tensor(ro, dtype=torch.float32, device=dev),
+             "angular_neighbors": torch.as_tensor(an, device=dev),
+             "angular_offsets": torch.as_tensor(ao, dtype=torch.float32, device=dev),
+             "n_atoms_per_structure": torch.tensor([len(s)], device=dev)}
+    out = model(batch)
+    check_against_oracle("loc", out, s, np.full(len(s), 13))
+    f_only = model({**batch, "compute_virial": False})
+    assert "virial" not in f_only and "forces" in f_only
+    e_only = model({**batch, "compute_forces": False, "compute_virial": False})
+    torch.testing.assert_close(e_only["energies"], out["energies"], rtol=0, atol=0)
+
+
+def test_batched_structures_match_single_calls():
+    ev, p = _evaluator("loc")
+    cells = [W.si_diamond(seed=40 + k, reps=1 + (k % 2)) for k in range(4)]
+    batched = ev.evaluate(cells)
+    off = 0
+    for k, s in enumerate(cells):
+        single = ev.evaluate(s)
+        n = len(s)
+        torch.testing.assert_close(batched["energies"][off:off + n], single["energies"],
+                                   rtol=0, atol=2e-6)
+        torch.testing.assert_close(batched["forces"][off:off + n], single["forces"],
+                                   rtol=0, atol=2e-5)
+        torch.testing.assert_close(batched["virial"][k], single["virial"][0], rtol=1e-5,
+                                   atol=1e-4)
+        off += n
+
+
+def test_errors_are_reported():
+    from rune_amd import _native as N
+    ev, p = _evaluator("loc")
+    s = W.si_diamond(seed=1, reps=2)
+    with pytest.raises(ValueError, match="not supported"):
+        ev.types_of([13, 2000])
+    nl = N.NeighborList()
+    with pytest.raises(ValueError, match="exceeds max_neighbors=10"):
+        nl.build(torch.as_tensor(s.positions, device="cuda"), [0, len(s)], [s.cell], [s.pbc],
+                 6.0, 5.0, 10, 100)
