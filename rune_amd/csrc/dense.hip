@@ -92,6 +92,9 @@ __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *
                 if (ep.bias) x += ep.bias[col];
                 if (ep.emb) x += ep.emb[size_t(ep.types[row]) * ep.ld_emb + col];
                 if (ep.residual) x += ep.residual[size_t(row) * ep.ldr + col];
+#pragma unroll
+                for (int k = 0; k < 3; ++k)
+                    if (ep.gtab[k]) x += ep.gtab[k][size_t(ep.gidx[k][row]) * ep.gld[k] + col];
                 if (ep.pre) ep.pre[size_t(row) * ep.ldp + col] = x;
                 if (ep.act >= 0) x = act_f(ep.act, x);
                 if (ep.dact_from) x *= act_d(ep.dact, ep.dact_from[size_t(row) * ep.ldu + col]);

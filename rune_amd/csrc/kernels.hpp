@@ -54,6 +54,7 @@ struct Records {
     const float4 *vec;            // [E] {x, y, z, |r|}
     const int32_t *tptr;          // [N+1]
     const int32_t *tidx;          // [E]
+    const int32_t *ctr;           // [E] centre of each record
     const int32_t *sptr;          // [B+1]
     int n_structures;
 };
@@ -77,6 +78,10 @@ struct Epilogue {
     int ld_emb = 0;
     const float *residual = nullptr;    // [M, ldr]
     int ldr = 0;
+    // v += gtab[k][gidx[k][m] * gld[k] + n]   (gathered row adds, k < 3)
+    const float *gtab[3] = {nullptr, nullptr, nullptr};
+    const int32_t *gidx[3] = {nullptr, nullptr, nullptr};
+    int gld[3] = {0, 0, 0};
     float *pre = nullptr;               // store pre-activation [M, ldp]
     int ldp = 0;
     int act = -1;                       // RUNE_ACT_* applied to the output, -1 none

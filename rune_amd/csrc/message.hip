@@ -1,45 +1,745 @@
-// Message blocks: MP (rune/mobius/message.py) and EQ (rune/mobius/equivariant.py).
-#include "model.hpp"
+// Message blocks.  MP: rune/mobius/message.py:100-193 (grouped scalar messages
+// plus the transient l=1 vector branch).  EQ lives in equivariant.hip.
+//
+// Layout: per-edge tensors are indexed by neighbour record e (see nlist.hpp);
+// a record takes part in message passing when it belongs to the radial list
+// of its centre, and its cosine cutoff fc(d) (message_cutoff) then weights
+// every message term.  Dense maps over atoms or edges are MFMA GEMMs
+// (dense.hip); gathers and segment sums are wave-per-atom kernels that walk a
+// centre's records (or, for neighbour-destined adjoints, the transpose list)
+// in a fixed order, so nothing uses floating-point atomics.
+#include <cmath>
+
+#include "message.hpp"
 
 namespace rune {
+namespace {
+
+constexpr int kWave = 64;
+constexpr float kPi = 3.14159265358979323846f;
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ inline float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// ---- shared edge preparation ----
+
+__global__ void k_edge_prep(EdgePrepArgs a) {
+    int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= a.E) return;
+    int i = a.r.ctr[e];
+    bool in_r = e >= a.r.view[4 * i] && e < a.r.view[4 * i + 1];
+    float4 v = a.r.vec[e];
+    float d = v.w;
+    float rc = a.cutoff;
+    float fc = 0.0f;
+    float *rb = a.rb + size_t(e) * a.ldrb;
+    for (int k = 0; k < a.ldrb; ++k) rb[k] = 0.0f;
+    if (in_r && d < rc) {
+        fc = 0.5f * cosf(kPi * d / rc) + 0.5f;
+        float x = 2.0f * (d / rc - 1.0f) * (d / rc - 1.0f) - 1.0f;
+        float half = 0.5f * fc;
+        float t2 = 1.0f, t1 = x;
+        rb[0] = 2.0f * half;
+        if (a.kb > 1) rb[1] = (x + 1.0f) * half;
+        for (int k = 2; k < a.kb; ++k) {
+            float t = 2.0f * x * t1 - t2;
+            t2 = t1;
+            t1 = t;
+            rb[k] = (t + 1.0f) * half;
+        }
+    }
+    a.fc[e] = fc;
+    a.pair[e] = a.types[i] * a.n_types + a.types[a.r.nbr[e]];
+    a.dv[e] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (a.harm) {
+        // normalised real harmonics Y = b(r_hat) * scale (descriptor.py:643-648)
+        float *y = a.harm + size_t(e) * a.nq;
+        if (!in_r) {
+            for (int c = 0; c < a.nq; ++c) y[c] = 0.0f;
+        } else {
+            float inv = 1.0f / fmaxf(d, 1.0e-12f);
+            harmonics(a.z, a.z_off, a.lq, v.x * inv, v.y * inv, v.z * inv, a.scale, y);
+        }
+    }
+}
+
+// d/dr of the masked Chebyshev basis, accumulated into dv.w:  sum_k drb_k f_k'(d)
+__global__ void k_edge_rb_backward(int64_t E, Records r, const float *fc, const float *drb,
+                                   int ld, int kb, float cutoff, float4 *dv) {
+    int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= E || fc[e] == 0.0f) return;
+    float d = r.vec[e].w;
+    float rc = cutoff;
+    float f = 0.5f * cosf(kPi * d / rc) + 0.5f;
+    float fp = -0.5f * kPi / rc * sinf(kPi * d / rc);
+    float rs = d / rc - 1.0f;
+    float x = 2.0f * rs * rs - 1.0f;
+    float dxdr = 4.0f * rs / rc;
+    const float *g = drb + size_t(e) * ld;
+    // k = 0: f0 = fc
+    float acc = g[0] * fp;
+    float t2 = 1.0f, t1 = x, u2 = 1.0f, u1 = 2.0f * x;
+    if (kb > 1) acc += g[1] * (0.5f * dxdr * f + 0.5f * (x + 1.0f) * fp);
+    for (int k = 2; k < kb; ++k) {
+        float tn = 2.0f * x * t1 - t2;
+        float un = 2.0f * x * u1 - u2;
+        acc += g[k] * (0.5f * float(k) * u1 * dxdr * f + 0.5f * (tn + 1.0f) * fp);
+        t2 = t1;
+        t1 = tn;
+        u2 = u1;
+        u1 = un;
+    }
+    dv[e].w += acc;
+}
+
+// g_direct = dE/dd * u + (I - u u^T) dE/du / d
+__global__ void k_edge_direct(int64_t E, Records r, const float4 *dv, float4 *g) {
+    int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    float4 v = r.vec[e];
+    float4 a = dv[e];
+    float inv = 1.0f / fmaxf(v.w, 1.0e-12f);
+    float ux = v.x * inv, uy = v.y * inv, uz = v.z * inv;
+    float proj = a.x * ux + a.y * uy + a.z * uz;
+    g[e] = make_float4(a.w * ux + (a.x - proj * ux) * inv, a.w * uy + (a.y - proj * uy) * inv,
+                       a.w * uz + (a.z - proj * uz) * inv, 0.0f);
+}
+
+// ---- MP kernels (one 64-lane wave per atom) ----
+
+struct MpArgs {
+    Records r;
+    int H, G, vc, NG, NP;
+    float eps;
+    const float *fc;       // [E]
+    const float *gv;       // [E, NG] gate logits
+    const float *vs;       // [N, NP] values | vector source
+    const float *vmix;     // [vc, vc]
+    float *msg;            // [N, H]
+    float *rm;             // [N]
+    float *vsum;           // [N, vc*3]
+    float *mixed;          // [N, vc*3]
+    float *uin;            // [N, H+vc]
+    // reverse
+    const float *duin;     // [N, H+vc]
+    float *dmsg;           // [N, H]
+    float *dvsum;          // [N, vc*3]
+    float *dgv;            // [E, NG]
+    float4 *dv;            // [E]
+    float *dvs;            // [N, NP]
+    float cutoff;          // message_cutoff
+};
+
+__global__ void __launch_bounds__(kWave) k_mp_aggregate(MpArgs a) {
+    __shared__ float vsL[3 * 64];
+    const int i = blockIdx.x, lane = threadIdx.x;
+    const int H = a.H, G = a.G, vc = a.vc, NG = a.NG, NP = a.NP, gw = H / G;
+    float acc[4] = {0, 0, 0, 0};      // channels lane + 64*k, H <= 256
+    float vsl = 0.0f;                 // lane = 3*k + x < 3*vc
+    const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
+    for (int e = rb; e < re; ++e) {
+        float fc = a.fc[e];
+        if (fc == 0.0f) continue;
+        int j = a.r.nbr[e];
+        const float *gl = a.gv + size_t(e) * NG;
+        const float *vj = a.vs + size_t(j) * NP;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            int c = lane + kWave * k;
+            if (c < H) acc[k] += sigm(gl[c / gw]) * fc * vj[c];
+        }
+        if (lane < 3 * vc) {
+            int k = lane / 3, x = lane - 3 * k;
+            float4 v = a.r.vec[e];
+            float inv = 1.0f / fmaxf(v.w, 1.0e-12f);
+            float u = (x == 0 ? v.x : (x == 1 ? v.y : v.z)) * inv;
+            vsl += sigm(gl[G + k]) * fc * vj[H + k] * u;
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        int c = lane + kWave * k;
+        if (c < H) {
+            a.msg[size_t(i) * H + c] = acc[k];
+            ss += acc[k] * acc[k];
+        }
+    }
+    ss = wave_sum(ss);
+    float r = 1.0f / sqrtf(ss / float(H) + a.eps);
+    if (lane == 0) a.rm[i] = r;
+    const int ldu = H + vc;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        int c = lane + kWave * k;
+        if (c < H) a.uin[size_t(i) * ldu + c] = acc[k] * r;
+    }
+    if (vc == 0) return;
+    if (lane < 3 * vc) {
+        vsL[lane] = vsl;
+        a.vsum[size_t(i) * 3 * vc + lane] = vsl;
+    }
+    __syncthreads();
+    float mx = 0.0f;
+    if (lane < 3 * vc) {
+        int k = lane / 3, x = lane - 3 * k;
+        for (int kk = 0; kk < vc; ++kk) mx += a.vmix[k * vc + kk] * vsL[3 * kk + x];
+        a.mixed[size_t(i) * 3 * vc + lane] = mx;
+    }
+    __syncthreads();
+    if (lane < 3 * vc) vsL[lane] = mx;
+    __syncthreads();
+    if (lane < vc) {
+        float t = vsL[3 * lane] * vsL[3 * lane] + vsL[3 * lane + 1] * vsL[3 * lane + 1] +
+                  vsL[3 * lane + 2] * vsL[3 * lane + 2];
+        a.uin[size_t(i) * ldu + H + lane] = t;
+    }
+}
+
+__global__ void __launch_bounds__(kWave) k_mp_node_backward(MpArgs a) {
+    __shared__ float dmx[3 * 64];
+    const int i = blockIdx.x, lane = threadIdx.x;
+    const int H = a.H, vc = a.vc, ldu = H + vc;
+    const float *d = a.duin + size_t(i) * ldu;
+    const float *m = a.msg + size_t(i) * H;
+    float dot = 0.0f;
+    for (int c = lane; c < H; c += kWave) dot += d[c] * m[c];
+    dot = wave_sum(dot);
+    float r = a.rm[i];
+    float coef = r * r * r * dot / float(H);
+    for (int c = lane; c < H; c += kWave) a.dmsg[size_t(i) * H + c] = r * d[c] - coef * m[c];
+    if (vc == 0) return;
+    if (lane < 3 * vc) {
+        int k = lane / 3;
+        dmx[lane] = 2.0f * a.mixed[size_t(i) * 3 * vc + lane] * d[H + k];
+    }
+    __syncthreads();
+    if (lane < 3 * vc) {
+        int kk = lane / 3, x = lane - 3 * kk;
+        float s = 0.0f;
+        for (int k = 0; k < vc; ++k) s += a.vmix[k * vc + kk] * dmx[3 * k + x];
+        a.dvsum[size_t(i) * 3 * vc + lane] = s;
+    }
+}
+
+// Adjoint of the gates, fc and the unit vector for the records of centre i.
+__global__ void __launch_bounds__(kWave) k_mp_edge_backward(MpArgs a) {
+    extern __shared__ float lds[];
+    float *pL = lds;                 // [H]
+    float *dvsL = pL + a.H;          // [3*vc]
+    const int i = blockIdx.x, lane = threadIdx.x;
+    const int H = a.H, G = a.G, vc = a.vc, NG = a.NG, NP = a.NP, gw = H / G;
+    float dm[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        int c = lane + kWave * k;
+        dm[k] = c < H ? a.dmsg[size_t(i) * H + c] : 0.0f;
+    }
+    if (lane < 3 * vc) dvsL[lane] = a.dvsum[size_t(i) * 3 * vc + lane];
+    __syncthreads();
+    const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
+    for (int e = rb; e < re; ++e) {
+        float fc = a.fc[e];
+        float *dg = a.dgv + size_t(e) * NG;
+        if (fc == 0.0f) {
+            for (int c = lane; c < NG; c += kWave) dg[c] = 0.0f;
+            continue;
+        }
+        int j = a.r.nbr[e];
+        const float *gl = a.gv + size_t(e) * NG;
+        const float *vj = a.vs + size_t(j) * NP;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            int c = lane + kWave * k;
+            if (c < H) pL[c] = dm[k] * vj[c];
+        }
+        __syncthreads();
+        float4 v = a.r.vec[e];
+        float d = v.w;
+        float inv = 1.0f / fmaxf(d, 1.0e-12f);
+        float u[3] = {v.x * inv, v.y * inv, v.z * inv};
+        float contrib = 0.0f, dux = 0.0f, duy = 0.0f, duz = 0.0f;
+        if (lane < G) {
+            float P = 0.0f;
+            for (int c = lane * gw; c < (lane + 1) * gw; ++c) P += pL[c];
+            float s = sigm(gl[lane]);
+            dg[lane] = P * fc * s * (1.0f - s);
+            contrib = P * s;
+        } else if (lane < G + vc) {
+            int k = lane - G;
+            float ak = dvsL[3 * k] * u[0] + dvsL[3 * k + 1] * u[1] + dvsL[3 * k + 2] * u[2];
+            float src = vj[H + k];
+            float vg = sigm(gl[G + k]);
+            dg[G + k] = ak * src * fc * vg * (1.0f - vg);
+            contrib = ak * src * vg;
+            float w = vg * fc * src;
+            dux = w * dvsL[3 * k];
+            duy = w * dvsL[3 * k + 1];
+            duz = w * dvsL[3 * k + 2];
+        }
+        contrib = wave_sum(contrib);
+        dux = wave_sum(dux);
+        duy = wave_sum(duy);
+        duz = wave_sum(duz);
+        if (lane == 0) {
+            float fcp = -0.5f * kPi / a.cutoff * sinf(kPi * d / a.cutoff);
+            float4 acc = a.dv[e];
+            acc.x += dux;
+            acc.y += duy;
+            acc.z += duz;
+            acc.w += contrib * fcp;
+            a.dv[e] = acc;
+        }
+        __syncthreads();
+    }
+}
+
+// Adjoint of the gathered neighbour rows (values | vector source) of atom j.
+__global__ void __launch_bounds__(kWave) k_mp_neighbor_backward(MpArgs a) {
+    const int j = blockIdx.x, lane = threadIdx.x;
+    const int H = a.H, G = a.G, vc = a.vc, NG = a.NG, NP = a.NP, gw = H / G;
+    float acc[4] = {0, 0, 0, 0};
+    float av = 0.0f;
+    for (int t = a.r.tptr[j]; t < a.r.tptr[j + 1]; ++t) {
+        int e = a.r.tidx[t];
+        float fc = a.fc[e];
+        if (fc == 0.0f) continue;
+        int i = a.r.ctr[e];
+        const float *gl = a.gv + size_t(e) * NG;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            int c = lane + kWave * k;
+            if (c < H) acc[k] += sigm(gl[c / gw]) * fc * a.dmsg[size_t(i) * H + c];
+        }
+        if (lane < vc) {
+            float4 v = a.r.vec[e];
+            float inv = 1.0f / fmaxf(v.w, 1.0e-12f);
+            const float *dvs = a.dvsum + size_t(i) * 3 * vc + 3 * lane;
+            float ak = (dvs[0] * v.x + dvs[1] * v.y + dvs[2] * v.z) * inv;
+            av += sigm(gl[G + lane]) * fc * ak;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        int c = lane + kWave * k;
+        if (c < H) a.dvs[size_t(j) * NP + c] = acc[k];
+    }
+    if (lane < vc) a.dvs[size_t(j) * NP + H + lane] = av;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
 
 void MessagePlan::bind(char *base) {
     ptrs.clear();
     for (size_t o : offs) ptrs.push_back(reinterpret_cast<float *>(base + o));
-    if (E > 0 || N > 0) {
+    if (o_gd || o_dmom) {
         g_direct = reinterpret_cast<float4 *>(base + o_gd);
         dmom = reinterpret_cast<float *>(base + o_dmom);
     }
 }
 
 void validate_messages(ModelImpl &m) {
-    if (m.cfg.family != RUNE_FAMILY_MOBIUS || m.cfg.message_layers == 0) return;
-    throw Error(RUNE_ERR_ARGUMENT, "message blocks are not available in this build yet");
+    const rune_model_config &c = m.cfg;
+    if (c.family != RUNE_FAMILY_MOBIUS || c.message_layers == 0) return;
+    RUNE_REQUIRE(c.hidden_dim <= 256, RUNE_ERR_ARGUMENT,
+                 "message blocks support hidden_dim <= 256");
+    RUNE_REQUIRE(c.message_groups >= 1 && c.hidden_dim % c.message_groups == 0,
+                 RUNE_ERR_ARGUMENT, "hidden_dim must be divisible by message_groups.");
+    RUNE_REQUIRE(c.message_basis_size >= 1 && c.message_basis_size <= 64, RUNE_ERR_ARGUMENT,
+                 "message_basis_size outside [1, 64]");
+    RUNE_REQUIRE(c.message_cutoff > 0 && c.message_cutoff <= c.rc_radial, RUNE_ERR_ARGUMENT,
+                 "message_cutoff must be positive and cannot exceed rcut_radial.");
+    if (c.message_mode == RUNE_MESSAGE_SCALAR) {
+        RUNE_REQUIRE(c.vector_channels <= 21, RUNE_ERR_ARGUMENT,
+                     "vector_channels outside [0, 21]");
+        RUNE_REQUIRE(c.message_groups + c.vector_channels <= kWave, RUNE_ERR_ARGUMENT,
+                     "message_groups + vector_channels must not exceed 64");
+    } else {
+        validate_equivariant(m);
+    }
 }
 
-void define_expected_messages(ModelImpl &) {}
+static void expect(ModelImpl &m, const std::string &name, int64_t n) { m.expected[name] = n; }
 
-void pack_messages(ModelImpl &, Packer &, std::map<std::string, size_t> &) {}
+void define_expected_messages(ModelImpl &m) {
+    const rune_model_config &c = m.cfg;
+    const int64_t T = c.n_types, H = c.hidden_dim, D = c.message_dim, P = c.pair_dim;
+    const int64_t G = c.message_groups, vc = c.vector_channels, kb = c.message_basis_size;
+    if (c.message_mode == RUNE_MESSAGE_EQUIVARIANT) {
+        define_expected_equivariant(m);
+        return;
+    }
+    for (int b = 0; b < c.message_layers; ++b) {
+        std::string p = "message_blocks." + std::to_string(b) + ".";
+        expect(m, p + "input_norm.weight", H);
+        expect(m, p + "pair_embedding.weight", T * T * P);
+        expect(m, p + "edge_mlp.0.weight", D * (kb + P));
+        expect(m, p + "edge_mlp.0.bias", D);
+        expect(m, p + "group_gate.weight", G * D);
+        expect(m, p + "group_gate.bias", G);
+        expect(m, p + "value_projection.weight", H * H);
+        if (vc) {
+            expect(m, p + "vector_gate.weight", vc * D);
+            expect(m, p + "vector_gate.bias", vc);
+            expect(m, p + "vector_source.weight", vc * H);
+            expect(m, p + "vector_mix.weight", vc * vc);
+        }
+        expect(m, p + "message_norm.weight", H);
+        expect(m, p + "update.0.weight", D * (H + vc));
+        expect(m, p + "update.0.bias", D);
+        expect(m, p + "update.2.weight", H * D);
+        expect(m, p + "update.2.bias", H);
+    }
+}
 
-void bind_messages(ModelImpl &, const PackedLookup &) {}
+// rows [r0, r1) of W [rows, cols] scaled column-wise by s (s may be null)
+std::vector<float> fold_cols(const std::vector<float> &w, int rows, int cols, const float *s) {
+    std::vector<float> out(w.begin(), w.begin() + size_t(rows) * cols);
+    if (s)
+        for (int r = 0; r < rows; ++r)
+            for (int c = 0; c < cols; ++c) out[size_t(r) * cols + c] *= s[c];
+    return out;
+}
 
-MessagePlan plan_messages(ModelImpl &, Arena &, int N, int64_t E) {
+std::vector<float> columns(const std::vector<float> &w, int rows, int cols, int c0, int c1) {
+    std::vector<float> out(size_t(rows) * (c1 - c0));
+    for (int r = 0; r < rows; ++r)
+        for (int c = c0; c < c1; ++c) out[size_t(r) * (c1 - c0) + c - c0] = w[size_t(r) * cols + c];
+    return out;
+}
+
+// pair_embedding [T*T, P] x W[:, c0:c0+P]^T + b  -> [T*T, D]
+std::vector<float> pair_projection(const std::vector<float> &emb, const std::vector<float> &w,
+                                   const std::vector<float> &b, int TT, int P, int D, int K,
+                                   int c0) {
+    std::vector<float> out(size_t(TT) * D);
+    for (int t = 0; t < TT; ++t)
+        for (int o = 0; o < D; ++o) {
+            double acc = 0.0;
+            for (int p = 0; p < P; ++p)
+                acc += double(emb[size_t(t) * P + p]) * double(w[size_t(o) * K + c0 + p]);
+            out[size_t(t) * D + o] = float(acc + double(b[o]));
+        }
+    return out;
+}
+
+void pack_messages(ModelImpl &m, Packer &pk, std::map<std::string, size_t> &off) {
+    const rune_model_config &c = m.cfg;
+    if (c.message_layers == 0) return;
+    if (c.message_mode == RUNE_MESSAGE_EQUIVARIANT) {
+        pack_equivariant(m, pk, off);
+        return;
+    }
+    const int T = c.n_types, H = c.hidden_dim, D = c.message_dim, P = c.pair_dim;
+    const int G = c.message_groups, vc = c.vector_channels, kb = c.message_basis_size;
+    const int NP = H + vc, NG = G + vc, K = kb + P;
+    for (int b = 0; b < c.message_layers; ++b) {
+        std::string p = "message_blocks." + std::to_string(b) + ".";
+        const auto &win = m.tensor(p + "input_norm.weight");
+        std::vector<float> node = m.tensor(p + "value_projection.weight");   // [H, H]
+        if (vc) {
+            const auto &src = m.tensor(p + "vector_source.weight");           // [vc, H]
+            node.insert(node.end(), src.begin(), src.end());
+        }
+        node = fold_cols(node, NP, H, win.data());
+        off[p + "node_f"] = pk.put(node);
+        off[p + "node_fT"] = pk.put(transpose(node, NP, H));
+        const auto &we = m.tensor(p + "edge_mlp.0.weight");                   // [D, K]
+        std::vector<float> wx = columns(we, D, K, 0, kb);
+        off[p + "edge_x"] = pk.put(wx);
+        off[p + "edge_xT"] = pk.put(transpose(wx, D, kb));
+        off[p + "pair_proj"] = pk.put(pair_projection(m.tensor(p + "pair_embedding.weight"), we,
+                                                      m.tensor(p + "edge_mlp.0.bias"), T * T, P,
+                                                      D, K, kb));
+        std::vector<float> gate = m.tensor(p + "group_gate.weight");         // [G, D]
+        std::vector<float> gb = m.tensor(p + "group_gate.bias");
+        if (vc) {
+            const auto &vg = m.tensor(p + "vector_gate.weight");
+            gate.insert(gate.end(), vg.begin(), vg.end());
+            const auto &vb = m.tensor(p + "vector_gate.bias");
+            gb.insert(gb.end(), vb.begin(), vb.end());
+            off[p + "vmix"] = pk.put(m.tensor(p + "vector_mix.weight"));
+        }
+        off[p + "gate"] = pk.put(gate);
+        off[p + "gate_T"] = pk.put(transpose(gate, NG, D));
+        off[p + "gate_b"] = pk.put(gb);
+        std::vector<float> wmsg = m.tensor(p + "message_norm.weight");
+        wmsg.resize(NP, 1.0f);                                                 // invariants unscaled
+        std::vector<float> up1 = fold_cols(m.tensor(p + "update.0.weight"), D, NP, wmsg.data());
+        off[p + "up1_f"] = pk.put(up1);
+        off[p + "up1_fT"] = pk.put(transpose(up1, D, NP));
+        off[p + "up1_b"] = pk.put(m.tensor(p + "update.0.bias"));
+        const auto &up2 = m.tensor(p + "update.2.weight");                    // [H, D]
+        off[p + "up2"] = pk.put(up2);
+        off[p + "up2_T"] = pk.put(transpose(up2, H, D));
+        off[p + "up2_b"] = pk.put(m.tensor(p + "update.2.bias"));
+    }
+}
+
+void bind_messages(ModelImpl &m, const PackedLookup &P) {
+    const rune_model_config &c = m.cfg;
+    if (c.message_layers == 0) return;
+    if (c.message_mode == RUNE_MESSAGE_EQUIVARIANT) {
+        bind_equivariant(m, P);
+        return;
+    }
+    m.msg.resize(c.message_layers);
+    for (int b = 0; b < c.message_layers; ++b) {
+        std::string p = "message_blocks." + std::to_string(b) + ".";
+        MessageWeights &w = m.msg[b];
+        w.NP = c.hidden_dim + c.vector_channels;
+        w.NG = c.message_groups + c.vector_channels;
+        w.KX = c.message_basis_size;
+        w.node_f = P(p + "node_f");
+        w.node_fT = P(p + "node_fT");
+        w.edge_x = P(p + "edge_x");
+        w.edge_xT = P(p + "edge_xT");
+        w.pair_proj = P(p + "pair_proj");
+        w.gate = P(p + "gate");
+        w.gate_T = P(p + "gate_T");
+        w.gate_b = P(p + "gate_b");
+        w.vmix = c.vector_channels ? P(p + "vmix") : nullptr;
+        w.up1_f = P(p + "up1_f");
+        w.up1_fT = P(p + "up1_fT");
+        w.up1_b = P(p + "up1_b");
+        w.up2 = P(p + "up2");
+        w.up2_T = P(p + "up2_T");
+        w.up2_b = P(p + "up2_b");
+    }
+}
+
+int MessagePlan::add(Arena &ar, size_t bytes) {
+    offs.push_back(ar.add(bytes));
+    return int(offs.size()) - 1;
+}
+
+MessagePlan plan_messages(ModelImpl &m, Arena &ar, int N, int64_t E) {
     MessagePlan p;
-    p.N = 0;
-    p.E = 0;
-    (void)N;
-    (void)E;
+    const rune_model_config &c = m.cfg;
+    if (c.family != RUNE_FAMILY_MOBIUS || c.message_layers == 0) return p;
+    if (c.message_mode == RUNE_MESSAGE_EQUIVARIANT) return plan_equivariant(m, ar, N, E);
+    const size_t n = size_t(N), e = size_t(std::max<int64_t>(E, 1));
+    const int H = c.hidden_dim, D = c.message_dim, vc = c.vector_channels;
+    const int NP = H + vc, NG = c.message_groups + vc, L = c.message_layers;
+    p.N = N;
+    p.E = E;
+    p.ldrb = (c.message_basis_size + 3) & ~3;
+    p.o_gd = ar.add(16 * e);
+    p.o_dmom = 0;
+    p.i_rb = p.add(ar, 4 * e * p.ldrb);
+    p.i_fc = p.add(ar, 4 * e);
+    p.i_pair = p.add(ar, 4 * e);
+    p.i_dv = p.add(ar, 16 * e);
+    for (int b = 0; b < L; ++b) {
+        BlockBuffers bb;
+        bb.h_out = p.add(ar, 4 * n * H);
+        bb.rin = p.add(ar, 4 * n);
+        bb.vs = p.add(ar, 4 * n * NP);
+        bb.ue = p.add(ar, 4 * e * D);
+        bb.eh = p.add(ar, 4 * e * D);
+        bb.gv = p.add(ar, 4 * e * NG);
+        bb.msg = p.add(ar, 4 * n * H);
+        bb.rm = p.add(ar, 4 * n);
+        bb.vsum = p.add(ar, 4 * n * 3 * std::max(vc, 1));
+        bb.mixed = p.add(ar, 4 * n * 3 * std::max(vc, 1));
+        bb.uin = p.add(ar, 4 * n * NP);
+        bb.u1 = p.add(ar, 4 * n * D);
+        bb.z1 = p.add(ar, 4 * n * D);
+        p.blocks.push_back(bb);
+    }
+    p.t_dz1 = p.add(ar, 4 * n * D);
+    p.t_duin = p.add(ar, 4 * n * NP);
+    p.t_dmsg = p.add(ar, 4 * n * H);
+    p.t_dvsum = p.add(ar, 4 * n * 3 * std::max(vc, 1));
+    p.t_dgv = p.add(ar, 4 * e * NG);
+    p.t_due = p.add(ar, 4 * e * D);
+    p.t_drb = p.add(ar, 4 * e * p.ldrb);
+    p.t_dvs = p.add(ar, 4 * n * NP);
+    p.t_dz = p.add(ar, 4 * n * H);
+    p.t_dh0 = p.add(ar, 4 * n * H);
+    p.t_dh1 = p.add(ar, 4 * n * H);
     return p;
 }
 
-float *messages_forward(ModelImpl &, MessagePlan &, LocalPlan &, const Records &,
-                        const int32_t *, const float *, float *h, hipStream_t, bool) {
-    return h;
+static int edge_grid(int64_t E) { return ceil_div(std::max<int64_t>(E, 1), 256); }
+
+void edge_prep(ModelImpl &m, MessagePlan &p, const Records &r, const int32_t *types,
+               hipStream_t s, float *harm, const float *scale, int lq, int nq) {
+    if (p.E == 0) return;
+    EdgePrepArgs a{};
+    a.r = r;
+    a.E = p.E;
+    a.types = types;
+    a.n_types = m.cfg.n_types;
+    a.cutoff = float(m.cfg.message_cutoff);
+    a.kb = m.cfg.message_basis_size;
+    a.ldrb = p.ldrb;
+    a.rb = p.at(p.i_rb);
+    a.fc = p.at(p.i_fc);
+    a.pair = reinterpret_cast<int32_t *>(p.at(p.i_pair));
+    a.dv = reinterpret_cast<float4 *>(p.at(p.i_dv));
+    a.harm = harm;
+    a.scale = scale;
+    a.lq = lq;
+    a.nq = nq;
+    a.z = m.desc.z;
+    for (int k = 0; k < kMaxL + 2; ++k) a.z_off[k] = m.desc.z_off[k];
+    hipLaunchKernelGGL(k_edge_prep, dim3(edge_grid(p.E)), dim3(256), 0, s, a);
+    RUNE_HIP_CHECK(hipGetLastError());
 }
 
-float *messages_backward(ModelImpl &, MessagePlan &, LocalPlan &, const Records &,
-                         const int32_t *, const float *, float *dh, hipStream_t) {
-    return dh;
+void edge_rb_backward(ModelImpl &m, MessagePlan &p, const Records &r, const float *drb,
+                      hipStream_t s) {
+    if (p.E == 0) return;
+    hipLaunchKernelGGL(k_edge_rb_backward, dim3(edge_grid(p.E)), dim3(256), 0, s, p.E, r,
+                       p.at(p.i_fc), drb, p.ldrb, m.cfg.message_basis_size,
+                       float(m.cfg.message_cutoff), reinterpret_cast<float4 *>(p.at(p.i_dv)));
+    RUNE_HIP_CHECK(hipGetLastError());
+}
+
+void edge_direct(MessagePlan &p, const Records &r, hipStream_t s) {
+    if (p.E == 0) return;
+    hipLaunchKernelGGL(k_edge_direct, dim3(edge_grid(p.E)), dim3(256), 0, s, p.E, r,
+                       reinterpret_cast<const float4 *>(p.at(p.i_dv)), p.g_direct);
+    RUNE_HIP_CHECK(hipGetLastError());
+}
+
+static MpArgs mp_args(ModelImpl &m, MessagePlan &p, const Records &r, int b) {
+    const rune_model_config &c = m.cfg;
+    const BlockBuffers &bb = p.blocks[b];
+    MpArgs a{};
+    a.r = r;
+    a.H = c.hidden_dim;
+    a.G = c.message_groups;
+    a.vc = c.vector_channels;
+    a.NG = a.G + a.vc;
+    a.NP = a.H + a.vc;
+    a.eps = float(c.norm_eps);
+    a.fc = p.at(p.i_fc);
+    a.gv = p.at(bb.gv);
+    a.vs = p.at(bb.vs);
+    a.vmix = m.msg[b].vmix;
+    a.msg = p.at(bb.msg);
+    a.rm = p.at(bb.rm);
+    a.vsum = p.at(bb.vsum);
+    a.mixed = p.at(bb.mixed);
+    a.uin = p.at(bb.uin);
+    a.duin = p.at(p.t_duin);
+    a.dmsg = p.at(p.t_dmsg);
+    a.dvsum = p.at(p.t_dvsum);
+    a.dgv = p.at(p.t_dgv);
+    a.dv = reinterpret_cast<float4 *>(p.at(p.i_dv));
+    a.dvs = p.at(p.t_dvs);
+    a.cutoff = float(c.message_cutoff);
+    return a;
+}
+
+float *messages_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Records &r,
+                        const int32_t *types, const float *moments, float *h, hipStream_t s,
+                        bool keep) {
+    const rune_model_config &c = m.cfg;
+    if (c.family != RUNE_FAMILY_MOBIUS || c.message_layers == 0) return h;
+    if (c.message_mode == RUNE_MESSAGE_EQUIVARIANT)
+        return equivariant_forward(m, p, lp, r, types, moments, h, s, keep);
+    const int N = p.N, H = c.hidden_dim, D = c.message_dim, act = c.activation;
+    const int64_t E = p.E;
+    (void)keep;
+    edge_prep(m, p, r, types, s, nullptr, nullptr, 0, 0);
+    float *cur = h;
+    for (int b = 0; b < c.message_layers; ++b) {
+        const MessageWeights &w = m.msg[b];
+        const BlockBuffers &bb = p.blocks[b];
+        row_inv_rms(N, H, cur, H, float(c.norm_eps), p.at(bb.rin), s);
+        Epilogue e0;
+        e0.row_scale = p.at(bb.rin);
+        gemm(N, w.NP, H, cur, H, w.node_fT, w.NP, p.at(bb.vs), w.NP, e0, s);
+        if (E > 0) {
+            Epilogue e1;
+            e1.gtab[0] = w.pair_proj;
+            e1.gidx[0] = reinterpret_cast<const int32_t *>(p.at(p.i_pair));
+            e1.gld[0] = D;
+            e1.pre = p.at(bb.ue);
+            e1.ldp = D;
+            e1.act = act;
+            gemm(int(E), D, w.KX, p.at(p.i_rb), p.ldrb, w.edge_xT, D, p.at(bb.eh), D, e1, s);
+            Epilogue e2;
+            e2.bias = w.gate_b;
+            gemm(int(E), w.NG, D, p.at(bb.eh), D, w.gate_T, w.NG, p.at(bb.gv), w.NG, e2, s);
+        }
+        MpArgs a = mp_args(m, p, r, b);
+        hipLaunchKernelGGL(k_mp_aggregate, dim3(N), dim3(kWave), 0, s, a);
+        RUNE_HIP_CHECK(hipGetLastError());
+        Epilogue e3;
+        e3.bias = w.up1_b;
+        e3.pre = p.at(bb.u1);
+        e3.ldp = D;
+        e3.act = act;
+        gemm(N, D, w.NP, p.at(bb.uin), w.NP, w.up1_fT, D, p.at(bb.z1), D, e3, s);
+        Epilogue e4;
+        e4.bias = w.up2_b;
+        e4.residual = cur;
+        e4.ldr = H;
+        gemm(N, H, D, p.at(bb.z1), D, w.up2_T, H, p.at(bb.h_out), H, e4, s);
+        p.block_input.push_back(cur);
+        cur = p.at(bb.h_out);
+    }
+    return cur;
+}
+
+float *messages_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Records &r,
+                         const int32_t *types, const float *moments, float *dh, hipStream_t s) {
+    const rune_model_config &c = m.cfg;
+    if (c.family != RUNE_FAMILY_MOBIUS || c.message_layers == 0) return dh;
+    if (c.message_mode == RUNE_MESSAGE_EQUIVARIANT)
+        return equivariant_backward(m, p, lp, r, types, moments, dh, s);
+    const int N = p.N, H = c.hidden_dim, D = c.message_dim, act = c.activation;
+    const int64_t E = p.E;
+    float *cur = dh;
+    for (int b = c.message_layers - 1; b >= 0; --b) {
+        const MessageWeights &w = m.msg[b];
+        const BlockBuffers &bb = p.blocks[b];
+        const float *hin = p.block_input[b];
+        Epilogue e0;
+        e0.dact_from = p.at(bb.u1);
+        e0.ldu = D;
+        e0.dact = act;
+        gemm(N, D, H, cur, H, w.up2, D, p.at(p.t_dz1), D, e0, s);
+        Epilogue e1;
+        gemm(N, w.NP, D, p.at(p.t_dz1), D, w.up1_f, w.NP, p.at(p.t_duin), w.NP, e1, s);
+        MpArgs a = mp_args(m, p, r, b);
+        hipLaunchKernelGGL(k_mp_node_backward, dim3(N), dim3(kWave), 0, s, a);
+        size_t lds = sizeof(float) * (H + 3 * std::max(c.vector_channels, 1));
+        hipLaunchKernelGGL(k_mp_edge_backward, dim3(N), dim3(kWave), lds, s, a);
+        hipLaunchKernelGGL(k_mp_neighbor_backward, dim3(N), dim3(kWave), 0, s, a);
+        RUNE_HIP_CHECK(hipGetLastError());
+        if (E > 0) {
+            Epilogue e2;
+            e2.dact_from = p.at(bb.ue);
+            e2.ldu = D;
+            e2.dact = act;
+            gemm(int(E), D, w.NG, p.at(p.t_dgv), w.NG, w.gate, D, p.at(p.t_due), D, e2, s);
+            Epilogue e3;
+            gemm(int(E), w.KX, D, p.at(p.t_due), D, w.edge_x, w.KX, p.at(p.t_drb), p.ldrb, e3, s);
+            edge_rb_backward(m, p, r, p.at(p.t_drb), s);
+        }
+        Epilogue e4;
+        gemm(N, H, w.NP, p.at(p.t_dvs), w.NP, w.node_f, H, p.at(p.t_dz), H, e4, s);
+        float *next = (cur == p.at(p.t_dh0)) ? p.at(p.t_dh1) : p.at(p.t_dh0);
+        rms_backward(N, H, hin, H, p.at(bb.rin), p.at(p.t_dz), H, cur, H, next, H, s);
+        cur = next;
+    }
+    edge_direct(p, r, s);
+    p.g_direct_used = E > 0;
+    return cur;
 }
 
 }  // namespace rune

@@ -26,30 +26,25 @@ struct ResidualWeights {
 };
 
 // Weights of one message block (MP: message.py, EQ: equivariant.py), packed.
+// "f" = RMSNorm weight folded into the columns; "T" = transposed copy used as
+// the B operand of the forward GEMM (the untransposed copy serves the reverse).
 struct MessageWeights {
-    const float *in_norm;       // [H]
-    const float *pair_emb;      // [T*T, P]
-    const float *edge_w;        // edge MLP weight rows [D, K_edge]  (radial|pair part)
-    const float *edge_wT;       // [K_edge, D]
-    const float *edge_b;        // [D]
-    const float *gate_w;        // group gate [G, D]
-    const float *gate_b;        // [G]
-    const float *value_wT;      // [H, H] value projection^T  (W_v^T)
-    const float *value_w;       // [H, H]
-    // MP vector branch
-    const float *vgate_w, *vgate_b;   // [vc, D], [vc]
-    const float *vsrc_wT, *vsrc_w;    // [H, vc], [vc, H]
-    const float *vmix;                // [vc, vc]
-    // EQ
-    const float *ctx_wT, *ctx_w;      // [H, 2D] (centre | neighbour contexts), [2D, H]
-    const float *dir_w, *dir_b;       // direction gates [2*lq*C, D], [2*lq*C]
-    const float *mix;                 // [lq, C, C]
-    const float *edge_w_ctx;          // edge MLP columns acting on probes [D, 2*lq*C]
-    // update MLP
-    const float *msg_norm;            // [H]
-    const float *up1_w, *up1_wT, *up1_b;   // [D, H+X], [H+X, D], [D]
-    const float *up2_w, *up2_wT, *up2_b;   // [H, D], [D, H], [H]
-    const float *pair_proj;           // EQ: pair_emb @ W_pair^T + b  [T*T, D]
+    // node projections of RMSNorm(h):  MP [values | vector source],
+    // EQ [W_e,c C_c | W_e,n C_n | values]
+    const float *node_fT, *node_f;    // [H, NP], [NP, H]
+    int NP;
+    // edge MLP on per-edge features: MP [radial basis], EQ [radial basis | probes]
+    const float *edge_xT, *edge_x;    // [KX, D], [D, KX]
+    int KX;
+    const float *pair_proj;           // [T*T, D] = pair_embedding W_pair^T + b
+    // gates from the edge hidden state: MP [groups | vector], EQ [groups | directions]
+    const float *gate_T, *gate, *gate_b;   // [D, NG], [NG, D], [NG]
+    int NG;
+    const float *vmix;                // MP [vc, vc]
+    const float *mix;                 // EQ [lq, C, C]
+    // update MLP on [RMSNorm(message) | invariants]
+    const float *up1_fT, *up1_f, *up1_b;   // [H+X, D], [D, H+X], [D]
+    const float *up2_T, *up2, *up2_b;      // [D, H], [H, D], [H]
 };
 
 struct LocalPlan {
@@ -58,6 +53,14 @@ struct LocalPlan {
     float *h = nullptr, *r = nullptr, *u = nullptr, *a = nullptr;
     float *dh_a = nullptr, *dh_b = nullptr, *dz = nullptr;
     void bind(char *base);
+};
+
+// Workspace indices of one message block (entries of MessagePlan::offs).
+struct BlockBuffers {
+    int h_out = -1, rin = -1, vs = -1, ue = -1, eh = -1, gv = -1, msg = -1, rm = -1;
+    int vsum = -1, mixed = -1, uin = -1, u1 = -1, z1 = -1;
+    int dir_in = -1, dir_out = -1, mixstate = -1;   // EQ angular states
+    int xe = -1;                                     // EQ per-edge features
 };
 
 struct MessagePlan {
@@ -69,6 +72,15 @@ struct MessagePlan {
     int N = 0;
     int64_t E = 0;
     size_t o_gd = 0, o_dmom = 0;
+    int ldrb = 0;
+    int i_rb = -1, i_fc = -1, i_pair = -1, i_dv = -1, i_harm = -1, i_dharm = -1;
+    std::vector<BlockBuffers> blocks;
+    // reverse-pass temporaries shared by the blocks
+    int t_dz1 = -1, t_duin = -1, t_dmsg = -1, t_dvsum = -1, t_dgv = -1, t_due = -1;
+    int t_drb = -1, t_dvs = -1, t_dz = -1, t_dh0 = -1, t_dh1 = -1;
+    int t_ddir0 = -1, t_ddir1 = -1, t_dmix = -1, t_dx = -1, t_dab = -1;
+    std::vector<const float *> block_input;
+    int add(Arena &ar, size_t bytes);
     void bind(char *base);
     float *at(int k) const { return ptrs[k]; }
 };

@@ -192,7 +192,7 @@ __global__ void enumerate_edges(int n, const double *pos, const int32_t *sptr, i
 __global__ void decode_records(int n, const double *pos, const int32_t *sptr, int nstruct,
                                const Geo *geo, const int32_t *ptr, const int32_t *cnt_r,
                                const int32_t *cnt_a, const uint64_t *keys, int32_t *view,
-                               int32_t *nbr, int32_t *shift, float4 *vec) {
+                               int32_t *nbr, int32_t *shift, float4 *vec, int32_t *ctr) {
     int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     int s = find_structure(sptr, nstruct, i);
@@ -216,6 +216,7 @@ __global__ void decode_records(int n, const double *pos, const int32_t *sptr, in
             v[d] = (pj + float(o)) - pi[d];
         }
         nbr[r] = j;
+        ctr[r] = i;
         shift[3 * r + 0] = S[0];
         shift[3 * r + 1] = S[1];
         shift[3 * r + 2] = S[2];
@@ -241,7 +242,7 @@ __global__ void count_padded(int n, const int64_t *rn, int kr, const int64_t *an
 __global__ void fill_padded(int n, const float *pos, const int64_t *rn, const float *ro, int kr,
                             const int64_t *an, const float *ao, int ka, const int32_t *ptr,
                             const int32_t *cnt_r, const int32_t *cnt_a, int32_t *view,
-                            int32_t *nbr, int32_t *shift, float4 *vec) {
+                            int32_t *nbr, int32_t *shift, float4 *vec, int32_t *ctr) {
     int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     int b = ptr[i];
@@ -261,6 +262,7 @@ __global__ void fill_padded(int n, const float *pos, const int64_t *rn, const fl
             float v[3];
             for (int d = 0; d < 3; ++d) v[d] = (pos[3 * j + d] + o[d]) - pos[3 * i + d];
             nbr[r] = int(j);
+            ctr[r] = i;
             shift[3 * r] = shift[3 * r + 1] = shift[3 * r + 2] = 0;
             vec[r] = make_float4(v[0], v[1], v[2], sqrtf(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]));
             ++r;
@@ -580,6 +582,7 @@ extern "C" int rune_nlist_build(rune_nlist *nl, int64_t n_atoms, const double *d
         nl->nbr.reserve(4 * ecap);
         nl->shift.reserve(12 * ecap);
         nl->vec.reserve(16 * ecap);
+        nl->ctr.reserve(4 * ecap);
         if (n > 0) {
             hipLaunchKernelGGL((enumerate_edges<true>), dim3(gb), dim3(kThreads), 0, s, n,
                                d_positions, sptr, n_structures, w.geo, w.atom_wrap, w.atom_cell,
@@ -591,7 +594,7 @@ extern "C" int rune_nlist_build(rune_nlist *nl, int64_t n_atoms, const double *d
                                sptr, n_structures, w.geo, nl->ptr.as<int32_t>(), w.cnt_r,
                                w.cnt_a, nl->keys.as<uint64_t>(), nl->view.as<int32_t>(),
                                nl->nbr.as<int32_t>(), nl->shift.as<int32_t>(),
-                               nl->vec.as<float4>());
+                               nl->vec.as<float4>(), nl->ctr.as<int32_t>());
         }
         RUNE_HIP_CHECK(hipGetLastError());
         build_transpose(nl, w.indeg, w.scan_tmp, s);
@@ -653,12 +656,14 @@ extern "C" int rune_nlist_from_padded(rune_nlist *nl, int64_t n_atoms, const flo
         nl->nbr.reserve(4 * ecap);
         nl->shift.reserve(12 * ecap);
         nl->vec.reserve(16 * ecap);
+        nl->ctr.reserve(4 * ecap);
         if (n > 0)
             hipLaunchKernelGGL(fill_padded, dim3(gb), dim3(kThreads), 0, s, n, d_positions,
                                d_radial_nbr, d_radial_off, k_radial, d_angular_nbr,
                                d_angular_off, k_angular, nl->ptr.as<int32_t>(), cr, ca,
                                nl->view.as<int32_t>(), nl->nbr.as<int32_t>(),
-                               nl->shift.as<int32_t>(), nl->vec.as<float4>());
+                               nl->shift.as<int32_t>(), nl->vec.as<float4>(),
+                               nl->ctr.as<int32_t>());
         RUNE_HIP_CHECK(hipGetLastError());
         build_transpose(nl, indeg, scan_tmp, s);
         if (n_records) *n_records = e;

@@ -17,6 +17,7 @@ struct rune_nlist {
     rune::DeviceBuffer nbr;      // int32 [E]
     rune::DeviceBuffer shift;    // int32 [E,3]
     rune::DeviceBuffer vec;      // float4 [E]
+    rune::DeviceBuffer ctr;      // int32 [E] centre atom of each record
     // transpose: records whose neighbour is atom a, ascending record id
     rune::DeviceBuffer tptr;     // int32 [N+1]
     rune::DeviceBuffer tidx;     // int32 [E]

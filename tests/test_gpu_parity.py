@@ -208,3 +208,60 @@ def test_errors_are_reported():
     with pytest.raises(ValueError, match="exceeds max_neighbors=10"):
         nl.build(torch.as_tensor(s.positions, device="cuda"), [0, len(s)], [s.cell], [s.pbc],
                  6.0, 5.0, 10, 100)
+
+
+@pytest.mark.parametrize("name", ["fec4", "fcc108", "amo200"])
+def test_mp_model_matches_oracle(name):
+    ev, p = _evaluator("mp")
+    s = _structures()[name]
+    out = ev.evaluate(s)
+    check_against_oracle("mp", out, s, ev.types_of(s.numbers))
+
+
+def _small_model(seed, **changes):
+    from rune_amd.mobius.model import Mobius
+    from rune_amd.mobius.plugin import resolve_params
+    values = {"elements": ["Fe", "C", "O"], "hidden_dim": 16, "blocks": 1, "ffn_dim": 24,
+              "message_layers": 2, "message_dim": 12, "message_groups": 4, "pair_dim": 3,
+              "vector_channels": 3, "message_basis_size": 5, "rcut_radial": 4.8,
+              "rcut_angular": 4.4, "n_max_radial": 2, "n_max_angular": 2,
+              "basis_size_radial": 3, "basis_size_angular": 3, "l_max": 4, "l_max_4body": 2,
+              "l_max_5body": 1, "has_q_112": 1, "has_q_123": 1, "has_q_233": 1, "has_q_134": 1,
+              "max_neighbors_radial": 200, "max_neighbors_angular": 200}
+    values.update(changes)
+    torch.manual_seed(seed)
+    model = Mobius(resolve_params(values))
+    with torch.no_grad():     # non-trivial norm weights and scaler
+        for name, t in model.named_parameters():
+            if name.endswith("norm.weight"):
+                t.uniform_(0.5, 1.5)
+        model.q_scaler.uniform_(0.5, 1.5)
+    return model
+
+
+@pytest.mark.parametrize("changes", [
+    {}, {"vector_channels": 0}, {"activation": "tanh"}, {"activation": "gelu"},
+    {"message_cutoff": 3.9, "message_basis_size": 4},
+    {"rcut_angular": 5.2, "zbl": [0.8, 1.6]},
+])
+def test_small_mp_variants_match_oracle(changes):
+    from rune_amd import _native as N
+    from rune_amd.api import Evaluator
+    model = _small_model(5, **changes)
+    p = model.params
+    rng = np.random.default_rng(3)
+    cell = np.diag([6.1, 6.4, 6.7]) + rng.uniform(-0.4, 0.4, (3, 3))
+    s = W.Structure(rng.random((14, 3)) @ cell, rng.choice([26, 6, 8], 14), cell)
+    ev = Evaluator(p, model.state_dict(), N.FAMILY_MOBIUS)
+    out = ev.evaluate(s)
+    types = ev.types_of(s.numbers)
+    sd = model.state_dict()
+    w64 = {k: v.double() if v.is_floating_point() else v for k, v in sd.items()}
+    r64 = _oracle(p, w64, s, types, torch.float64)
+    w32 = {k: v.float() if v.is_floating_point() else v for k, v in sd.items()}
+    r32 = _oracle(p, w32, s, types, torch.float32)
+    gpu = _compare(out, r64, len(s))
+    ref = _compare(r32, r64, len(s))
+    print(changes, gpu, ref)
+    for g, r, t in zip(gpu, ref, TOL):
+        assert g <= max(t, 2.0 * r)
