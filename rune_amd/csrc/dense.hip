@@ -15,6 +15,7 @@ __device__ inline float act_f(int a, float x) {
     if (a == RUNE_ACT_SILU) return x / (1.0f + expf(-x));
     if (a == RUNE_ACT_TANH) return tanhf(x);
     if (a == RUNE_ACT_GELU) return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+    if (a == kActSigmoid) return 1.0f / (1.0f + expf(-x));
     return x;
 }
 
@@ -43,7 +44,7 @@ __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *
     __shared__ float Bs[kBK][kBN + 4];
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
-    const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+    const int m0 = blockIdx.x * kBM, n0 = blockIdx.y * kBN;
     const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
     floatx4 acc[2][2];
 #pragma unroll
@@ -96,7 +97,10 @@ __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *
                 for (int k = 0; k < 3; ++k)
                     if (ep.gtab[k]) x += ep.gtab[k][size_t(ep.gidx[k][row]) * ep.gld[k] + col];
                 if (ep.pre) ep.pre[size_t(row) * ep.ldp + col] = x;
-                if (ep.act >= 0) x = act_f(ep.act, x);
+                if (ep.act_split >= 0 && col >= ep.act_split)
+                    x = act_f(ep.act2, x);
+                else if (ep.act >= 0)
+                    x = act_f(ep.act, x);
                 if (ep.dact_from) x *= act_d(ep.dact, ep.dact_from[size_t(row) * ep.ldu + col]);
                 C[size_t(row) * ldc + col] = x;
             }
@@ -198,7 +202,7 @@ __global__ void k_nep_mlp(int M, int Q, int Hn, const float *q, int ldq, const i
 void gemm(int M, int N, int K, const float *A, int lda, const float *B, int ldb, float *C,
           int ldc, const Epilogue &ep, hipStream_t s) {
     if (M == 0 || N == 0) return;
-    dim3 grid(ceil_div(N, kBN), ceil_div(M, kBM));
+    dim3 grid(ceil_div(M, kBM), ceil_div(N, kBN));
     hipLaunchKernelGGL(k_gemm, grid, dim3(256), 0, s, M, N, K, A, lda, B, ldb, C, ldc, ep);
     RUNE_HIP_CHECK(hipGetLastError());
 }

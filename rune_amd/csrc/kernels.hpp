@@ -5,6 +5,8 @@
 
 namespace rune {
 
+constexpr int kActSigmoid = 3;   // internal activation code next to RUNE_ACT_*
+
 constexpr int kMaxNr = 16;    // radial descriptor channels  (n_max_radial + 1)
 constexpr int kMaxKr = 24;    // radial basis size           (basis_size_radial + 1)
 constexpr int kMaxNa = 16;    // angular descriptor channels
@@ -85,6 +87,8 @@ struct Epilogue {
     float *pre = nullptr;               // store pre-activation [M, ldp]
     int ldp = 0;
     int act = -1;                       // RUNE_ACT_* applied to the output, -1 none
+    int act_split = -1;                 // columns >= act_split use act2 instead of act
+    int act2 = -1;
     const float *dact_from = nullptr;   // v *= act'(U[m, n]) with U [M, ldu]
     int ldu = 0;
     int dact = -1;                      // activation whose derivative is used

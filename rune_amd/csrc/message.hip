@@ -597,11 +597,11 @@ void edge_prep(ModelImpl &m, MessagePlan &p, const Records &r, const int32_t *ty
     RUNE_HIP_CHECK(hipGetLastError());
 }
 
-void edge_rb_backward(ModelImpl &m, MessagePlan &p, const Records &r, const float *drb,
+void edge_rb_backward(ModelImpl &m, MessagePlan &p, const Records &r, const float *drb, int ld,
                       hipStream_t s) {
     if (p.E == 0) return;
     hipLaunchKernelGGL(k_edge_rb_backward, dim3(edge_grid(p.E)), dim3(256), 0, s, p.E, r,
-                       p.at(p.i_fc), drb, p.ldrb, m.cfg.message_basis_size,
+                       p.at(p.i_fc), drb, ld, m.cfg.message_basis_size,
                        float(m.cfg.message_cutoff), reinterpret_cast<float4 *>(p.at(p.i_dv)));
     RUNE_HIP_CHECK(hipGetLastError());
 }
@@ -729,7 +729,7 @@ float *messages_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Reco
             gemm(int(E), D, w.NG, p.at(p.t_dgv), w.NG, w.gate, D, p.at(p.t_due), D, e2, s);
             Epilogue e3;
             gemm(int(E), w.KX, D, p.at(p.t_due), D, w.edge_x, w.KX, p.at(p.t_drb), p.ldrb, e3, s);
-            edge_rb_backward(m, p, r, p.at(p.t_drb), s);
+            edge_rb_backward(m, p, r, p.at(p.t_drb), p.ldrb, s);
         }
         Epilogue e4;
         gemm(N, H, w.NP, p.at(p.t_dvs), w.NP, w.node_f, H, p.at(p.t_dz), H, e4, s);

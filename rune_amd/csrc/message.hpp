@@ -63,8 +63,12 @@ std::vector<float> pair_projection(const std::vector<float> &emb, const std::vec
                                    int c0);
 void edge_prep(ModelImpl &m, MessagePlan &p, const Records &r, const int32_t *types,
                hipStream_t s, float *harm, const float *scale, int lq, int nq);
-void edge_rb_backward(ModelImpl &m, MessagePlan &p, const Records &r, const float *drb,
+void edge_rb_backward(ModelImpl &m, MessagePlan &p, const Records &r, const float *drb, int ld,
                       hipStream_t s);
+
+struct EdgeZ {
+    int off[kMaxL + 2];
+};
 void edge_direct(MessagePlan &p, const Records &r, hipStream_t s);
 
 // EQ (equivariant.hip)

@@ -265,3 +265,44 @@ def test_small_mp_variants_match_oracle(changes):
     print(changes, gpu, ref)
     for g, r, t in zip(gpu, ref, TOL):
         assert g <= max(t, 2.0 * r)
+
+
+@pytest.mark.parametrize("name", ["fec4", "fcc108", "amo200"])
+def test_eq_model_matches_oracle(name):
+    ev, p = _evaluator("eq")
+    s = _structures()[name]
+    out = ev.evaluate(s)
+    check_against_oracle("eq", out, s, ev.types_of(s.numbers))
+
+
+def _check_small(model):
+    from rune_amd import _native as N
+    from rune_amd.api import Evaluator
+    p = model.params
+    rng = np.random.default_rng(4)
+    cell = np.diag([6.1, 6.4, 6.7]) + rng.uniform(-0.4, 0.4, (3, 3))
+    s = W.Structure(rng.random((14, 3)) @ cell, rng.choice([26, 6, 8], 14), cell)
+    ev = Evaluator(p, model.state_dict(), N.FAMILY_MOBIUS)
+    out = ev.evaluate(s)
+    types = ev.types_of(s.numbers)
+    sd = model.state_dict()
+    w64 = {k: v.double() if v.is_floating_point() else v for k, v in sd.items()}
+    w32 = {k: v.float() if v.is_floating_point() else v for k, v in sd.items()}
+    r64 = _oracle(p, w64, s, types, torch.float64)
+    r32 = _oracle(p, w32, s, types, torch.float32)
+    gpu = _compare(out, r64, len(s))
+    ref = _compare(r32, r64, len(s))
+    print(gpu, ref)
+    for g, r, t in zip(gpu, ref, TOL):
+        assert g <= max(t, 2.0 * r)
+
+
+@pytest.mark.parametrize("changes", [
+    {}, {"equivariant_l_max": 1}, {"equivariant_l_max": 2}, {"activation": "gelu"},
+    {"message_cutoff": 3.9}, {"rcut_angular": 5.2, "zbl": [0.8, 1.6]},
+    {"equivariant_channels": 5, "message_groups": 2},
+])
+def test_small_eq_variants_match_oracle(changes):
+    base = {"message_mode": "equivariant", "equivariant_channels": 3}
+    base.update(changes)
+    _check_small(_small_model(6, **base))
