@@ -40,7 +40,7 @@ WORKLOADS = {
     "C4": "Mobius-EQ (oam-eq), 100000-atom amorphous cell, 0.08 /A^3, dmin 1.8, 10 elements",
     "C5": "Mobius-EQ (oam-eq), 256 small triclinic cells of 8-64 atoms",
 }
-DEFAULT_WORKLOAD = "C2"
+DEFAULT_WORKLOAD = "C4"
 
 
 def build_workload(name, device):

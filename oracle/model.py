@@ -483,6 +483,15 @@ class Edges:
     offsets: torch.Tensor
 
 
+def _vjp(outputs, inputs, cotangents):
+    """VJP of the descriptor; ``(None, None)`` when there are no edges (no graph)."""
+    pairs = [(o, c) for o, c in zip(outputs, cotangents) if o.requires_grad]
+    if not pairs:
+        return None, None
+    return torch.autograd.grad([o for o, _ in pairs], inputs, [c for _, c in pairs],
+                               allow_unused=True)
+
+
 def _structure_ids(counts):
     counts = torch.as_tensor(counts, dtype=torch.long)
     return torch.repeat_interleave(torch.arange(counts.numel()), counts)
@@ -581,7 +590,7 @@ def forward(w, p, positions, types, counts, radial, angular, *, compute_forces=T
         if ds is not None:
             outs.append(s)
             cots.append(ds)
-        gr, ga = torch.autograd.grad(outs, (vr, va), cots, allow_unused=True)
+        gr, ga = _vjp(outs, (vr, va), cots)
     gr = torch.zeros_like(vr) if gr is None else gr
     ga = torch.zeros_like(va) if ga is None else ga
     forces = positions.new_zeros((n, 3))
@@ -602,7 +611,7 @@ def contract(w, p, positions, types, radial, angular, dq, dmom=None):
         if dmom is not None:
             outs.append(s)
             cots.append(dmom)
-        gr, ga = torch.autograd.grad(outs, (vr, va), cots, allow_unused=True)
+        gr, ga = _vjp(outs, (vr, va), cots)
     gr = torch.zeros_like(vr) if gr is None else gr
     ga = torch.zeros_like(va) if ga is None else ga
     forces = positions.new_zeros((n, 3))
@@ -694,7 +703,7 @@ def nep_forward(w, p, positions, types, counts, radial, angular, *, compute_forc
         dq, dv = torch.autograd.grad(energies.sum(), (qd, ve), allow_unused=True)
         dq = torch.zeros_like(qd) if dq is None else dq
         dv = torch.zeros_like(ve) if dv is None else dv
-        gr, ga = torch.autograd.grad([q], (vr, va), [dq], allow_unused=True)
+        gr, ga = _vjp([q], (vr, va), [dq])
     gr = torch.zeros_like(vr) if gr is None else gr
     ga = torch.zeros_like(va) if ga is None else ga
     forces = positions.new_zeros((n, 3))

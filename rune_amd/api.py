@@ -15,6 +15,7 @@ import numpy as np
 import torch
 
 from . import _native as N
+from . import ops
 from .elements import ATOMIC_NUMBERS, symbol_of
 
 
@@ -47,6 +48,7 @@ class Evaluator:
         self.z_to_type = {ATOMIC_NUMBERS[e]: t for t, e in enumerate(self.elements)}
         self.native = N.NativeModel(params, state_dict, family)
         self.nlist = N.NeighborList()
+        self._op_handle = None
 
     def types_of(self, numbers):
         numbers = [int(z) for z in numbers]
@@ -83,12 +85,31 @@ class Evaluator:
 
     def evaluate(self, structures_or_prepared, compute_forces=True, compute_virial=True,
                  atom_virial=False):
+        """E + F + virial through ``torch.ops.rune_hip.evaluate`` (see ``rune_amd.ops``)."""
         prep = structures_or_prepared
         if not isinstance(prep, Prepared):
             prep = self.prepare(prep)
-        nl = self.build_neighbors(prep)
-        return self.native.compute(nl, prep.types, prep.n_structures, compute_forces,
-                                   compute_virial, atom_virial)
+        if atom_virial:
+            nl = self.build_neighbors(prep)
+            return self.native.compute(nl, prep.types, prep.n_structures, compute_forces,
+                                       compute_virial, atom_virial)
+        if self._op_handle is None:
+            self._op_handle = ops.register(self)
+        e, etot, f, v = torch.ops.rune_hip.evaluate(
+            self._op_handle, prep.positions, prep.types, [int(x) for x in prep.struct_ptr],
+            [float(x) for x in np.asarray(prep.cells).reshape(-1)],
+            [int(x) for x in np.asarray(prep.pbc).reshape(-1)], bool(compute_forces),
+            bool(compute_virial))
+        out = {"energies": e, "energy": etot}
+        if compute_forces:
+            out["forces"] = f
+        if compute_virial:
+            out["virial"] = v
+        return out
+
+    def __del__(self):
+        if getattr(self, "_op_handle", None) is not None:
+            ops.unregister(self._op_handle)
 
 
 def load_checkpoint(path):

@@ -41,6 +41,14 @@ class AngularDescriptor(nn.Module):
         for L in range(1, 9):
             self.register_buffer(f"Z{L}", torch.tensor(T.Z_COEFF[L], dtype=torch.float32))
 
+    def orthonormal_scale(self, reference, l_max):
+        """``descriptor.py:626-637``: sqrt(2 C3B), halved at m = 0, in ``reference``'s dtype."""
+        size = l_max * (l_max + 2)
+        metric = reference.new_tensor(T.C3B[:size]) * 2.0
+        for order in range(1, l_max + 1):
+            metric[order * order - 1] *= 0.5
+        return metric.sqrt()
+
 
 def descriptor_flags(params):
     """(q222, q1111, q112, q123, q233, q134) as ``descriptor.py:893-900`` resolves them."""

@@ -299,11 +299,47 @@ def main(reference):
     path = HERE / "nep_desc_pbte64.npz"
     np.savez_compressed(path, **rec)
     out_files.append(path)
+    out_files += export_fixtures(reference)
     with open(HERE / "MANIFEST.txt", "w") as fh:
         fh.write("# sha256  file  (written by make_golden.py)\n")
         for f in out_files:
             fh.write(f"{hashlib.sha256(f.read_bytes()).hexdigest()}  {f.name}\n")
     print("\n".join(str(f) for f in out_files))
+
+
+EXPORT_CASES = {
+    "local": {"message_layers": 0},
+    "mp": {"zbl": [0.5, 1.5]},
+    "eq": {"message_mode": "equivariant", "equivariant_channels": 3, "activation": "gelu"},
+}
+
+
+def small_export_model(kind):
+    """Small seeded model of this build's drop-in Mobius (same state_dict layout)."""
+    from rune_amd.mobius.model import Mobius
+    from rune_amd.mobius.plugin import resolve_params
+    values = {"elements": ["Fe", "C"], "hidden_dim": 8, "blocks": 1, "ffn_dim": 12,
+              "message_layers": 2, "message_dim": 8, "message_groups": 2, "pair_dim": 3,
+              "vector_channels": 2, "message_basis_size": 3, "rcut_radial": 3.8,
+              "rcut_angular": 3.5, "n_max_radial": 1, "n_max_angular": 1,
+              "basis_size_radial": 2, "basis_size_angular": 2, "l_max": 4, "l_max_4body": 2,
+              "l_max_5body": 1, "has_q_112": 1, "has_q_123": 1, "has_q_233": 1, "has_q_134": 1}
+    values.update(EXPORT_CASES[kind])
+    torch.manual_seed(20261021)
+    return Mobius(resolve_params(values))
+
+
+def export_fixtures(reference):
+    """mobius.txt written by the reference exporter (rune/mobius/export.py)."""
+    sys.path.insert(0, str(reference))
+    from rune.mobius import export as ref_export
+    out = []
+    for kind in EXPORT_CASES:
+        model = small_export_model(kind)
+        path = HERE / f"export_{kind}.mobius.txt"
+        ref_export.export_model(model, path)
+        out.append(path)
+    return out
 
 
 if __name__ == "__main__":
