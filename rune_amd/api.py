@@ -11,6 +11,8 @@ the neighbour search.
 
 from __future__ import annotations
 
+import weakref
+
 import numpy as np
 import torch
 
@@ -95,6 +97,9 @@ class Evaluator:
                                        compute_virial, atom_virial)
         if self._op_handle is None:
             self._op_handle = ops.register(self)
+            # finalize (not __del__) also runs at interpreter exit, before the
+            # ops module is torn down
+            weakref.finalize(self, ops.unregister, self._op_handle)
         e, etot, f, v = torch.ops.rune_hip.evaluate(
             self._op_handle, prep.positions, prep.types, [int(x) for x in prep.struct_ptr],
             [float(x) for x in np.asarray(prep.cells).reshape(-1)],
@@ -106,10 +111,6 @@ class Evaluator:
         if compute_virial:
             out["virial"] = v
         return out
-
-    def __del__(self):
-        if getattr(self, "_op_handle", None) is not None:
-            ops.unregister(self._op_handle)
 
 
 def load_checkpoint(path):

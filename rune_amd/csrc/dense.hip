@@ -9,7 +9,9 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 64, kBN = 64, kBK = 16;
+// GEMM tiling: 4 waves in 2x2, each wave (16*kWM) x (16*WN) of the output;
+// block tile kBM x (32*WN); K advances kBK = 32 per LDS stage.
+constexpr int kWM = 2, kBM = 32 * kWM, kBK = 32, kLdk = kBK + 4;
 
 __device__ inline float act_f(int a, float x) {
     if (a == RUNE_ACT_SILU) return x / (1.0f + expf(-x));
@@ -34,77 +36,148 @@ __device__ inline float act_d(int a, float x) {
     return 1.0f;
 }
 
-// 256 threads, 2x2 waves, each wave a 32x32 sub-tile of v_mfma_f32_16x16x4f32.
-// MFMA operand layout: lane l supplies A[l%16][l/16] and B[l/16][l%16];
-// accumulator register v of lane l is C[4*(l/16)+v][l%16].
+// One K stage of a row-major operand X[rows, K] (A, or B stored as Bt[N, K])
+// into registers.  Slot q of the tile covers row q/8 and four K values:
+// vector path (ld % 4 == 0, 16-byte aligned base) k = 4*(q%8) + {0..3};
+// scalar path k = q%8 + 8*{0..3}, so each load instruction stays coalesced.
+// Either way the four values land in LDS columns 4*(q%8)..+3, and A and B use
+// the same path, so LDS column c holds the same k for both operands.
+template <int kRows, bool kVec>
+__device__ inline void load_stage(float4 (&r)[kRows * 8 / 256], const float *__restrict__ X,
+                                  int ld, int row0, int nrows, int k0, int K, int tid) {
+#pragma unroll
+    for (int it = 0; it < kRows * 8 / 256; ++it) {
+        int q = tid + 256 * it, row = q >> 3, c4 = q & 7;
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (row0 + row < nrows) {
+            const float *x = X + size_t(row0 + row) * ld;
+            if (kVec) {
+                int k = k0 + 4 * c4;
+                if (k + 3 < K) {
+                    v = *reinterpret_cast<const float4 *>(x + k);
+                } else if (k < K) {
+                    v.x = x[k];
+                    if (k + 1 < K) v.y = x[k + 1];
+                    if (k + 2 < K) v.z = x[k + 2];
+                }
+            } else {
+                int k = k0 + c4;
+                if (k < K) v.x = x[k];
+                if (k + 8 < K) v.y = x[k + 8];
+                if (k + 16 < K) v.z = x[k + 16];
+                if (k + 24 < K) v.w = x[k + 24];
+            }
+        }
+        r[it] = v;
+    }
+}
+
+template <int kRows>
+__device__ inline void store_stage(const float4 (&r)[kRows * 8 / 256], float *S, int tid) {
+#pragma unroll
+    for (int it = 0; it < kRows * 8 / 256; ++it) {
+        int q = tid + 256 * it;
+        *reinterpret_cast<float4 *>(S + (q >> 3) * kLdk + 4 * (q & 7)) = r[it];
+    }
+}
+
+// C[M,N] = A[M,K] Bt[N,K]^T with the fused epilogue.  256 threads.
+// MFMA operand layout (v_mfma_f32_16x16x4f32): lane l supplies A[l%16][l/16]
+// and B[l/16][l%16]; accumulator register v of lane l is C[4*(l/16)+v][l%16].
+// The k index l/16 of MFMA step s in half h is LDS column 16h + 4(l/16) + s, so
+// each lane fetches its four steps with one 16-byte LDS read.  Row stride
+// kLdk = 36 floats keeps those reads free of bank conflicts.
+// Block b covers row tile b / nbn and column tile b % nbn.
+template <int WN, bool kVec>
 __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *__restrict__ A,
-                                              int lda, const float *__restrict__ B, int ldb,
-                                              float *__restrict__ C, int ldc, Epilogue ep) {
-    __shared__ float As[kBK][kBM + 4];
-    __shared__ float Bs[kBK][kBN + 4];
+                                              int lda, const float *__restrict__ Bt, int ldb,
+                                              float *__restrict__ C, int ldc, Epilogue ep,
+                                              int nbn) {
+    constexpr int BN = 32 * WN, kLdo = BN + 4;
+    static_assert(32 * kLdo <= (kBM + BN) * kLdk, "epilogue staging exceeds the tile LDS");
+    __shared__ __attribute__((aligned(16))) float smem[(kBM + BN) * kLdk];
+    float *As = smem, *Bs = smem + kBM * kLdk;
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
-    const int m0 = blockIdx.x * kBM, n0 = blockIdx.y * kBN;
-    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
-    floatx4 acc[2][2];
+    const int m0 = (blockIdx.x / nbn) * kBM, n0 = (blockIdx.x % nbn) * BN;
+    const int wm = (wave >> 1) * 16 * kWM, wn = (wave & 1) * 16 * WN;
+    const int g = lane >> 4, rr = lane & 15;
+    floatx4 acc[kWM][WN];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < kWM; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) acc[a][b] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int b = 0; b < WN; ++b) acc[a][b] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    float4 ra[kBM * 8 / 256], rb[BN * 8 / 256];
+    load_stage<kBM, kVec>(ra, A, lda, m0, M, 0, K, tid);
+    load_stage<BN, kVec>(rb, Bt, ldb, n0, N, 0, K, tid);
     for (int k0 = 0; k0 < K; k0 += kBK) {
-#pragma unroll
-        for (int it = 0; it < (kBM * kBK) / 256; ++it) {
-            int idx = tid + 256 * it;
-            int mm = idx / kBK, kk = idx % kBK;
-            int gm = m0 + mm, gk = k0 + kk;
-            As[kk][mm] = (gm < M && gk < K) ? A[size_t(gm) * lda + gk] : 0.0f;
-        }
-#pragma unroll
-        for (int it = 0; it < (kBK * kBN) / 256; ++it) {
-            int idx = tid + 256 * it;
-            int kk = idx / kBN, nn = idx % kBN;
-            int gk = k0 + kk, gn = n0 + nn;
-            Bs[kk][nn] = (gk < K && gn < N) ? B[size_t(gk) * ldb + gn] : 0.0f;
-        }
+        store_stage<kBM>(ra, As, tid);
+        store_stage<BN>(rb, Bs, tid);
         __syncthreads();
+        if (k0 + kBK < K) {
+            load_stage<kBM, kVec>(ra, A, lda, m0, M, k0 + kBK, K, tid);
+            load_stage<BN, kVec>(rb, Bt, ldb, n0, N, k0 + kBK, K, tid);
+        }
 #pragma unroll
-        for (int kk = 0; kk < kBK; kk += 4) {
-            int kq = kk + (lane >> 4), rr = lane & 15;
-            float a0 = As[kq][wm + rr], a1 = As[kq][wm + 16 + rr];
-            float b0 = Bs[kq][wn + rr], b1 = Bs[kq][wn + 16 + rr];
-            acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc[1][1], 0, 0, 0);
+        for (int h = 0; h < 2; ++h) {
+            float4 fa[kWM], fb[WN];
+#pragma unroll
+            for (int a = 0; a < kWM; ++a)
+                fa[a] = *reinterpret_cast<const float4 *>(As + (wm + 16 * a + rr) * kLdk +
+                                                          16 * h + 4 * g);
+#pragma unroll
+            for (int b = 0; b < WN; ++b)
+                fb[b] = *reinterpret_cast<const float4 *>(Bs + (wn + 16 * b + rr) * kLdk +
+                                                          16 * h + 4 * g);
+#pragma unroll
+            for (int a = 0; a < kWM; ++a)
+#pragma unroll
+                for (int b = 0; b < WN; ++b) {
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a].x, fb[b].x, acc[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a].y, fb[b].y, acc[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a].z, fb[b].z, acc[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a].w, fb[b].w, acc[a][b], 0, 0, 0);
+                }
         }
         __syncthreads();
     }
+    // Epilogue through LDS, one 32-row half of the tile at a time: the waves
+    // owning the half store their accumulators (row stride kLdo = BN + 4 puts
+    // the four lane groups on distinct banks), then all 256 threads apply the
+    // epilogue row-contiguously.
 #pragma unroll
-    for (int a = 0; a < 2; ++a) {
+    for (int half = 0; half < 2; ++half) {
+        if ((wave >> 1) == half) {
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
+            for (int a = 0; a < kWM; ++a)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                int row = m0 + wm + a * 16 + 4 * (lane >> 4) + v;
-                int col = n0 + wn + b * 16 + (lane & 15);
-                if (row >= M || col >= N) continue;
-                float x = acc[a][b][v];
-                if (ep.row_scale) x *= ep.row_scale[row];
-                if (ep.bias) x += ep.bias[col];
-                if (ep.emb) x += ep.emb[size_t(ep.types[row]) * ep.ld_emb + col];
-                if (ep.residual) x += ep.residual[size_t(row) * ep.ldr + col];
+                for (int b = 0; b < WN; ++b)
 #pragma unroll
-                for (int k = 0; k < 3; ++k)
-                    if (ep.gtab[k]) x += ep.gtab[k][size_t(ep.gidx[k][row]) * ep.gld[k] + col];
-                if (ep.pre) ep.pre[size_t(row) * ep.ldp + col] = x;
-                if (ep.act_split >= 0 && col >= ep.act_split)
-                    x = act_f(ep.act2, x);
-                else if (ep.act >= 0)
-                    x = act_f(ep.act, x);
-                if (ep.dact_from) x *= act_d(ep.dact, ep.dact_from[size_t(row) * ep.ldu + col]);
-                C[size_t(row) * ldc + col] = x;
-            }
+                    for (int v = 0; v < 4; ++v)
+                        smem[(16 * a + 4 * g + v) * kLdo + wn + 16 * b + rr] = acc[a][b][v];
         }
+        __syncthreads();
+        for (int idx = tid; idx < 32 * BN; idx += 256) {
+            int lr = idx / BN, lc = idx - lr * BN;
+            int row = m0 + 32 * half + lr, col = n0 + lc;
+            if (row >= M || col >= N) continue;
+            float x = smem[lr * kLdo + lc];
+            if (ep.row_scale) x *= ep.row_scale[row];
+            if (ep.bias) x += ep.bias[col];
+            if (ep.emb) x += ep.emb[size_t(ep.types[row]) * ep.ld_emb + col];
+            if (ep.residual) x += ep.residual[size_t(row) * ep.ldr + col];
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+                if (ep.gtab[k]) x += ep.gtab[k][size_t(ep.gidx[k][row]) * ep.gld[k] + col];
+            if (ep.pre) ep.pre[size_t(row) * ep.ldp + col] = x;
+            if (ep.act_split >= 0 && col >= ep.act_split)
+                x = act_f(ep.act2, x);
+            else if (ep.act >= 0)
+                x = act_f(ep.act, x);
+            if (ep.dact_from) x *= act_d(ep.dact, ep.dact_from[size_t(row) * ep.ldu + col]);
+            C[size_t(row) * ldc + col] = x;
+        }
+        __syncthreads();
     }
 }
 
@@ -199,11 +272,45 @@ __global__ void k_nep_mlp(int M, int Q, int Hn, const float *q, int ldq, const i
 
 }  // namespace
 
-void gemm(int M, int N, int K, const float *A, int lda, const float *B, int ldb, float *C,
+// Column tile 32*WN with the least padding of N; ties go to the wider tile.
+static int pick_wn(int N) {
+    const int opts[4] = {9, 6, 4, 2};
+    int best = 2, waste = 1 << 30;
+    for (int wn : opts) {
+        int bn = 32 * wn, w = ceil_div(N, bn) * bn - N;
+        if (w < waste) {
+            waste = w;
+            best = wn;
+        }
+    }
+    return best;
+}
+
+template <int WN>
+static void launch_gemm(bool vec, int M, int N, int K, const float *A, int lda, const float *Bt,
+                        int ldb, float *C, int ldc, const Epilogue &ep, hipStream_t s) {
+    int nbn = ceil_div(N, 32 * WN);
+    int64_t blocks = int64_t(ceil_div(M, kBM)) * nbn;
+    if (blocks > 0x7fffffff) throw Error(RUNE_ERR_ARGUMENT, "gemm: problem too large");
+    if (vec)
+        hipLaunchKernelGGL((k_gemm<WN, true>), dim3(unsigned(blocks)), dim3(256), 0, s, M, N, K,
+                           A, lda, Bt, ldb, C, ldc, ep, nbn);
+    else
+        hipLaunchKernelGGL((k_gemm<WN, false>), dim3(unsigned(blocks)), dim3(256), 0, s, M, N,
+                           K, A, lda, Bt, ldb, C, ldc, ep, nbn);
+}
+
+void gemm(int M, int N, int K, const float *A, int lda, const float *Bt, int ldb, float *C,
           int ldc, const Epilogue &ep, hipStream_t s) {
     if (M == 0 || N == 0) return;
-    dim3 grid(ceil_div(M, kBM), ceil_div(N, kBN));
-    hipLaunchKernelGGL(k_gemm, grid, dim3(256), 0, s, M, N, K, A, lda, B, ldb, C, ldc, ep);
+    bool vec = lda % 4 == 0 && ldb % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
+               (reinterpret_cast<uintptr_t>(Bt) & 15) == 0;
+    switch (pick_wn(N)) {
+    case 9: launch_gemm<9>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s); break;
+    case 6: launch_gemm<6>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s); break;
+    case 4: launch_gemm<4>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s); break;
+    default: launch_gemm<2>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s); break;
+    }
     RUNE_HIP_CHECK(hipGetLastError());
 }
 

@@ -93,11 +93,14 @@ __global__ void __launch_bounds__(kWave) k_eq_mix(const float *mixw, const float
 // Edge features [rb | probes_c | probes_n] of the radial records of centre i.
 __global__ void __launch_bounds__(kWave) k_eq_features(EqArgs a) {
     extern __shared__ float lds[];
-    float *Hi = lds;   // [C*nq]
+    const int C = a.C, nq = a.nq, lq = a.lq, LC = lq * C, CN = C * nq;
+    const int ldc = nq | 1;   // odd LDS row stride: channel-strided reads hit distinct banks
+    float *Hi = lds;          // [C][ldc] centre state
+    float *Hj = Hi + C * ldc; // [C][ldc] neighbour state of the current record
+    float *Yl = Hj + C * ldc; // [nq]
     const int i = blockIdx.x, lane = threadIdx.x;
-    const int C = a.C, nq = a.nq, lq = a.lq, LC = lq * C;
-    for (int o = lane; o < C * nq; o += kWave) Hi[o] = a.dir_in[size_t(i) * C * nq + o];
-    __syncthreads();
+    for (int o = lane; o < CN; o += kWave)
+        Hi[(o / nq) * ldc + o % nq] = a.dir_in[size_t(i) * CN + o];
     const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
     for (int e = rb; e < re; ++e) {
         float *x = a.x + size_t(e) * a.ldx;
@@ -106,28 +109,33 @@ __global__ void __launch_bounds__(kWave) k_eq_features(EqArgs a) {
             for (int k = lane; k < a.KX; k += kWave) x[k] = 0.0f;
             continue;
         }
-        const float *Y = a.harm + size_t(e) * nq;
-        const float *Hj = a.dir_in + size_t(a.r.nbr[e]) * C * nq;
+        const float *hj = a.dir_in + size_t(a.r.nbr[e]) * CN;
+        for (int o = lane; o < CN; o += kWave) Hj[(o / nq) * ldc + o % nq] = hj[o];
+        if (lane < nq) Yl[lane] = a.harm[size_t(e) * nq + lane];
         if (lane < a.kb) x[lane] = a.rb[size_t(e) * a.ldrb + lane];
+        __syncthreads();
         for (int p = lane; p < LC; p += kWave) {
             int L = p / C + 1, c = p - (L - 1) * C, st = L * L - 1;
             float pc = 0.0f, pn = 0.0f;
             for (int m = 0; m < 2 * L + 1; ++m) {
-                pc += Hi[c * nq + st + m] * Y[st + m];
-                pn += Hj[c * nq + st + m] * Y[st + m];
+                pc += Hi[c * ldc + st + m] * Yl[st + m];
+                pn += Hj[c * ldc + st + m] * Yl[st + m];
             }
             x[a.kb + p] = pc;
             x[a.kb + LC + p] = (L & 1) ? -pn : pn;
         }
+        __syncthreads();
     }
 }
 
 __global__ void __launch_bounds__(kWave) k_eq_aggregate(EqArgs a) {
     extern __shared__ float lds[];
-    float *Ho = lds;   // [C*nq]
-    const int i = blockIdx.x, lane = threadIdx.x;
     const int H = a.H, G = a.G, C = a.C, nq = a.nq, lq = a.lq, gw = H / G, LC = lq * C;
     const int CN = C * nq;
+    float *Ho = lds;          // [CN]
+    float *gL = Ho + CN;      // [NG] gates of the current record
+    float *Yl = gL + a.NG;    // [nq]
+    const int i = blockIdx.x, lane = threadIdx.x;
     float macc[4] = {0, 0, 0, 0};
     float dacc[kMaxOut];
     int gT[kMaxOut];
@@ -146,20 +154,23 @@ __global__ void __launch_bounds__(kWave) k_eq_aggregate(EqArgs a) {
         if (fc == 0.0f) continue;
         int j = a.r.nbr[e];
         const float *gl = a.ag + size_t(e) * a.NG;
+        for (int k = lane; k < a.NG; k += kWave) gL[k] = gl[k];
+        if (lane < nq) Yl[lane] = a.harm[size_t(e) * nq + lane];
+        __syncthreads();
         const float *V = a.node + size_t(j) * a.NP + 2 * a.D;
         const float *MX = a.mixst + size_t(j) * CN;
-        const float *Y = a.harm + size_t(e) * nq;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             int c = lane + kWave * t;
-            if (c < H) macc[t] += gl[c / gw] * fc * V[c];
+            if (c < H) macc[t] += gL[c / gw] * fc * V[c];
         }
 #pragma unroll
         for (int t = 0; t < kMaxOut; ++t) {
             int o = lane + kWave * t;
             if (o < CN)
-                dacc[t] += fc * (gl[gT[t]] * MX[o] + gl[gT[t] + LC] * Y[kk[t]]);
+                dacc[t] += fc * (gL[gT[t]] * MX[o] + gL[gT[t] + LC] * Yl[kk[t]]);
         }
+        __syncthreads();
     }
 #pragma unroll
     for (int t = 0; t < kMaxOut; ++t) {
@@ -220,20 +231,31 @@ __global__ void __launch_bounds__(kWave) k_eq_node_backward(EqArgs a) {
 __global__ void __launch_bounds__(kWave) k_eq_edge_backward(EqArgs a) {
     extern __shared__ float lds[];
     const int H = a.H, G = a.G, C = a.C, nq = a.nq, lq = a.lq, gw = H / G, LC = lq * C;
-    const int CN = C * nq;
-    float *dHt = lds;            // [CN]
-    float *term = dHt + CN;      // [CN]
-    float *pL = term + CN;       // [H]
-    float *YL = pL + H;          // [nq]
+    const int CN = C * nq, ldc = nq | 1;   // odd row stride: conflict-free channel reads
+    float *pT = lds;             // [C][ldc] dHt_i * mixed_j
+    float *pI = pT + C * ldc;    // [C][ldc] dHt_i * Y
+    float *term = pI + C * ldc;  // [C][ldc] tanh(injection) * dHt_i
+    float *pL = term + C * ldc;  // [H]
+    float *gL = pL + H;          // [NG]
+    float *YL = gL + a.NG;       // [nq]
     const int i = blockIdx.x, lane = threadIdx.x;
-    for (int o = lane; o < CN; o += kWave) dHt[o] = a.dht[size_t(i) * CN + o];
+    float dh[kMaxOut];
+    int gI[kMaxOut], kk[kMaxOut], so[kMaxOut];
+#pragma unroll
+    for (int t = 0; t < kMaxOut; ++t) {
+        int o = lane + kWave * t;
+        int c = o / nq, k = o - c * nq;
+        kk[t] = k;
+        so[t] = c * ldc + k;
+        gI[t] = o < CN ? G + LC + (order_of(k) - 1) * C + c : 0;
+        dh[t] = o < CN ? a.dht[size_t(i) * CN + o] : 0.0f;
+    }
     float dm[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         int c = lane + kWave * t;
         dm[t] = c < H ? a.dmsg[size_t(i) * H + c] : 0.0f;
     }
-    __syncthreads();
     const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
     for (int e = rb; e < re; ++e) {
         float fc = a.fc[e];
@@ -246,6 +268,7 @@ __global__ void __launch_bounds__(kWave) k_eq_edge_backward(EqArgs a) {
         const float *gl = a.ag + size_t(e) * a.NG;
         const float *V = a.node + size_t(j) * a.NP + 2 * a.D;
         const float *MX = a.mixst + size_t(j) * CN;
+        for (int k = lane; k < a.NG; k += kWave) gL[k] = gl[k];
         if (lane < nq) YL[lane] = a.harm[size_t(e) * nq + lane];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -253,35 +276,39 @@ __global__ void __launch_bounds__(kWave) k_eq_edge_backward(EqArgs a) {
             if (c < H) pL[c] = dm[t] * V[c];
         }
         __syncthreads();
+#pragma unroll
+        for (int t = 0; t < kMaxOut; ++t) {
+            int o = lane + kWave * t;
+            if (o < CN) {
+                pT[so[t]] = dh[t] * MX[o];
+                pI[so[t]] = dh[t] * YL[kk[t]];
+                term[so[t]] = gL[gI[t]] * dh[t];
+            }
+        }
+        __syncthreads();
         float dfc = 0.0f;
         for (int p = lane; p < LC; p += kWave) {
             int L = p / C + 1, c = p - (L - 1) * C, st = L * L - 1;
             float sT = 0.0f, sI = 0.0f;
             for (int m = 0; m < 2 * L + 1; ++m) {
-                float g = dHt[c * nq + st + m];
-                sT += g * MX[c * nq + st + m];
-                sI += g * YL[st + m];
+                sT += pT[c * ldc + st + m];
+                sI += pI[c * ldc + st + m];
             }
-            float tT = gl[G + p], tI = gl[G + LC + p];
+            float tT = gL[G + p], tI = gL[G + LC + p];
             dg[G + p] = (1.0f - tT * tT) * fc * sT;
             dg[G + LC + p] = (1.0f - tI * tI) * fc * sI;
             dfc += tT * sT + tI * sI;
         }
-        for (int o = lane; o < CN; o += kWave) {
-            int c = o / nq, k = o - c * nq, L = order_of(k);
-            term[o] = gl[G + LC + (L - 1) * C + c] * dHt[o];
-        }
         if (lane < G) {
             float P = 0.0f;
             for (int c = lane * gw; c < (lane + 1) * gw; ++c) P += pL[c];
-            float s = gl[lane];
+            float s = gL[lane];
             dg[lane] = P * fc * s * (1.0f - s);
             dfc += P * s;
         }
-        __syncthreads();
         if (lane < nq) {
             float y = 0.0f;
-            for (int c = 0; c < C; ++c) y += term[c * nq + lane];
+            for (int c = 0; c < C; ++c) y += term[c * ldc + lane];
             a.dy[size_t(e) * nq + lane] += fc * y;
         }
         dfc = wave_sum(dfc);
@@ -296,6 +323,7 @@ __global__ void __launch_bounds__(kWave) k_eq_edge_backward(EqArgs a) {
 
 // Adjoints landing on neighbour j: mixed states and gathered values.
 __global__ void __launch_bounds__(kWave) k_eq_neighbor_backward(EqArgs a) {
+    extern __shared__ float gL[];   // [NG] gates of the current record
     const int j = blockIdx.x, lane = threadIdx.x;
     const int H = a.H, G = a.G, C = a.C, nq = a.nq, gw = H / G, CN = C * nq;
     float macc[kMaxOut];
@@ -314,17 +342,20 @@ __global__ void __launch_bounds__(kWave) k_eq_neighbor_backward(EqArgs a) {
         if (fc == 0.0f) continue;
         int i = a.r.ctr[e];
         const float *gl = a.ag + size_t(e) * a.NG;
+        for (int k = lane; k < a.NG; k += kWave) gL[k] = gl[k];
+        __syncthreads();
         const float *dh = a.dht + size_t(i) * CN;
 #pragma unroll
         for (int q = 0; q < kMaxOut; ++q) {
             int o = lane + kWave * q;
-            if (o < CN) macc[q] += fc * gl[gT[q]] * dh[o];
+            if (o < CN) macc[q] += fc * gL[gT[q]] * dh[o];
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             int c = lane + kWave * q;
-            if (c < H) vacc[q] += gl[c / gw] * fc * a.dmsg[size_t(i) * H + c];
+            if (c < H) vacc[q] += gL[c / gw] * fc * a.dmsg[size_t(i) * H + c];
         }
+        __syncthreads();
     }
 #pragma unroll
     for (int q = 0; q < kMaxOut; ++q) {
@@ -341,59 +372,116 @@ __global__ void __launch_bounds__(kWave) k_eq_neighbor_backward(EqArgs a) {
 // Per-atom adjoints: context projections A (own records) and B (as neighbour),
 // and dE/d(dir_in) = identity + probes + channel mix.
 __global__ void __launch_bounds__(kWave) k_eq_atom_backward(EqArgs a) {
-    const int n = blockIdx.x, lane = threadIdx.x;
+    extern __shared__ float lds[];
     const int C = a.C, nq = a.nq, lq = a.lq, LC = lq * C, CN = C * nq, D = a.D;
-    const int rb = a.r.view[4 * n], re = a.r.view[4 * n + 1];
-    for (int c = lane; c < D; c += kWave) {
-        float sa = 0.0f, sb = 0.0f;
-        for (int e = rb; e < re; ++e)
-            if (a.fc[e] != 0.0f) sa += a.due[size_t(e) * D + c];
-        for (int t = a.r.tptr[n]; t < a.r.tptr[n + 1]; ++t) {
-            int e = a.r.tidx[t];
-            if (a.fc[e] != 0.0f) sb += a.due[size_t(e) * D + c];
-        }
-        a.dnode[size_t(n) * a.NP + c] = sa;
-        a.dnode[size_t(n) * a.NP + D + c] = sb;
+    float *dxL = lds;          // [LC] probe adjoints of the current record
+    float *Yl = dxL + LC;      // [nq]
+    float *dmixL = Yl + nq;    // [CN]
+    const int n = blockIdx.x, lane = threadIdx.x;
+    float sa[4] = {0, 0, 0, 0}, sb[4] = {0, 0, 0, 0};
+    float g[kMaxOut];
+    int col[kMaxOut], kk[kMaxOut], LL[kMaxOut];
+#pragma unroll
+    for (int t = 0; t < kMaxOut; ++t) {
+        int o = lane + kWave * t;
+        int c = o / nq, k = o - c * nq, L = o < CN ? order_of(k) : 1;
+        kk[t] = k;
+        LL[t] = L;
+        col[t] = (L - 1) * C + c;
+        g[t] = o < CN ? a.dht[size_t(n) * CN + o] : 0.0f;
     }
-    for (int o = lane; o < CN; o += kWave) {
-        int c = o / nq, k = o - c * nq, L = order_of(k);
-        int col = a.kb + (L - 1) * C + c;
-        float g = a.dht[size_t(n) * CN + o];
-        for (int e = rb; e < re; ++e)
-            if (a.fc[e] != 0.0f) g += a.dx[size_t(e) * a.ldx + col] * a.harm[size_t(e) * nq + k];
-        float gn = 0.0f;
-        for (int t = a.r.tptr[n]; t < a.r.tptr[n + 1]; ++t) {
-            int e = a.r.tidx[t];
-            if (a.fc[e] != 0.0f) gn += a.dx[size_t(e) * a.ldx + col + LC] * a.harm[size_t(e) * nq + k];
+    const int rb = a.r.view[4 * n], re = a.r.view[4 * n + 1];
+    // own records: dA, probes_c adjoint
+    for (int e = rb; e < re; ++e) {
+        if (a.fc[e] == 0.0f) continue;
+        const float *du = a.due + size_t(e) * D;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            int c = lane + kWave * q;
+            if (c < D) sa[q] += du[c];
         }
-        g += (L & 1) ? -gn : gn;
-        const float *M = a.mixw + size_t(L - 1) * C * C;
-        for (int cc = 0; cc < C; ++cc) g += M[cc * C + c] * a.dmix[size_t(n) * CN + cc * nq + k];
-        a.ddir_in[size_t(n) * CN + o] = g;
+        const float *dx = a.dx + size_t(e) * a.ldx + a.kb;
+        for (int p = lane; p < LC; p += kWave) dxL[p] = dx[p];
+        if (lane < nq) Yl[lane] = a.harm[size_t(e) * nq + lane];
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < kMaxOut; ++t)
+            if (lane + kWave * t < CN) g[t] += dxL[col[t]] * Yl[kk[t]];
+        __syncthreads();
+    }
+    // records where n is the neighbour: dB, probes_n adjoint
+    for (int q2 = a.r.tptr[n]; q2 < a.r.tptr[n + 1]; ++q2) {
+        int e = a.r.tidx[q2];
+        if (a.fc[e] == 0.0f) continue;
+        const float *du = a.due + size_t(e) * D;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            int c = lane + kWave * q;
+            if (c < D) sb[q] += du[c];
+        }
+        const float *dx = a.dx + size_t(e) * a.ldx + a.kb + LC;
+        for (int p = lane; p < LC; p += kWave) dxL[p] = dx[p];
+        if (lane < nq) Yl[lane] = a.harm[size_t(e) * nq + lane];
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < kMaxOut; ++t)
+            if (lane + kWave * t < CN) {
+                float v = dxL[col[t]] * Yl[kk[t]];
+                g[t] += (LL[t] & 1) ? -v : v;
+            }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        int c = lane + kWave * q;
+        if (c < D) {
+            a.dnode[size_t(n) * a.NP + c] = sa[q];
+            a.dnode[size_t(n) * a.NP + D + c] = sb[q];
+        }
+    }
+    // channel mix adjoint: dH[c][k] += sum_c' M_L[c'][c] dMIX[c'][k]
+    for (int o = lane; o < CN; o += kWave) dmixL[o] = a.dmix[size_t(n) * CN + o];
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < kMaxOut; ++t) {
+        int o = lane + kWave * t;
+        if (o >= CN) continue;
+        int c = col[t] - (LL[t] - 1) * C;
+        const float *M = a.mixw + size_t(LL[t] - 1) * C * C + c;
+        float s = 0.0f;
+        for (int cc = 0; cc < C; ++cc) s += M[cc * C] * dmixL[cc * nq + kk[t]];
+        a.ddir_in[size_t(n) * CN + o] = g[t] + s;
     }
 }
 
 // dE/dY from the probes of the records of centre i.
 __global__ void __launch_bounds__(kWave) k_eq_probe_dy(EqArgs a) {
     extern __shared__ float lds[];
-    float *Hi = lds;
-    const int i = blockIdx.x, lane = threadIdx.x;
     const int C = a.C, nq = a.nq, LC = a.lq * C, CN = C * nq;
+    float *Hi = lds;          // [CN]
+    float *Hj = Hi + CN;      // [CN]
+    float *dxL = Hj + CN;     // [2 LC]
+    const int i = blockIdx.x, lane = threadIdx.x;
     for (int o = lane; o < CN; o += kWave) Hi[o] = a.dir_in[size_t(i) * CN + o];
-    __syncthreads();
     const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
-    if (lane >= nq) return;
-    const int k = lane, L = order_of(k);
+    const int k = lane < nq ? lane : 0, L = order_of(k);
     for (int e = rb; e < re; ++e) {
         if (a.fc[e] == 0.0f) continue;
-        const float *Hj = a.dir_in + size_t(a.r.nbr[e]) * CN;
-        const float *dx = a.dx + size_t(e) * a.ldx + a.kb + (L - 1) * C;
-        float yc = 0.0f, yn = 0.0f;
-        for (int c = 0; c < C; ++c) {
-            yc += dx[c] * Hi[c * nq + k];
-            yn += dx[LC + c] * Hj[c * nq + k];
+        const float *hj = a.dir_in + size_t(a.r.nbr[e]) * CN;
+        for (int o = lane; o < CN; o += kWave) Hj[o] = hj[o];
+        const float *dx = a.dx + size_t(e) * a.ldx + a.kb;
+        for (int p = lane; p < 2 * LC; p += kWave) dxL[p] = dx[p];
+        __syncthreads();
+        if (lane < nq) {
+            const float *dc = dxL + (L - 1) * C;
+            float yc = 0.0f, yn = 0.0f;
+            for (int c = 0; c < C; ++c) {
+                yc += dc[c] * Hi[c * nq + k];
+                yn += dc[LC + c] * Hj[c * nq + k];
+            }
+            a.dy[size_t(e) * nq + k] += yc + ((L & 1) ? -yn : yn);
         }
-        a.dy[size_t(e) * nq + k] += yc + ((L & 1) ? -yn : yn);
+        __syncthreads();
     }
 }
 
@@ -486,6 +574,8 @@ void validate_equivariant(ModelImpl &m) {
     RUNE_REQUIRE(C >= 1 && C * lq * (lq + 2) <= kWave * kMaxOut, RUNE_ERR_ARGUMENT,
                  "equivariant_channels * l(l+2) must not exceed 768");
     RUNE_REQUIRE(c.message_groups <= kWave, RUNE_ERR_ARGUMENT, "message_groups must be <= 64");
+    RUNE_REQUIRE(c.message_dim <= 4 * kWave, RUNE_ERR_ARGUMENT,
+                 "equivariant blocks support message_dim <= 256");
 }
 
 void define_expected_equivariant(ModelImpl &m) {
@@ -578,7 +668,7 @@ void pack_equivariant(ModelImpl &m, Packer &pk, std::map<std::string, size_t> &o
             for (int k = 0; k < kb; ++k) x[size_t(r) * KX + k] = wx[size_t(r) * kb + k];
             for (int k = 0; k < 2 * W; ++k) x[size_t(r) * KX + kb + k] = wp[size_t(r) * 2 * W + k];
         }
-        off[p + "edge_x"] = pk.put(x);
+        off[p + "edge_x"] = pk.put(pad_rows(x, D, KX));
         off[p + "edge_xT"] = pk.put(transpose(x, D, KX));
         off[p + "pair_proj"] = pk.put(pair_projection(m.tensor(p + "pair_embedding.weight"), we,
                                                       m.tensor(p + "edge_mlp.0.bias"), T * T, P,
@@ -623,6 +713,7 @@ void bind_equivariant(ModelImpl &m, const PackedLookup &P) {
         w.NP = 2 * c.message_dim + c.hidden_dim;
         w.NG = c.message_groups + 2 * W;
         w.KX = c.message_basis_size + 2 * W;
+        w.ld_edge_x = (w.KX + 3) & ~3;
         w.node_f = P(p + "node_f");
         w.node_fT = P(p + "node_fT");
         w.edge_x = P(p + "edge_x");
@@ -769,11 +860,12 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
         row_inv_rms(N, H, cur, H, float(c.norm_eps), p.at(bb.rin), s);
         Epilogue e0;
         e0.row_scale = p.at(bb.rin);
-        gemm(N, w.NP, H, cur, H, w.node_fT, w.NP, p.at(bb.vs), w.NP, e0, s);
+        gemm(N, w.NP, H, cur, H, w.node_f, H, p.at(bb.vs), w.NP, e0, s);
         hipLaunchKernelGGL(k_eq_mix, dim3(N), dim3(kWave), 0, s, w.mix, p.at(bb.dir_in), C, nq,
                            p.at(bb.mixstate));
         if (E > 0) {
-            hipLaunchKernelGGL(k_eq_features, dim3(N), dim3(kWave), sizeof(float) * C * nq, s, a);
+            hipLaunchKernelGGL(k_eq_features, dim3(N), dim3(kWave),
+                               sizeof(float) * (2 * C * (nq | 1) + nq), s, a);
             RUNE_HIP_CHECK(hipGetLastError());
             Epilogue e1;
             e1.gtab[0] = p.at(bb.vs);
@@ -788,15 +880,17 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
             e1.pre = p.at(bb.ue);
             e1.ldp = D;
             e1.act = act;
-            gemm(int(E), D, w.KX, p.at(bb.xe), a.ldx, w.edge_xT, D, p.at(bb.eh), D, e1, s);
+            gemm(int(E), D, w.KX, p.at(bb.xe), a.ldx, w.edge_x, w.ld_edge_x, p.at(bb.eh), D, e1,
+                 s);
             Epilogue e2;
             e2.bias = w.gate_b;
             e2.act = kActSigmoid;
             e2.act_split = c.message_groups;
             e2.act2 = RUNE_ACT_TANH;
-            gemm(int(E), w.NG, D, p.at(bb.eh), D, w.gate_T, w.NG, p.at(bb.gv), w.NG, e2, s);
+            gemm(int(E), w.NG, D, p.at(bb.eh), D, w.gate, D, p.at(bb.gv), w.NG, e2, s);
         }
-        hipLaunchKernelGGL(k_eq_aggregate, dim3(N), dim3(kWave), sizeof(float) * C * nq, s, a);
+        hipLaunchKernelGGL(k_eq_aggregate, dim3(N), dim3(kWave),
+                           sizeof(float) * (C * nq + w.NG + nq), s, a);
         RUNE_HIP_CHECK(hipGetLastError());
         const int NU = H + lq * C;
         Epilogue e3;
@@ -804,12 +898,12 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
         e3.pre = p.at(bb.u1);
         e3.ldp = D;
         e3.act = act;
-        gemm(N, D, NU, p.at(bb.uin), NU, w.up1_fT, D, p.at(bb.z1), D, e3, s);
+        gemm(N, D, NU, p.at(bb.uin), NU, w.up1_f, NU, p.at(bb.z1), D, e3, s);
         Epilogue e4;
         e4.bias = w.up2_b;
         e4.residual = cur;
         e4.ldr = H;
-        gemm(N, H, D, p.at(bb.z1), D, w.up2_T, H, p.at(bb.h_out), H, e4, s);
+        gemm(N, H, D, p.at(bb.z1), D, w.up2, D, p.at(bb.h_out), H, e4, s);
         p.block_input.push_back(cur);
         cur = p.at(bb.h_out);
     }
@@ -840,29 +934,33 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         e0.dact_from = p.at(bb.u1);
         e0.ldu = D;
         e0.dact = act;
-        gemm(N, D, H, cur, H, w.up2, D, p.at(p.t_dz1), D, e0, s);
+        gemm(N, D, H, cur, H, w.up2_T, H, p.at(p.t_dz1), D, e0, s);
         Epilogue e1;
-        gemm(N, NU, D, p.at(p.t_dz1), D, w.up1_f, NU, p.at(p.t_duin), NU, e1, s);
+        gemm(N, NU, D, p.at(p.t_dz1), D, w.up1_fT, D, p.at(p.t_duin), NU, e1, s);
         hipLaunchKernelGGL(k_eq_node_backward, dim3(N), dim3(kWave), 0, s, a);
-        size_t lds = sizeof(float) * (2 * CN + H + nq);
+        size_t lds = sizeof(float) * (3 * C * (nq | 1) + H + w.NG + nq);
         hipLaunchKernelGGL(k_eq_edge_backward, dim3(N), dim3(kWave), lds, s, a);
-        hipLaunchKernelGGL(k_eq_neighbor_backward, dim3(N), dim3(kWave), 0, s, a);
+        hipLaunchKernelGGL(k_eq_neighbor_backward, dim3(N), dim3(kWave), sizeof(float) * w.NG,
+                           s, a);
         RUNE_HIP_CHECK(hipGetLastError());
         if (E > 0) {
             Epilogue e2;
             e2.dact_from = p.at(bb.ue);
             e2.ldu = D;
             e2.dact = act;
-            gemm(int(E), D, w.NG, p.at(p.t_dgv), w.NG, w.gate, D, p.at(p.t_due), D, e2, s);
+            gemm(int(E), D, w.NG, p.at(p.t_dgv), w.NG, w.gate_T, w.NG, p.at(p.t_due), D, e2, s);
             Epilogue e3;
-            gemm(int(E), w.KX, D, p.at(p.t_due), D, w.edge_x, w.KX, p.at(p.t_dx), a.ldx, e3, s);
+            gemm(int(E), w.KX, D, p.at(p.t_due), D, w.edge_xT, D, p.at(p.t_dx), a.ldx, e3, s);
             edge_rb_backward(m, p, r, p.at(p.t_dx), a.ldx, s);
         }
-        hipLaunchKernelGGL(k_eq_atom_backward, dim3(N), dim3(kWave), 0, s, a);
-        hipLaunchKernelGGL(k_eq_probe_dy, dim3(N), dim3(kWave), sizeof(float) * CN, s, a);
+        const int LC = lq * C;
+        hipLaunchKernelGGL(k_eq_atom_backward, dim3(N), dim3(kWave),
+                           sizeof(float) * (LC + nq + CN), s, a);
+        hipLaunchKernelGGL(k_eq_probe_dy, dim3(N), dim3(kWave), sizeof(float) * (2 * CN + 2 * LC),
+                           s, a);
         RUNE_HIP_CHECK(hipGetLastError());
         Epilogue e4;
-        gemm(N, H, w.NP, p.at(p.t_dvs), w.NP, w.node_f, H, p.at(p.t_dz), H, e4, s);
+        gemm(N, H, w.NP, p.at(p.t_dvs), w.NP, w.node_fT, w.NP, p.at(p.t_dz), H, e4, s);
         float *next = (cur == p.at(p.t_dh0)) ? p.at(p.t_dh1) : p.at(p.t_dh0);
         rms_backward(N, H, p.block_input[b], H, p.at(bb.rin), p.at(p.t_dz), H, cur, H, next, H, s);
         cur = next;

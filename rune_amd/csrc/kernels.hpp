@@ -93,8 +93,8 @@ struct Epilogue {
     int ldu = 0;
     int dact = -1;                      // activation whose derivative is used
 };
-// C[M,N] = A[M,K] B[K,N] (+ epilogue); row-major with leading dimensions.
-void gemm(int M, int N, int K, const float *A, int lda, const float *B, int ldb, float *C,
+// C[M,N] = A[M,K] Bt[N,K]^T (+ epilogue); row-major with leading dimensions.
+void gemm(int M, int N, int K, const float *A, int lda, const float *Bt, int ldb, float *C,
           int ldc, const Epilogue &ep, hipStream_t s);
 // inv_rms[m] = rsqrt(mean_n x[m,n]^2 + eps)
 void row_inv_rms(int M, int N, const float *x, int ldx, float eps, float *inv_rms, hipStream_t s);

@@ -455,7 +455,7 @@ void pack_messages(ModelImpl &m, Packer &pk, std::map<std::string, size_t> &off)
         off[p + "node_fT"] = pk.put(transpose(node, NP, H));
         const auto &we = m.tensor(p + "edge_mlp.0.weight");                   // [D, K]
         std::vector<float> wx = columns(we, D, K, 0, kb);
-        off[p + "edge_x"] = pk.put(wx);
+        off[p + "edge_x"] = pk.put(pad_rows(wx, D, kb));
         off[p + "edge_xT"] = pk.put(transpose(wx, D, kb));
         off[p + "pair_proj"] = pk.put(pair_projection(m.tensor(p + "pair_embedding.weight"), we,
                                                       m.tensor(p + "edge_mlp.0.bias"), T * T, P,
@@ -499,6 +499,7 @@ void bind_messages(ModelImpl &m, const PackedLookup &P) {
         w.NP = c.hidden_dim + c.vector_channels;
         w.NG = c.message_groups + c.vector_channels;
         w.KX = c.message_basis_size;
+        w.ld_edge_x = (w.KX + 3) & ~3;
         w.node_f = P(p + "node_f");
         w.node_fT = P(p + "node_fT");
         w.edge_x = P(p + "edge_x");
@@ -661,7 +662,7 @@ float *messages_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Recor
         row_inv_rms(N, H, cur, H, float(c.norm_eps), p.at(bb.rin), s);
         Epilogue e0;
         e0.row_scale = p.at(bb.rin);
-        gemm(N, w.NP, H, cur, H, w.node_fT, w.NP, p.at(bb.vs), w.NP, e0, s);
+        gemm(N, w.NP, H, cur, H, w.node_f, H, p.at(bb.vs), w.NP, e0, s);
         if (E > 0) {
             Epilogue e1;
             e1.gtab[0] = w.pair_proj;
@@ -670,10 +671,11 @@ float *messages_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Recor
             e1.pre = p.at(bb.ue);
             e1.ldp = D;
             e1.act = act;
-            gemm(int(E), D, w.KX, p.at(p.i_rb), p.ldrb, w.edge_xT, D, p.at(bb.eh), D, e1, s);
+            gemm(int(E), D, w.KX, p.at(p.i_rb), p.ldrb, w.edge_x, w.ld_edge_x, p.at(bb.eh), D, e1,
+                 s);
             Epilogue e2;
             e2.bias = w.gate_b;
-            gemm(int(E), w.NG, D, p.at(bb.eh), D, w.gate_T, w.NG, p.at(bb.gv), w.NG, e2, s);
+            gemm(int(E), w.NG, D, p.at(bb.eh), D, w.gate, D, p.at(bb.gv), w.NG, e2, s);
         }
         MpArgs a = mp_args(m, p, r, b);
         hipLaunchKernelGGL(k_mp_aggregate, dim3(N), dim3(kWave), 0, s, a);
@@ -683,12 +685,12 @@ float *messages_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Recor
         e3.pre = p.at(bb.u1);
         e3.ldp = D;
         e3.act = act;
-        gemm(N, D, w.NP, p.at(bb.uin), w.NP, w.up1_fT, D, p.at(bb.z1), D, e3, s);
+        gemm(N, D, w.NP, p.at(bb.uin), w.NP, w.up1_f, w.NP, p.at(bb.z1), D, e3, s);
         Epilogue e4;
         e4.bias = w.up2_b;
         e4.residual = cur;
         e4.ldr = H;
-        gemm(N, H, D, p.at(bb.z1), D, w.up2_T, H, p.at(bb.h_out), H, e4, s);
+        gemm(N, H, D, p.at(bb.z1), D, w.up2, D, p.at(bb.h_out), H, e4, s);
         p.block_input.push_back(cur);
         cur = p.at(bb.h_out);
     }
@@ -712,9 +714,9 @@ float *messages_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Reco
         e0.dact_from = p.at(bb.u1);
         e0.ldu = D;
         e0.dact = act;
-        gemm(N, D, H, cur, H, w.up2, D, p.at(p.t_dz1), D, e0, s);
+        gemm(N, D, H, cur, H, w.up2_T, H, p.at(p.t_dz1), D, e0, s);
         Epilogue e1;
-        gemm(N, w.NP, D, p.at(p.t_dz1), D, w.up1_f, w.NP, p.at(p.t_duin), w.NP, e1, s);
+        gemm(N, w.NP, D, p.at(p.t_dz1), D, w.up1_fT, D, p.at(p.t_duin), w.NP, e1, s);
         MpArgs a = mp_args(m, p, r, b);
         hipLaunchKernelGGL(k_mp_node_backward, dim3(N), dim3(kWave), 0, s, a);
         size_t lds = sizeof(float) * (H + 3 * std::max(c.vector_channels, 1));
@@ -726,13 +728,13 @@ float *messages_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Reco
             e2.dact_from = p.at(bb.ue);
             e2.ldu = D;
             e2.dact = act;
-            gemm(int(E), D, w.NG, p.at(p.t_dgv), w.NG, w.gate, D, p.at(p.t_due), D, e2, s);
+            gemm(int(E), D, w.NG, p.at(p.t_dgv), w.NG, w.gate_T, w.NG, p.at(p.t_due), D, e2, s);
             Epilogue e3;
-            gemm(int(E), w.KX, D, p.at(p.t_due), D, w.edge_x, w.KX, p.at(p.t_drb), p.ldrb, e3, s);
+            gemm(int(E), w.KX, D, p.at(p.t_due), D, w.edge_xT, D, p.at(p.t_drb), p.ldrb, e3, s);
             edge_rb_backward(m, p, r, p.at(p.t_drb), p.ldrb, s);
         }
         Epilogue e4;
-        gemm(N, H, w.NP, p.at(p.t_dvs), w.NP, w.node_f, H, p.at(p.t_dz), H, e4, s);
+        gemm(N, H, w.NP, p.at(p.t_dvs), w.NP, w.node_fT, w.NP, p.at(p.t_dz), H, e4, s);
         float *next = (cur == p.at(p.t_dh0)) ? p.at(p.t_dh1) : p.at(p.t_dh0);
         rms_backward(N, H, hin, H, p.at(bb.rin), p.at(p.t_dz), H, cur, H, next, H, s);
         cur = next;

@@ -144,6 +144,14 @@ std::vector<float> transpose(const std::vector<float> &w, int rows, int cols) {
     return t;
 }
 
+std::vector<float> pad_rows(const std::vector<float> &w, int rows, int cols) {
+    const int ld = (cols + 3) & ~3;
+    std::vector<float> t(size_t(rows) * ld, 0.0f);
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c) t[size_t(r) * ld + c] = w[size_t(r) * cols + c];
+    return t;
+}
+
 static void pack_descriptor(ModelImpl &m, Packer &pk, std::map<std::string, size_t> &off) {
     const rune_model_config &c = m.cfg;
     off["c_radial"] = pk.put(m.tensor("descriptor.radial.c_table"));
@@ -482,7 +490,7 @@ float *local_forward(ModelImpl &m, LocalPlan &p, int N, const float *q, int ldq,
     e0.emb = m.emb;
     e0.types = types;
     e0.ld_emb = H;
-    gemm(N, H, m.Q, q, ldq, m.in_wT, H, p.h, H, e0, s);
+    gemm(N, H, m.Q, q, ldq, m.in_w, m.Q, p.h, H, e0, s);
     for (int b = 0; b < nb; ++b) {
         float *hb = p.h + size_t(b) * N * H;
         float *hn = p.h + size_t(b + 1) * N * H;
@@ -495,12 +503,12 @@ float *local_forward(ModelImpl &m, LocalPlan &p, int N, const float *q, int ldq,
         e1.pre = ub;
         e1.ldp = F;
         e1.act = act;
-        gemm(N, F, H, hb, H, m.res[b].w1T, F, p.a, F, e1, s);
+        gemm(N, F, H, hb, H, m.res[b].w1, H, p.a, F, e1, s);
         Epilogue e2;
         e2.bias = m.res[b].b2;
         e2.residual = hb;
         e2.ldr = H;
-        gemm(N, H, F, p.a, F, m.res[b].w2T, H, hn, H, e2, s);
+        gemm(N, H, F, p.a, F, m.res[b].w2, F, hn, H, e2, s);
     }
     return p.h + size_t(nb) * N * H;
 }
@@ -518,14 +526,14 @@ void local_backward(ModelImpl &m, LocalPlan &p, int N, float *dh, float *dq, int
         e1.dact_from = ub;
         e1.ldu = F;
         e1.dact = act;
-        gemm(N, F, H, cur, H, m.res[b].w2, F, p.a, F, e1, s);       // du
+        gemm(N, F, H, cur, H, m.res[b].w2T, H, p.a, F, e1, s);      // du
         Epilogue e2;
-        gemm(N, H, F, p.a, F, m.res[b].w1, H, p.dz, H, e2, s);      // dz
+        gemm(N, H, F, p.a, F, m.res[b].w1T, F, p.dz, H, e2, s);     // dz
         rms_backward(N, H, hb, H, rb, p.dz, H, cur, H, other, H, s);
         std::swap(cur, other);
     }
     Epilogue e3;
-    gemm(N, m.Q, H, cur, H, m.in_w, m.Q, dq, ldq, e3, s);
+    gemm(N, m.Q, H, cur, H, m.in_wT, H, dq, ldq, e3, s);
 }
 
 }  // namespace rune

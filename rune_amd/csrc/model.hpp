@@ -20,22 +20,25 @@ struct Packer {
 };
 
 std::vector<float> transpose(const std::vector<float> &w, int rows, int cols);
+// W [rows, cols] -> [rows, (cols + 3) & ~3], zero columns appended (16-byte rows).
+std::vector<float> pad_rows(const std::vector<float> &w, int rows, int cols);
 
 struct ResidualWeights {
     const float *w1, *w1T, *b1, *w2, *w2T, *b2;
 };
 
 // Weights of one message block (MP: message.py, EQ: equivariant.py), packed.
-// "f" = RMSNorm weight folded into the columns; "T" = transposed copy used as
-// the B operand of the forward GEMM (the untransposed copy serves the reverse).
+// "f" = RMSNorm weight folded into the columns.  The GEMM takes its weight
+// operand as Bt[N, K] (K contiguous): the [out, in] copy serves the forward
+// products and the "T" (transposed, [in, out]) copy the reverse ones.
 struct MessageWeights {
     // node projections of RMSNorm(h):  MP [values | vector source],
     // EQ [W_e,c C_c | W_e,n C_n | values]
     const float *node_fT, *node_f;    // [H, NP], [NP, H]
     int NP;
     // edge MLP on per-edge features: MP [radial basis], EQ [radial basis | probes]
-    const float *edge_xT, *edge_x;    // [KX, D], [D, KX]
-    int KX;
+    const float *edge_xT, *edge_x;    // [KX, D], [D, ld_edge_x]
+    int KX, ld_edge_x;
     const float *pair_proj;           // [T*T, D] = pair_embedding W_pair^T + b
     // gates from the edge hidden state: MP [groups | vector], EQ [groups | directions]
     const float *gate_T, *gate, *gate_b;   // [D, NG], [NG, D], [NG]
