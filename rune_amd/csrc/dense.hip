@@ -9,9 +9,9 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-// GEMM tiling: 4 waves in 2x2, each wave (16*kWM) x (16*WN) of the output;
-// block tile kBM x (32*WN); K advances kBK = 32 per LDS stage.
-constexpr int kWM = 2, kBM = 32 * kWM, kBK = 32, kLdk = kBK + 4;
+// GEMM tiling: 4 waves in 2x2, each wave (16*WM) x (16*WN) of the output;
+// block tile (32*WM) x (32*WN); K advances kBK = 32 per LDS stage.
+constexpr int kBK = 32, kLdk = kBK + 4;
 
 __device__ inline float act_f(int a, float x) {
     if (a == RUNE_ACT_SILU) return x / (1.0f + expf(-x));
@@ -88,23 +88,23 @@ __device__ inline void store_stage(const float4 (&r)[kRows * 8 / 256], float *S,
 // each lane fetches its four steps with one 16-byte LDS read.  Row stride
 // kLdk = 36 floats keeps those reads free of bank conflicts.
 // Block b covers row tile b / nbn and column tile b % nbn.
-template <int WN, bool kVec>
+template <int WM, int WN, bool kVec>
 __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *__restrict__ A,
                                               int lda, const float *__restrict__ Bt, int ldb,
                                               float *__restrict__ C, int ldc, Epilogue ep,
                                               int nbn) {
-    constexpr int BN = 32 * WN, kLdo = BN + 4;
+    constexpr int kBM = 32 * WM, BN = 32 * WN, kLdo = BN + 4;
     static_assert(32 * kLdo <= (kBM + BN) * kLdk, "epilogue staging exceeds the tile LDS");
     __shared__ __attribute__((aligned(16))) float smem[(kBM + BN) * kLdk];
     float *As = smem, *Bs = smem + kBM * kLdk;
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int m0 = (blockIdx.x / nbn) * kBM, n0 = (blockIdx.x % nbn) * BN;
-    const int wm = (wave >> 1) * 16 * kWM, wn = (wave & 1) * 16 * WN;
+    const int wm = (wave >> 1) * 16 * WM, wn = (wave & 1) * 16 * WN;
     const int g = lane >> 4, rr = lane & 15;
-    floatx4 acc[kWM][WN];
+    floatx4 acc[WM][WN];
 #pragma unroll
-    for (int a = 0; a < kWM; ++a)
+    for (int a = 0; a < WM; ++a)
 #pragma unroll
         for (int b = 0; b < WN; ++b) acc[a][b] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     float4 ra[kBM * 8 / 256], rb[BN * 8 / 256];
@@ -120,9 +120,9 @@ __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *
         }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            float4 fa[kWM], fb[WN];
+            float4 fa[WM], fb[WN];
 #pragma unroll
-            for (int a = 0; a < kWM; ++a)
+            for (int a = 0; a < WM; ++a)
                 fa[a] = *reinterpret_cast<const float4 *>(As + (wm + 16 * a + rr) * kLdk +
                                                           16 * h + 4 * g);
 #pragma unroll
@@ -130,7 +130,7 @@ __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *
                 fb[b] = *reinterpret_cast<const float4 *>(Bs + (wn + 16 * b + rr) * kLdk +
                                                           16 * h + 4 * g);
 #pragma unroll
-            for (int a = 0; a < kWM; ++a)
+            for (int a = 0; a < WM; ++a)
 #pragma unroll
                 for (int b = 0; b < WN; ++b) {
                     acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a].x, fb[b].x, acc[a][b], 0, 0, 0);
@@ -141,41 +141,92 @@ __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *
         }
         __syncthreads();
     }
-    // Epilogue through LDS, one 32-row half of the tile at a time: the waves
-    // owning the half store their accumulators (row stride kLdo = BN + 4 puts
-    // the four lane groups on distinct banks), then all 256 threads apply the
-    // epilogue row-contiguously.
+    // Epilogue through LDS, 32 rows of the tile at a time: the waves owning
+    // those rows store their accumulators (row stride kLdo = BN + 4 puts
+    // the four lane groups on distinct banks); the rows' own data goes to
+    // LDS; then all 256 threads apply the epilogue row-contiguously, kB
+    // elements per thread at once so that each term's loads are issued
+    // together.  Out-of-range elements load from clamped indices and store
+    // nothing.
+    constexpr int kE = 32 * BN / 256;
+    constexpr int kB = kE % 12 == 0 ? 12 : kE % 10 == 0 ? 10 : kE % 8 == 0 ? 8 : 4;
+    static_assert(kE % kB == 0, "epilogue batch must divide the per-thread count");
+    __shared__ float s_rs[32];
+    __shared__ int s_ix[4][32];
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        if ((wave >> 1) == half) {
+    for (int part = 0; part < kBM / 32; ++part) {
+        // accumulator row block a of this wave is 16-row block blk of the tile
 #pragma unroll
-            for (int a = 0; a < kWM; ++a)
+        for (int a = 0; a < WM; ++a) {
+            const int blk = (wave >> 1) * WM + a;
+            if ((blk >> 1) == part) {
 #pragma unroll
                 for (int b = 0; b < WN; ++b)
 #pragma unroll
                     for (int v = 0; v < 4; ++v)
-                        smem[(16 * a + 4 * g + v) * kLdo + wn + 16 * b + rr] = acc[a][b][v];
+                        smem[(16 * (blk & 1) + 4 * g + v) * kLdo + wn + 16 * b + rr] =
+                            acc[a][b][v];
+            }
+        }
+        if (tid < 32) {
+            int row = min(m0 + 32 * part + tid, M - 1);
+            s_rs[tid] = ep.row_scale ? ep.row_scale[row] : 1.0f;
+            s_ix[0][tid] = ep.emb ? ep.types[row] : 0;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) s_ix[1 + k][tid] = ep.gtab[k] ? ep.gidx[k][row] : 0;
         }
         __syncthreads();
-        for (int idx = tid; idx < 32 * BN; idx += 256) {
-            int lr = idx / BN, lc = idx - lr * BN;
-            int row = m0 + 32 * half + lr, col = n0 + lc;
-            if (row >= M || col >= N) continue;
-            float x = smem[lr * kLdo + lc];
-            if (ep.row_scale) x *= ep.row_scale[row];
-            if (ep.bias) x += ep.bias[col];
-            if (ep.emb) x += ep.emb[size_t(ep.types[row]) * ep.ld_emb + col];
-            if (ep.residual) x += ep.residual[size_t(row) * ep.ldr + col];
+        for (int j0 = 0; j0 < kE; j0 += kB) {
+            float x[kB], du[kB];
+            int lr[kB], cc[kB], rc[kB];
 #pragma unroll
-            for (int k = 0; k < 3; ++k)
-                if (ep.gtab[k]) x += ep.gtab[k][size_t(ep.gidx[k][row]) * ep.gld[k] + col];
-            if (ep.pre) ep.pre[size_t(row) * ep.ldp + col] = x;
-            if (ep.act_split >= 0 && col >= ep.act_split)
-                x = act_f(ep.act2, x);
-            else if (ep.act >= 0)
-                x = act_f(ep.act, x);
-            if (ep.dact_from) x *= act_d(ep.dact, ep.dact_from[size_t(row) * ep.ldu + col]);
-            C[size_t(row) * ldc + col] = x;
+            for (int u = 0; u < kB; ++u) {
+                int idx = tid + 256 * (j0 + u);
+                lr[u] = idx / BN;
+                int lc = idx - lr[u] * BN;
+                cc[u] = min(n0 + lc, N - 1);
+                rc[u] = min(m0 + 32 * part + lr[u], M - 1);
+                x[u] = smem[lr[u] * kLdo + lc] * s_rs[lr[u]];
+            }
+            if (ep.bias) {
+#pragma unroll
+                for (int u = 0; u < kB; ++u) x[u] += ep.bias[cc[u]];
+            }
+            if (ep.emb) {
+#pragma unroll
+                for (int u = 0; u < kB; ++u)
+                    x[u] += ep.emb[size_t(s_ix[0][lr[u]]) * ep.ld_emb + cc[u]];
+            }
+            if (ep.residual) {
+#pragma unroll
+                for (int u = 0; u < kB; ++u) x[u] += ep.residual[size_t(rc[u]) * ep.ldr + cc[u]];
+            }
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+                if (ep.gtab[k]) {
+#pragma unroll
+                    for (int u = 0; u < kB; ++u)
+                        x[u] += ep.gtab[k][size_t(s_ix[1 + k][lr[u]]) * ep.gld[k] + cc[u]];
+                }
+            }
+            if (ep.dact_from) {
+#pragma unroll
+                for (int u = 0; u < kB; ++u) du[u] = ep.dact_from[size_t(rc[u]) * ep.ldu + cc[u]];
+            }
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                int idx = tid + 256 * (j0 + u);
+                int row = m0 + 32 * part + lr[u], col = n0 + idx - lr[u] * BN;
+                if (row >= M || col >= N) continue;
+                float v = x[u];
+                if (ep.pre) ep.pre[size_t(row) * ep.ldp + col] = v;
+                if (ep.act_split >= 0 && col >= ep.act_split)
+                    v = act_f(ep.act2, v);
+                else if (ep.act >= 0)
+                    v = act_f(ep.act, v);
+                if (ep.dact_from) v *= act_d(ep.dact, du[u]);
+                C[size_t(row) * ldc + col] = v;
+            }
         }
         __syncthreads();
     }
@@ -286,18 +337,18 @@ static int pick_wn(int N) {
     return best;
 }
 
-template <int WN>
+template <int WM, int WN>
 static void launch_gemm(bool vec, int M, int N, int K, const float *A, int lda, const float *Bt,
                         int ldb, float *C, int ldc, const Epilogue &ep, hipStream_t s) {
     int nbn = ceil_div(N, 32 * WN);
-    int64_t blocks = int64_t(ceil_div(M, kBM)) * nbn;
+    int64_t blocks = int64_t(ceil_div(M, 32 * WM)) * nbn;
     if (blocks > 0x7fffffff) throw Error(RUNE_ERR_ARGUMENT, "gemm: problem too large");
     if (vec)
-        hipLaunchKernelGGL((k_gemm<WN, true>), dim3(unsigned(blocks)), dim3(256), 0, s, M, N, K,
-                           A, lda, Bt, ldb, C, ldc, ep, nbn);
-    else
-        hipLaunchKernelGGL((k_gemm<WN, false>), dim3(unsigned(blocks)), dim3(256), 0, s, M, N,
+        hipLaunchKernelGGL((k_gemm<WM, WN, true>), dim3(unsigned(blocks)), dim3(256), 0, s, M, N,
                            K, A, lda, Bt, ldb, C, ldc, ep, nbn);
+    else
+        hipLaunchKernelGGL((k_gemm<WM, WN, false>), dim3(unsigned(blocks)), dim3(256), 0, s, M,
+                           N, K, A, lda, Bt, ldb, C, ldc, ep, nbn);
 }
 
 void gemm(int M, int N, int K, const float *A, int lda, const float *Bt, int ldb, float *C,
@@ -306,10 +357,10 @@ void gemm(int M, int N, int K, const float *A, int lda, const float *Bt, int ldb
     bool vec = lda % 4 == 0 && ldb % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
                (reinterpret_cast<uintptr_t>(Bt) & 15) == 0;
     switch (pick_wn(N)) {
-    case 9: launch_gemm<9>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s); break;
-    case 6: launch_gemm<6>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s); break;
-    case 4: launch_gemm<4>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s); break;
-    default: launch_gemm<2>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s); break;
+    case 9: launch_gemm<2, 9>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s); break;
+    case 6: launch_gemm<2, 6>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s); break;
+    case 4: launch_gemm<2, 4>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s); break;
+    default: launch_gemm<2, 2>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s); break;
     }
     RUNE_HIP_CHECK(hipGetLastError());
 }
