@@ -90,6 +90,19 @@ __global__ void __launch_bounds__(kWave) k_eq_mix(const float *mixw, const float
     }
 }
 
+// Per-edge loops.  Each kernel walks the records of one atom in chunks of 64:
+// the chunk's record metadata (neighbour / centre index, cutoff value) is read
+// lane-parallel once and broadcast per record with readlane, and the rows of
+// the next record are fetched into registers while the current one is
+// processed, so no record waits on a chain of dependent loads.
+__device__ inline int lane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ inline float lane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+constexpr int kMaxG = 9;     // NG <= 64 + 2 * 256 gate columns, 9 per lane
+constexpr int kMaxY = 1;     // nq <= 64 harmonic components, 1 per lane
+
 // Edge features [rb | probes_c | probes_n] of the radial records of centre i.
 __global__ void __launch_bounds__(kWave) k_eq_features(EqArgs a) {
     extern __shared__ float lds[];
@@ -99,47 +112,75 @@ __global__ void __launch_bounds__(kWave) k_eq_features(EqArgs a) {
     float *Hj = Hi + C * ldc; // [C][ldc] neighbour state of the current record
     float *Yl = Hj + C * ldc; // [nq]
     const int i = blockIdx.x, lane = threadIdx.x;
-    for (int o = lane; o < CN; o += kWave)
-        Hi[(o / nq) * ldc + o % nq] = a.dir_in[size_t(i) * CN + o];
+    int so[kMaxOut];
+#pragma unroll
+    for (int t = 0; t < kMaxOut; ++t) {
+        int o = lane + kWave * t;
+        so[t] = o < CN ? (o / nq) * ldc + o % nq : -1;
+        if (so[t] >= 0) Hi[so[t]] = a.dir_in[size_t(i) * CN + o];
+    }
+    float hn[kMaxOut], yn = 0.0f, rn = 0.0f;
+    auto fetch = [&](int e, int j) {
+#pragma unroll
+        for (int t = 0; t < kMaxOut; ++t)
+            hn[t] = so[t] >= 0 ? a.dir_in[size_t(j) * CN + lane + kWave * t] : 0.0f;
+        yn = lane < nq ? a.harm[size_t(e) * nq + lane] : 0.0f;
+        rn = lane < a.kb ? a.rb[size_t(e) * a.ldrb + lane] : 0.0f;
+    };
     const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
-    for (int e = rb; e < re; ++e) {
-        float *x = a.x + size_t(e) * a.ldx;
-        float fc = a.fc[e];
-        if (fc == 0.0f) {
-            for (int k = lane; k < a.KX; k += kWave) x[k] = 0.0f;
-            continue;
+    for (int c0 = rb; c0 < re; c0 += kWave) {
+        const int cnt = min(kWave, re - c0);
+        int mj = 0;
+        float mf = 0.0f;
+        if (lane < cnt) {
+            mj = a.r.nbr[c0 + lane];
+            mf = a.fc[c0 + lane];
         }
-        const float *hj = a.dir_in + size_t(a.r.nbr[e]) * CN;
-        for (int o = lane; o < CN; o += kWave) Hj[(o / nq) * ldc + o % nq] = hj[o];
-        if (lane < nq) Yl[lane] = a.harm[size_t(e) * nq + lane];
-        if (lane < a.kb) x[lane] = a.rb[size_t(e) * a.ldrb + lane];
-        __syncthreads();
-        for (int p = lane; p < LC; p += kWave) {
-            int L = p / C + 1, c = p - (L - 1) * C, st = L * L - 1;
-            float pc = 0.0f, pn = 0.0f;
-            for (int m = 0; m < 2 * L + 1; ++m) {
-                pc += Hi[c * ldc + st + m] * Yl[st + m];
-                pn += Hj[c * ldc + st + m] * Yl[st + m];
+        fetch(c0, lane_i(mj, 0));
+        for (int u = 0; u < cnt; ++u) {
+            const int e = c0 + u;
+            const float fc = lane_f(mf, u);
+            __syncthreads();
+#pragma unroll
+            for (int t = 0; t < kMaxOut; ++t)
+                if (so[t] >= 0) Hj[so[t]] = hn[t];
+            if (lane < nq) Yl[lane] = yn;
+            const float rcur = rn;
+            __syncthreads();
+            if (u + 1 < cnt) fetch(e + 1, lane_i(mj, u + 1));
+            float *x = a.x + size_t(e) * a.ldx;
+            if (fc == 0.0f) {
+                for (int k = lane; k < a.KX; k += kWave) x[k] = 0.0f;
+                continue;
             }
-            x[a.kb + p] = pc;
-            x[a.kb + LC + p] = (L & 1) ? -pn : pn;
+            if (lane < a.kb) x[lane] = rcur;
+            for (int p = lane; p < LC; p += kWave) {
+                int L = p / C + 1, c = p - (L - 1) * C, st = L * L - 1;
+                float pc = 0.0f, pn = 0.0f;
+                for (int m = 0; m < 2 * L + 1; ++m) {
+                    pc += Hi[c * ldc + st + m] * Yl[st + m];
+                    pn += Hj[c * ldc + st + m] * Yl[st + m];
+                }
+                x[a.kb + p] = pc;
+                x[a.kb + LC + p] = (L & 1) ? -pn : pn;
+            }
         }
-        __syncthreads();
     }
 }
 
+// Messages and transported / injected direction states of centre i, then the
+// update input [RMSNorm(msg) | per-(L, c) squared norms of dir_out].
 __global__ void __launch_bounds__(kWave) k_eq_aggregate(EqArgs a) {
     extern __shared__ float lds[];
     const int H = a.H, G = a.G, C = a.C, nq = a.nq, lq = a.lq, gw = H / G, LC = lq * C;
-    const int CN = C * nq;
+    const int CN = C * nq, NG = a.NG;
     float *Ho = lds;          // [CN]
     float *gL = Ho + CN;      // [NG] gates of the current record
-    float *Yl = gL + a.NG;    // [nq]
+    float *Yl = gL + NG;      // [nq]
     const int i = blockIdx.x, lane = threadIdx.x;
     float macc[4] = {0, 0, 0, 0};
     float dacc[kMaxOut];
-    int gT[kMaxOut];
-    int kk[kMaxOut];
+    int gT[kMaxOut], kk[kMaxOut];
 #pragma unroll
     for (int t = 0; t < kMaxOut; ++t) {
         dacc[t] = 0.0f;
@@ -148,30 +189,64 @@ __global__ void __launch_bounds__(kWave) k_eq_aggregate(EqArgs a) {
         kk[t] = k;
         gT[t] = o < CN ? G + (order_of(k) - 1) * C + c : 0;
     }
-    const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
-    for (int e = rb; e < re; ++e) {
-        float fc = a.fc[e];
-        if (fc == 0.0f) continue;
-        int j = a.r.nbr[e];
-        const float *gl = a.ag + size_t(e) * a.NG;
-        for (int k = lane; k < a.NG; k += kWave) gL[k] = gl[k];
-        if (lane < nq) Yl[lane] = a.harm[size_t(e) * nq + lane];
-        __syncthreads();
+    float gn[kMaxG], vn[4], mxn[kMaxOut], yn = 0.0f;
+    auto fetch = [&](int e, int j) {
+#pragma unroll
+        for (int q = 0; q < kMaxG; ++q) {
+            int k = lane + kWave * q;
+            gn[q] = k < NG ? a.ag[size_t(e) * NG + k] : 0.0f;
+        }
+        yn = lane < nq ? a.harm[size_t(e) * nq + lane] : 0.0f;
         const float *V = a.node + size_t(j) * a.NP + 2 * a.D;
-        const float *MX = a.mixst + size_t(j) * CN;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             int c = lane + kWave * t;
-            if (c < H) macc[t] += gL[c / gw] * fc * V[c];
+            vn[t] = c < H ? V[c] : 0.0f;
         }
 #pragma unroll
         for (int t = 0; t < kMaxOut; ++t) {
             int o = lane + kWave * t;
-            if (o < CN)
-                dacc[t] += fc * (gL[gT[t]] * MX[o] + gL[gT[t] + LC] * Yl[kk[t]]);
+            mxn[t] = o < CN ? a.mixst[size_t(j) * CN + o] : 0.0f;
         }
-        __syncthreads();
+    };
+    const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
+    for (int c0 = rb; c0 < re; c0 += kWave) {
+        const int cnt = min(kWave, re - c0);
+        int mj = 0;
+        float mf = 0.0f;
+        if (lane < cnt) {
+            mj = a.r.nbr[c0 + lane];
+            mf = a.fc[c0 + lane];
+        }
+        fetch(c0, lane_i(mj, 0));
+        for (int u = 0; u < cnt; ++u) {
+            const float fc = lane_f(mf, u);
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < kMaxG; ++q)
+                if (lane + kWave * q < NG) gL[lane + kWave * q] = gn[q];
+            if (lane < nq) Yl[lane] = yn;
+            float vc[4], mx[kMaxOut];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) vc[t] = vn[t];
+#pragma unroll
+            for (int t = 0; t < kMaxOut; ++t) mx[t] = mxn[t];
+            __syncthreads();
+            if (u + 1 < cnt) fetch(c0 + u + 1, lane_i(mj, u + 1));
+            if (fc == 0.0f) continue;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                int c = lane + kWave * t;
+                if (c < H) macc[t] += gL[c / gw] * fc * vc[t];
+            }
+#pragma unroll
+            for (int t = 0; t < kMaxOut; ++t) {
+                int o = lane + kWave * t;
+                if (o < CN) dacc[t] += fc * (gL[gT[t]] * mx[t] + gL[gT[t] + LC] * Yl[kk[t]]);
+            }
+        }
     }
+    __syncthreads();
 #pragma unroll
     for (int t = 0; t < kMaxOut; ++t) {
         int o = lane + kWave * t;
@@ -227,28 +302,23 @@ __global__ void __launch_bounds__(kWave) k_eq_node_backward(EqArgs a) {
     }
 }
 
-// Gate adjoints, dE/dY (injection) and dE/dfc for the records of centre i.
+// Gate adjoints and dE/dfc for the records of centre i.
 __global__ void __launch_bounds__(kWave) k_eq_edge_backward(EqArgs a) {
     extern __shared__ float lds[];
     const int H = a.H, G = a.G, C = a.C, nq = a.nq, lq = a.lq, gw = H / G, LC = lq * C;
-    const int CN = C * nq, ldc = nq | 1;   // odd row stride: conflict-free channel reads
-    float *pT = lds;             // [C][ldc] dHt_i * mixed_j
-    float *pI = pT + C * ldc;    // [C][ldc] dHt_i * Y
-    float *term = pI + C * ldc;  // [C][ldc] tanh(injection) * dHt_i
-    float *pL = term + C * ldc;  // [H]
+    const int CN = C * nq, NG = a.NG, ldc = nq | 1;
+    float *DH = lds;             // [C][ldc] dE/d(dir_out) of centre i
+    float *MX = DH + C * ldc;    // [C][ldc] mixed state of the current neighbour
+    float *pL = MX + C * ldc;    // [H] dmsg_i * V_j
     float *gL = pL + H;          // [NG]
-    float *YL = gL + a.NG;       // [nq]
+    float *YL = gL + NG;         // [nq]
     const int i = blockIdx.x, lane = threadIdx.x;
-    float dh[kMaxOut];
-    int gI[kMaxOut], kk[kMaxOut], so[kMaxOut];
+    int so[kMaxOut];
 #pragma unroll
     for (int t = 0; t < kMaxOut; ++t) {
         int o = lane + kWave * t;
-        int c = o / nq, k = o - c * nq;
-        kk[t] = k;
-        so[t] = c * ldc + k;
-        gI[t] = o < CN ? G + LC + (order_of(k) - 1) * C + c : 0;
-        dh[t] = o < CN ? a.dht[size_t(i) * CN + o] : 0.0f;
+        so[t] = o < CN ? (o / nq) * ldc + o % nq : -1;
+        if (so[t] >= 0) DH[so[t]] = a.dht[size_t(i) * CN + o];
     }
     float dm[4];
 #pragma unroll
@@ -256,68 +326,85 @@ __global__ void __launch_bounds__(kWave) k_eq_edge_backward(EqArgs a) {
         int c = lane + kWave * t;
         dm[t] = c < H ? a.dmsg[size_t(i) * H + c] : 0.0f;
     }
-    const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
-    for (int e = rb; e < re; ++e) {
-        float fc = a.fc[e];
-        float *dg = a.dgg + size_t(e) * a.NG;
-        if (fc == 0.0f) {
-            for (int k = lane; k < a.NG; k += kWave) dg[k] = 0.0f;
-            continue;
+    float gn[kMaxG], vn[4], mxn[kMaxOut], yn = 0.0f;
+    auto fetch = [&](int e, int j) {
+#pragma unroll
+        for (int q = 0; q < kMaxG; ++q) {
+            int k = lane + kWave * q;
+            gn[q] = k < NG ? a.ag[size_t(e) * NG + k] : 0.0f;
         }
-        int j = a.r.nbr[e];
-        const float *gl = a.ag + size_t(e) * a.NG;
+        yn = lane < nq ? a.harm[size_t(e) * nq + lane] : 0.0f;
         const float *V = a.node + size_t(j) * a.NP + 2 * a.D;
-        const float *MX = a.mixst + size_t(j) * CN;
-        for (int k = lane; k < a.NG; k += kWave) gL[k] = gl[k];
-        if (lane < nq) YL[lane] = a.harm[size_t(e) * nq + lane];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             int c = lane + kWave * t;
-            if (c < H) pL[c] = dm[t] * V[c];
+            vn[t] = c < H ? V[c] : 0.0f;
         }
-        __syncthreads();
 #pragma unroll
-        for (int t = 0; t < kMaxOut; ++t) {
-            int o = lane + kWave * t;
-            if (o < CN) {
-                pT[so[t]] = dh[t] * MX[o];
-                pI[so[t]] = dh[t] * YL[kk[t]];
-                term[so[t]] = gL[gI[t]] * dh[t];
+        for (int t = 0; t < kMaxOut; ++t)
+            mxn[t] = so[t] >= 0 ? a.mixst[size_t(j) * CN + lane + kWave * t] : 0.0f;
+    };
+    const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
+    for (int c0 = rb; c0 < re; c0 += kWave) {
+        const int cnt = min(kWave, re - c0);
+        int mj = 0;
+        float mf = 0.0f;
+        if (lane < cnt) {
+            mj = a.r.nbr[c0 + lane];
+            mf = a.fc[c0 + lane];
+        }
+        fetch(c0, lane_i(mj, 0));
+        for (int u = 0; u < cnt; ++u) {
+            const int e = c0 + u;
+            const float fc = lane_f(mf, u);
+            float *dg = a.dgg + size_t(e) * NG;
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < kMaxG; ++q)
+                if (lane + kWave * q < NG) gL[lane + kWave * q] = gn[q];
+            if (lane < nq) YL[lane] = yn;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                int c = lane + kWave * t;
+                if (c < H) pL[c] = dm[t] * vn[t];
+            }
+#pragma unroll
+            for (int t = 0; t < kMaxOut; ++t)
+                if (so[t] >= 0) MX[so[t]] = mxn[t];
+            __syncthreads();
+            if (u + 1 < cnt) fetch(e + 1, lane_i(mj, u + 1));
+            if (fc == 0.0f) {
+                for (int k = lane; k < NG; k += kWave) dg[k] = 0.0f;
+                continue;
+            }
+            float dfc = 0.0f;
+            for (int p = lane; p < LC; p += kWave) {
+                int L = p / C + 1, c = p - (L - 1) * C, st = L * L - 1;
+                float sT = 0.0f, sI = 0.0f;
+                for (int m = 0; m < 2 * L + 1; ++m) {
+                    float d = DH[c * ldc + st + m];
+                    sT += d * MX[c * ldc + st + m];
+                    sI += d * YL[st + m];
+                }
+                float tT = gL[G + p], tI = gL[G + LC + p];
+                dg[G + p] = (1.0f - tT * tT) * fc * sT;
+                dg[G + LC + p] = (1.0f - tI * tI) * fc * sI;
+                dfc += tT * sT + tI * sI;
+            }
+            if (lane < G) {
+                float P = 0.0f;
+                for (int c = lane * gw; c < (lane + 1) * gw; ++c) P += pL[c];
+                float s = gL[lane];
+                dg[lane] = P * fc * s * (1.0f - s);
+                dfc += P * s;
+            }
+            dfc = wave_sum(dfc);
+            if (lane == 0) {
+                float d = a.r.vec[e].w;
+                float fcp = -0.5f * kPi / a.cutoff * sinf(kPi * d / a.cutoff);
+                a.dv[e].w += dfc * fcp;
             }
         }
-        __syncthreads();
-        float dfc = 0.0f;
-        for (int p = lane; p < LC; p += kWave) {
-            int L = p / C + 1, c = p - (L - 1) * C, st = L * L - 1;
-            float sT = 0.0f, sI = 0.0f;
-            for (int m = 0; m < 2 * L + 1; ++m) {
-                sT += pT[c * ldc + st + m];
-                sI += pI[c * ldc + st + m];
-            }
-            float tT = gL[G + p], tI = gL[G + LC + p];
-            dg[G + p] = (1.0f - tT * tT) * fc * sT;
-            dg[G + LC + p] = (1.0f - tI * tI) * fc * sI;
-            dfc += tT * sT + tI * sI;
-        }
-        if (lane < G) {
-            float P = 0.0f;
-            for (int c = lane * gw; c < (lane + 1) * gw; ++c) P += pL[c];
-            float s = gL[lane];
-            dg[lane] = P * fc * s * (1.0f - s);
-            dfc += P * s;
-        }
-        if (lane < nq) {
-            float y = 0.0f;
-            for (int c = 0; c < C; ++c) y += term[c * ldc + lane];
-            a.dy[size_t(e) * nq + lane] += fc * y;
-        }
-        dfc = wave_sum(dfc);
-        if (lane == 0) {
-            float d = a.r.vec[e].w;
-            float fcp = -0.5f * kPi / a.cutoff * sinf(kPi * d / a.cutoff);
-            a.dv[e].w += dfc * fcp;
-        }
-        __syncthreads();
     }
 }
 
@@ -325,7 +412,7 @@ __global__ void __launch_bounds__(kWave) k_eq_edge_backward(EqArgs a) {
 __global__ void __launch_bounds__(kWave) k_eq_neighbor_backward(EqArgs a) {
     extern __shared__ float gL[];   // [NG] gates of the current record
     const int j = blockIdx.x, lane = threadIdx.x;
-    const int H = a.H, G = a.G, C = a.C, nq = a.nq, gw = H / G, CN = C * nq;
+    const int H = a.H, G = a.G, C = a.C, nq = a.nq, gw = H / G, CN = C * nq, NG = a.NG;
     float macc[kMaxOut];
     int gT[kMaxOut];
 #pragma unroll
@@ -336,26 +423,60 @@ __global__ void __launch_bounds__(kWave) k_eq_neighbor_backward(EqArgs a) {
         gT[t] = o < CN ? G + (order_of(k) - 1) * C + c : 0;
     }
     float vacc[4] = {0, 0, 0, 0};
-    for (int t = a.r.tptr[j]; t < a.r.tptr[j + 1]; ++t) {
-        int e = a.r.tidx[t];
-        float fc = a.fc[e];
-        if (fc == 0.0f) continue;
-        int i = a.r.ctr[e];
-        const float *gl = a.ag + size_t(e) * a.NG;
-        for (int k = lane; k < a.NG; k += kWave) gL[k] = gl[k];
-        __syncthreads();
-        const float *dh = a.dht + size_t(i) * CN;
+    float gn[kMaxG], dhn[kMaxOut], dmn[4];
+    auto fetch = [&](int e, int i) {
 #pragma unroll
-        for (int q = 0; q < kMaxOut; ++q) {
-            int o = lane + kWave * q;
-            if (o < CN) macc[q] += fc * gL[gT[q]] * dh[o];
+        for (int q = 0; q < kMaxG; ++q) {
+            int k = lane + kWave * q;
+            gn[q] = k < NG ? a.ag[size_t(e) * NG + k] : 0.0f;
         }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            int c = lane + kWave * q;
-            if (c < H) vacc[q] += gL[c / gw] * fc * a.dmsg[size_t(i) * H + c];
+        for (int t = 0; t < kMaxOut; ++t) {
+            int o = lane + kWave * t;
+            dhn[t] = o < CN ? a.dht[size_t(i) * CN + o] : 0.0f;
         }
-        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            int c = lane + kWave * t;
+            dmn[t] = c < H ? a.dmsg[size_t(i) * H + c] : 0.0f;
+        }
+    };
+    const int tb = a.r.tptr[j], te = a.r.tptr[j + 1];
+    for (int c0 = tb; c0 < te; c0 += kWave) {
+        const int cnt = min(kWave, te - c0);
+        int me = 0, mi = 0;
+        float mf = 0.0f;
+        if (lane < cnt) {
+            me = a.r.tidx[c0 + lane];
+            mi = a.r.ctr[me];
+            mf = a.fc[me];
+        }
+        fetch(lane_i(me, 0), lane_i(mi, 0));
+        for (int u = 0; u < cnt; ++u) {
+            const float fc = lane_f(mf, u);
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < kMaxG; ++q)
+                if (lane + kWave * q < NG) gL[lane + kWave * q] = gn[q];
+            float dh[kMaxOut], dmc[4];
+#pragma unroll
+            for (int t = 0; t < kMaxOut; ++t) dh[t] = dhn[t];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) dmc[t] = dmn[t];
+            __syncthreads();
+            if (u + 1 < cnt) fetch(lane_i(me, u + 1), lane_i(mi, u + 1));
+            if (fc == 0.0f) continue;
+#pragma unroll
+            for (int q = 0; q < kMaxOut; ++q) {
+                int o = lane + kWave * q;
+                if (o < CN) macc[q] += fc * gL[gT[q]] * dh[q];
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                int c = lane + kWave * q;
+                if (c < H) vacc[q] += gL[c / gw] * fc * dmc[q];
+            }
+        }
     }
 #pragma unroll
     for (int q = 0; q < kMaxOut; ++q) {
@@ -390,46 +511,58 @@ __global__ void __launch_bounds__(kWave) k_eq_atom_backward(EqArgs a) {
         col[t] = (L - 1) * C + c;
         g[t] = o < CN ? a.dht[size_t(n) * CN + o] : 0.0f;
     }
-    const int rb = a.r.view[4 * n], re = a.r.view[4 * n + 1];
-    // own records: dA, probes_c adjoint
-    for (int e = rb; e < re; ++e) {
-        if (a.fc[e] == 0.0f) continue;
-        const float *du = a.due + size_t(e) * D;
+    float dun[4], dxn[4], yn = 0.0f;
+    auto fetch = [&](int e, int off) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             int c = lane + kWave * q;
-            if (c < D) sa[q] += du[c];
+            dun[q] = c < D ? a.due[size_t(e) * D + c] : 0.0f;
+            dxn[q] = c < LC ? a.dx[size_t(e) * a.ldx + a.kb + off + c] : 0.0f;
         }
-        const float *dx = a.dx + size_t(e) * a.ldx + a.kb;
-        for (int p = lane; p < LC; p += kWave) dxL[p] = dx[p];
-        if (lane < nq) Yl[lane] = a.harm[size_t(e) * nq + lane];
-        __syncthreads();
-#pragma unroll
-        for (int t = 0; t < kMaxOut; ++t)
-            if (lane + kWave * t < CN) g[t] += dxL[col[t]] * Yl[kk[t]];
-        __syncthreads();
-    }
-    // records where n is the neighbour: dB, probes_n adjoint
-    for (int q2 = a.r.tptr[n]; q2 < a.r.tptr[n + 1]; ++q2) {
-        int e = a.r.tidx[q2];
-        if (a.fc[e] == 0.0f) continue;
-        const float *du = a.due + size_t(e) * D;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            int c = lane + kWave * q;
-            if (c < D) sb[q] += du[c];
-        }
-        const float *dx = a.dx + size_t(e) * a.ldx + a.kb + LC;
-        for (int p = lane; p < LC; p += kWave) dxL[p] = dx[p];
-        if (lane < nq) Yl[lane] = a.harm[size_t(e) * nq + lane];
-        __syncthreads();
-#pragma unroll
-        for (int t = 0; t < kMaxOut; ++t)
-            if (lane + kWave * t < CN) {
-                float v = dxL[col[t]] * Yl[kk[t]];
-                g[t] += (LL[t] & 1) ? -v : v;
+        yn = lane < nq ? a.harm[size_t(e) * nq + lane] : 0.0f;
+    };
+    // own records: dA, probes_c adjoint (sign +1); records as neighbour: dB,
+    // probes_n adjoint (sign (-1)^L)
+    for (int side = 0; side < 2; ++side) {
+        const int b0 = side ? a.r.tptr[n] : a.r.view[4 * n];
+        const int b1 = side ? a.r.tptr[n + 1] : a.r.view[4 * n + 1];
+        for (int c0 = b0; c0 < b1; c0 += kWave) {
+            const int cnt = min(kWave, b1 - c0);
+            int me = 0;
+            float mf = 0.0f;
+            if (lane < cnt) {
+                me = side ? a.r.tidx[c0 + lane] : c0 + lane;
+                mf = a.fc[me];
             }
-        __syncthreads();
+            fetch(lane_i(me, 0), side * LC);
+            for (int u = 0; u < cnt; ++u) {
+                const float fc = lane_f(mf, u);
+                __syncthreads();
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (lane + kWave * q < LC) dxL[lane + kWave * q] = dxn[q];
+                if (lane < nq) Yl[lane] = yn;
+                float du[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) du[q] = dun[q];
+                __syncthreads();
+                if (u + 1 < cnt) fetch(lane_i(me, u + 1), side * LC);
+                if (fc == 0.0f) continue;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if (side)
+                        sb[q] += du[q];
+                    else
+                        sa[q] += du[q];
+                }
+#pragma unroll
+                for (int t = 0; t < kMaxOut; ++t)
+                    if (lane + kWave * t < CN) {
+                        float v = dxL[col[t]] * Yl[kk[t]];
+                        g[t] += (side && (LL[t] & 1)) ? -v : v;
+                    }
+            }
+        }
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -440,6 +573,7 @@ __global__ void __launch_bounds__(kWave) k_eq_atom_backward(EqArgs a) {
         }
     }
     // channel mix adjoint: dH[c][k] += sum_c' M_L[c'][c] dMIX[c'][k]
+    __syncthreads();
     for (int o = lane; o < CN; o += kWave) dmixL[o] = a.dmix[size_t(n) * CN + o];
     __syncthreads();
 #pragma unroll
@@ -454,34 +588,84 @@ __global__ void __launch_bounds__(kWave) k_eq_atom_backward(EqArgs a) {
     }
 }
 
-// dE/dY from the probes of the records of centre i.
+// dE/dY of the records of centre i: the injected direction term
+// fc tI[L,c] dHt_i[c][k] and the probes of the centre and neighbour states.
 __global__ void __launch_bounds__(kWave) k_eq_probe_dy(EqArgs a) {
     extern __shared__ float lds[];
-    const int C = a.C, nq = a.nq, LC = a.lq * C, CN = C * nq;
-    float *Hi = lds;          // [CN]
-    float *Hj = Hi + CN;      // [CN]
-    float *dxL = Hj + CN;     // [2 LC]
+    const int C = a.C, nq = a.nq, LC = a.lq * C, CN = C * nq, G = a.G, NG = a.NG;
+    const int ldc = nq | 1;
+    float *Hi = lds;             // [C][ldc]
+    float *DH = Hi + C * ldc;    // [C][ldc]
+    float *Hj = DH + C * ldc;    // [C][ldc]
+    float *cf = Hj + C * ldc;    // [3 LC] injection gates | centre / neighbour probe adjoints
     const int i = blockIdx.x, lane = threadIdx.x;
-    for (int o = lane; o < CN; o += kWave) Hi[o] = a.dir_in[size_t(i) * CN + o];
-    const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
-    const int k = lane < nq ? lane : 0, L = order_of(k);
-    for (int e = rb; e < re; ++e) {
-        if (a.fc[e] == 0.0f) continue;
-        const float *hj = a.dir_in + size_t(a.r.nbr[e]) * CN;
-        for (int o = lane; o < CN; o += kWave) Hj[o] = hj[o];
-        const float *dx = a.dx + size_t(e) * a.ldx + a.kb;
-        for (int p = lane; p < 2 * LC; p += kWave) dxL[p] = dx[p];
-        __syncthreads();
-        if (lane < nq) {
-            const float *dc = dxL + (L - 1) * C;
-            float yc = 0.0f, yn = 0.0f;
-            for (int c = 0; c < C; ++c) {
-                yc += dc[c] * Hi[c * nq + k];
-                yn += dc[LC + c] * Hj[c * nq + k];
-            }
-            a.dy[size_t(e) * nq + k] += yc + ((L & 1) ? -yn : yn);
+    int so[kMaxOut];
+#pragma unroll
+    for (int t = 0; t < kMaxOut; ++t) {
+        int o = lane + kWave * t;
+        so[t] = o < CN ? (o / nq) * ldc + o % nq : -1;
+        if (so[t] >= 0) {
+            Hi[so[t]] = a.dir_in[size_t(i) * CN + o];
+            DH[so[t]] = a.dht[size_t(i) * CN + o];
         }
-        __syncthreads();
+    }
+    // contraction layout: component k = lane % nq, channels c = cg, cg + ncg, ...
+    const int ncg = kWave / nq, k = lane % nq, cg = lane / nq, L = order_of(k);
+    float hn[kMaxOut], cn[kMaxOut];
+    auto fetch = [&](int e, int j) {
+#pragma unroll
+        for (int t = 0; t < kMaxOut; ++t)
+            hn[t] = so[t] >= 0 ? a.dir_in[size_t(j) * CN + lane + kWave * t] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < kMaxOut; ++t) {
+            int q = lane + kWave * t;
+            float v = 0.0f;
+            if (q < LC)
+                v = a.ag[size_t(e) * NG + G + LC + q];
+            else if (q < 3 * LC)
+                v = a.dx[size_t(e) * a.ldx + a.kb + q - LC];
+            cn[t] = v;
+        }
+    };
+    const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
+    for (int c0 = rb; c0 < re; c0 += kWave) {
+        const int cnt = min(kWave, re - c0);
+        int mj = 0;
+        float mf = 0.0f;
+        if (lane < cnt) {
+            mj = a.r.nbr[c0 + lane];
+            mf = a.fc[c0 + lane];
+        }
+        fetch(c0, lane_i(mj, 0));
+        for (int u = 0; u < cnt; ++u) {
+            const int e = c0 + u;
+            const float fc = lane_f(mf, u);
+            __syncthreads();
+#pragma unroll
+            for (int t = 0; t < kMaxOut; ++t) {
+                if (so[t] >= 0) Hj[so[t]] = hn[t];
+                if (lane + kWave * t < 3 * LC) cf[lane + kWave * t] = cn[t];
+            }
+            __syncthreads();
+            if (u + 1 < cnt) fetch(e + 1, lane_i(mj, u + 1));
+            if (fc == 0.0f) continue;
+            float y = 0.0f;
+            if (cg < ncg) {
+                const float *ti = cf + (L - 1) * C, *dc = ti + LC, *dn = ti + 2 * LC;
+                float yi = 0.0f, yc = 0.0f, yn = 0.0f;
+                for (int c = cg; c < C; c += ncg) {
+                    yi += ti[c] * DH[c * ldc + k];
+                    yc += dc[c] * Hi[c * ldc + k];
+                    yn += dn[c] * Hj[c * ldc + k];
+                }
+                y = fc * yi + yc + ((L & 1) ? -yn : yn);
+            }
+            for (int s2 = 1; s2 < ncg; ++s2) {
+                float v = __shfl(y, min(lane + s2 * nq, kWave - 1), kWave);
+                if (cg == 0) y += v;
+            }
+            if (cg == 0) a.dy[size_t(e) * nq + k] += y;
+        }
     }
 }
 
@@ -569,8 +753,8 @@ static void expect(ModelImpl &m, const std::string &name, int64_t n) { m.expecte
 void validate_equivariant(ModelImpl &m) {
     const rune_model_config &c = m.cfg;
     const int lq = c.equivariant_l_max, C = c.equivariant_channels;
-    RUNE_REQUIRE(lq >= 1 && lq <= std::min(c.l_max, 8), RUNE_ERR_ARGUMENT,
-                 "equivariant_l_max must be in 1..min(l_max, 8).");
+    RUNE_REQUIRE(lq >= 1 && lq <= std::min(c.l_max, 7), RUNE_ERR_ARGUMENT,
+                 "equivariant blocks support equivariant_l_max in 1..min(l_max, 7)");
     RUNE_REQUIRE(C >= 1 && C * lq * (lq + 2) <= kWave * kMaxOut, RUNE_ERR_ARGUMENT,
                  "equivariant_channels * l(l+2) must not exceed 768");
     RUNE_REQUIRE(c.message_groups <= kWave, RUNE_ERR_ARGUMENT, "message_groups must be <= 64");
@@ -938,7 +1122,7 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         Epilogue e1;
         gemm(N, NU, D, p.at(p.t_dz1), D, w.up1_fT, D, p.at(p.t_duin), NU, e1, s);
         hipLaunchKernelGGL(k_eq_node_backward, dim3(N), dim3(kWave), 0, s, a);
-        size_t lds = sizeof(float) * (3 * C * (nq | 1) + H + w.NG + nq);
+        size_t lds = sizeof(float) * (2 * C * (nq | 1) + H + w.NG + nq);
         hipLaunchKernelGGL(k_eq_edge_backward, dim3(N), dim3(kWave), lds, s, a);
         hipLaunchKernelGGL(k_eq_neighbor_backward, dim3(N), dim3(kWave), sizeof(float) * w.NG,
                            s, a);
@@ -956,8 +1140,8 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         const int LC = lq * C;
         hipLaunchKernelGGL(k_eq_atom_backward, dim3(N), dim3(kWave),
                            sizeof(float) * (LC + nq + CN), s, a);
-        hipLaunchKernelGGL(k_eq_probe_dy, dim3(N), dim3(kWave), sizeof(float) * (2 * CN + 2 * LC),
-                           s, a);
+        hipLaunchKernelGGL(k_eq_probe_dy, dim3(N), dim3(kWave),
+                           sizeof(float) * (3 * C * (nq | 1) + 3 * LC), s, a);
         RUNE_HIP_CHECK(hipGetLastError());
         Epilogue e4;
         gemm(N, H, w.NP, p.at(p.t_dvs), w.NP, w.node_fT, w.NP, p.at(p.t_dz), H, e4, s);
