@@ -18,8 +18,9 @@ namespace rune {
 namespace {
 
 constexpr int kWave = 64;
+constexpr int kWaves = 4;               // waves per block in the per-atom kernels
+constexpr int kBlock = kWave * kWaves;
 constexpr float kPi = 3.14159265358979323846f;
-constexpr int kMaxOut = 12;   // C * nq <= 768 outputs per atom, 12 per lane
 
 __device__ inline float wave_sum(float v) {
 #pragma unroll
@@ -27,7 +28,43 @@ __device__ inline float wave_sum(float v) {
     return v;
 }
 
-__device__ inline int order_of(int k) {
+// Lane permutations for reductions: DPP quad_perm (xor 1, xor 2) and row
+// rotations (4, 8 lanes within a 16-lane row) are VALU operations;
+// ds_swizzle in bit mode exchanges lanes l and l ^ m within 32 lanes.
+template <int kCtrl>
+__device__ inline float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF,
+                                                      false));
+}
+template <int kXor>
+__device__ inline float swz(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (kXor << 10)));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppRor4 = 0x124, kDppRor8 = 0x128;
+
+// Sum over the w lanes of a lane group (w a power of two <= 64, groups
+// aligned); every lane of the group receives the sum.
+__device__ inline float group_sum(float v, int w) {
+    if (w >= 2) v += dpp<kDppXor1>(v);
+    if (w >= 4) v += dpp<kDppXor2>(v);
+    if (w == 8) v += swz<4>(v);
+    if (w >= 16) {
+        v += dpp<kDppRor4>(v);
+        v += dpp<kDppRor8>(v);
+    }
+    if (w >= 32) v += swz<16>(v);
+    if (w >= 64) v += __shfl_xor(v, 32, kWave);
+    return v;
+}
+
+// Orders LDS traffic of one wave (lanes exchange data through LDS).
+__device__ inline void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __host__ inline int order_of(int k) {
     int L = 1;
     while ((L + 1) * (L + 1) - 1 <= k) ++L;
     return L;
@@ -36,8 +73,11 @@ __device__ inline int order_of(int k) {
 struct EqArgs {
     Records r;
     int H, D, G, C, lq, nq, NG, NP, KX, kb, ldx, na, nlm;
+    int S;                    // records in flight per wave (lane slots of 64 / S lanes)
+    int gmode;                // group-sum method of k_eq_pair_backward
     float eps, cutoff;
     const float *fc;          // [E]
+    const float *tfc;         // [E] fc of transposed record t (fc[tidx[t]])
     const float *harm;        // [E, nq]
     const float *rb;          // [E, ldrb]
     int ldrb;
@@ -56,7 +96,8 @@ struct EqArgs {
     const float *ddir_out;    // [N, C*nq] from later blocks, or null
     float *dgg;               // [E, NG]
     float4 *dv;               // [E]
-    float *dy;                // [E, nq]
+    float *dy;                // [E, nq] dE/dY, centre-side shares
+    float *dyn;               // [E, nq] dE/dY, neighbour-side shares
     float *dnode;             // [N, NP]
     float *dmix;              // [N, C*nq]
     const float *due;         // [E, D]
@@ -77,209 +118,307 @@ __global__ void __launch_bounds__(kWave) k_eq_encode(int N, const float *s, int 
     }
 }
 
-__global__ void __launch_bounds__(kWave) k_eq_mix(const float *mixw, const float *in, int C,
-                                                  int nq, float *out) {
-    const int i = blockIdx.x, lane = threadIdx.x;
-    const float *h = in + size_t(i) * C * nq;
-    for (int o = lane; o < C * nq; o += kWave) {
-        int c = o / nq, k = o - c * nq, L = order_of(k);
-        const float *M = mixw + size_t((L - 1) * C + c) * C;
-        float acc = 0.0f;
-        for (int cc = 0; cc < C; ++cc) acc += M[cc] * h[cc * nq + k];
-        out[size_t(i) * C * nq + o] = acc;
-    }
+// ---- work assignment of the per-atom kernels ----
+// One atom per wave, four waves per block.  Blocks are dealt to the 8 XCDs
+// round-robin; xcd_rank renumbers them so that each XCD walks one contiguous
+// range of the processing order.  The order is the neighbour builder's
+// Morton-ordered cell bins, so the rows an XCD gathers stay in its L2.
+__device__ inline int xcd_rank(int b, int nb) {
+    const int x = b & 7, k = b >> 3, q = nb >> 3, r = nb & 7;
+    return x * q + min(x, r) + k;
 }
 
-// Per-edge loops.  Each kernel walks the records of one atom in chunks of 64:
-// the chunk's record metadata (neighbour / centre index, cutoff value) is read
-// lane-parallel once and broadcast per record with readlane, and the rows of
-// the next record are fetched into registers while the current one is
-// processed, so no record waits on a chain of dependent loads.
-__device__ inline int lane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
-__device__ inline float lane_f(float v, int l) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+__device__ inline int wave_atom(const Records &r) {
+    const int t = __builtin_amdgcn_readfirstlane(xcd_rank(blockIdx.x, gridDim.x) * kWaves +
+                                                 int(threadIdx.x >> 6));
+    if (t >= r.n_atoms) return -1;
+    return r.order ? __builtin_amdgcn_readfirstlane(r.order[t]) : t;
 }
 
-constexpr int kMaxG = 9;     // NG <= 64 + 2 * 256 gate columns, 9 per lane
-constexpr int kMaxY = 1;     // nq <= 64 harmonic components, 1 per lane
-
-// Edge features [rb | probes_c | probes_n] of the radial records of centre i.
-__global__ void __launch_bounds__(kWave) k_eq_features(EqArgs a) {
-    extern __shared__ float lds[];
-    const int C = a.C, nq = a.nq, lq = a.lq, LC = lq * C, CN = C * nq;
-    const int ldc = nq | 1;   // odd LDS row stride: channel-strided reads hit distinct banks
-    float *Hi = lds;          // [C][ldc] centre state
-    float *Hj = Hi + C * ldc; // [C][ldc] neighbour state of the current record
-    float *Yl = Hj + C * ldc; // [nq]
-    const int i = blockIdx.x, lane = threadIdx.x;
-    int so[kMaxOut];
-#pragma unroll
-    for (int t = 0; t < kMaxOut; ++t) {
-        int o = lane + kWave * t;
-        so[t] = o < CN ? (o / nq) * ldc + o % nq : -1;
-        if (so[t] >= 0) Hi[so[t]] = a.dir_in[size_t(i) * CN + o];
+// Lane layout of the record loops: the wave holds S records at once, one per
+// slot of W = 64 / S lanes.  Lane c of a slot owns channel c (c < C) with all
+// NQ components of it (one contiguous state row), and the hidden / message
+// columns c, c + W, c + 2W, ...
+template <int S>
+struct Lanes {
+    static constexpr int W = kWave / S;
+    static constexpr int HM = 4 * kWave / W;   // columns per lane for widths <= 256
+    int lane, slot, c;
+    bool act;
+    __device__ explicit Lanes(int C) {
+        lane = threadIdx.x & (kWave - 1);
+        slot = lane / W;
+        c = lane - slot * W;
+        act = c < C;
     }
-    float hn[kMaxOut], yn = 0.0f, rn = 0.0f;
-    auto fetch = [&](int e, int j) {
+};
+
+template <int NQ>
+__device__ inline void load_row(float (&v)[NQ], const float *__restrict__ p) {
+    if constexpr (NQ % 4 == 0) {
 #pragma unroll
-        for (int t = 0; t < kMaxOut; ++t)
-            hn[t] = so[t] >= 0 ? a.dir_in[size_t(j) * CN + lane + kWave * t] : 0.0f;
-        yn = lane < nq ? a.harm[size_t(e) * nq + lane] : 0.0f;
-        rn = lane < a.kb ? a.rb[size_t(e) * a.ldrb + lane] : 0.0f;
-    };
-    const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
-    for (int c0 = rb; c0 < re; c0 += kWave) {
-        const int cnt = min(kWave, re - c0);
-        int mj = 0;
-        float mf = 0.0f;
-        if (lane < cnt) {
-            mj = a.r.nbr[c0 + lane];
-            mf = a.fc[c0 + lane];
+        for (int q = 0; q < NQ / 4; ++q) {
+            const float4 t = reinterpret_cast<const float4 *>(p)[q];
+            v[4 * q] = t.x;
+            v[4 * q + 1] = t.y;
+            v[4 * q + 2] = t.z;
+            v[4 * q + 3] = t.w;
         }
-        fetch(c0, lane_i(mj, 0));
-        for (int u = 0; u < cnt; ++u) {
-            const int e = c0 + u;
-            const float fc = lane_f(mf, u);
-            __syncthreads();
+    } else {
 #pragma unroll
-            for (int t = 0; t < kMaxOut; ++t)
-                if (so[t] >= 0) Hj[so[t]] = hn[t];
-            if (lane < nq) Yl[lane] = yn;
-            const float rcur = rn;
-            __syncthreads();
-            if (u + 1 < cnt) fetch(e + 1, lane_i(mj, u + 1));
-            float *x = a.x + size_t(e) * a.ldx;
-            if (fc == 0.0f) {
-                for (int k = lane; k < a.KX; k += kWave) x[k] = 0.0f;
-                continue;
+        for (int k = 0; k < NQ; ++k) v[k] = p[k];
+    }
+}
+
+template <int NQ>
+__device__ inline void store_row(const float (&v)[NQ], float *__restrict__ p) {
+    if constexpr (NQ % 4 == 0) {
+#pragma unroll
+        for (int q = 0; q < NQ / 4; ++q)
+            reinterpret_cast<float4 *>(p)[q] =
+                make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    } else {
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) p[k] = v[k];
+    }
+}
+
+template <int N>
+__device__ inline void zero(float (&v)[N]) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) v[k] = 0.0f;
+}
+
+template <int N>
+__device__ inline void copy(float (&d)[N], const float (&s)[N]) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) d[k] = s[k];
+}
+
+// Adds the partial sums of the S slots (fixed tree order); every slot ends
+// with the total.
+template <int S, int N>
+__device__ inline void fold_slots(float (&v)[N]) {
+#pragma unroll
+    for (int off = kWave >> 1; off >= kWave / S; off >>= 1) {
+#pragma unroll
+        for (int k = 0; k < N; ++k) v[k] += __shfl_xor(v[k], off, kWave);
+    }
+}
+
+// out[n, c, k] = sum_c' W_L[c][c'] in[n, c', k] (trans = 0) or
+// sum_c' W_L[c'][c] in[n, c', k] (trans = 1), L the order of component k.
+template <int LQ>
+__global__ void __launch_bounds__(256) k_eq_mix(int N, const float *mixw, const float *in, int C,
+                                                int trans, float *out) {
+    constexpr int NQ = LQ * (LQ + 2);
+    extern __shared__ float lds[];
+    const int CN = C * NQ, CC = C * C;
+    float *Wl = lds;                  // [LQ][c][c'] as applied
+    float *row = lds + LQ * CC;       // [C][NQ] input row of the current atom
+    for (int o = threadIdx.x; o < LQ * CC; o += blockDim.x) {
+        const int L = o / CC, r = o - L * CC, c = r / C, cc = r - c * C;
+        Wl[o] = trans ? mixw[size_t(L) * CC + cc * C + c] : mixw[o];
+    }
+    for (int n = blockIdx.x; n < N; n += gridDim.x) {
+        __syncthreads();
+        for (int o = threadIdx.x; o < CN; o += blockDim.x) row[o] = in[size_t(n) * CN + o];
+        __syncthreads();
+        for (int o = threadIdx.x; o < CN; o += blockDim.x) {
+            const int c = o / NQ, k = o - c * NQ;
+            const float *w = Wl + size_t((order_of(k) - 1) * C + c) * C;
+            float acc = 0.0f;
+            for (int cc = 0; cc < C; ++cc) acc += w[cc] * row[cc * NQ + k];
+            out[size_t(n) * CN + o] = acc;
+        }
+    }
+}
+
+// Record metadata is read 64 records at a time, lane-parallel, and handed to
+// the slots by shuffles, so the row loads of the next S records depend on no
+// other load and are issued while the current records are processed.
+__device__ inline int bcast(int v, int src) { return __shfl(v, src, kWave); }
+__device__ inline float bcast(float v, int src) { return __shfl(v, src, kWave); }
+
+// Edge features [rb | probes_c | probes_n] = [rb | H_i.Y | (-1)^L H_j.Y].
+// The wave of atom n holds H_n in registers and fills the probes of its own
+// records (n = centre: rb and probes_c, all records of the segment) and of
+// the records that see it as neighbour (probes_n), so no state row is
+// gathered.
+template <int LQ, int S>
+__global__ void __launch_bounds__(kBlock) k_eq_features(EqArgs a) {
+    constexpr int NQ = LQ * (LQ + 2), LY = NQ + (NQ % 4 == 0 ? 4 : 1);
+    using Ln = Lanes<S>;
+    extern __shared__ float lds[];
+    const int n = wave_atom(a.r);
+    if (n < 0) return;
+    const Ln ln(a.C);
+    const int C = a.C, CN = C * NQ, LC = LQ * C, kb = a.kb;
+    // harmonic rows of the current chunk of 64 records, one row per record
+    float *Yc = lds + (threadIdx.x >> 6) * kWave * LY;
+    float Hn[NQ];
+    zero(Hn);
+    if (ln.act) load_row(Hn, a.dir_in + size_t(n) * CN + ln.c * NQ);
+#pragma unroll
+    for (int side = 0; side < 2; ++side) {
+        const int b0 = side ? a.r.tptr[n] : a.r.ptr[n];
+        const int b1 = side ? a.r.tptr[n + 1] : a.r.ptr[n + 1];
+        for (int t0 = b0; t0 < b1; t0 += kWave) {
+            const int cnt = min(kWave, b1 - t0);
+            int me = -1;
+            float mf = 0.0f;
+            wave_sync();
+            if (ln.lane < cnt) {
+                me = side ? a.r.tidx[t0 + ln.lane] : t0 + ln.lane;
+                mf = side ? a.tfc[t0 + ln.lane] : a.fc[t0 + ln.lane];
+                float y[NQ];
+                load_row(y, a.harm + size_t(me) * NQ);
+#pragma unroll
+                for (int k = 0; k < NQ; ++k) Yc[ln.lane * LY + k] = y[k];
             }
-            if (lane < a.kb) x[lane] = rcur;
-            for (int p = lane; p < LC; p += kWave) {
-                int L = p / C + 1, c = p - (L - 1) * C, st = L * L - 1;
-                float pc = 0.0f, pn = 0.0f;
-                for (int m = 0; m < 2 * L + 1; ++m) {
-                    pc += Hi[c * ldc + st + m] * Yl[st + m];
-                    pn += Hj[c * ldc + st + m] * Yl[st + m];
+            wave_sync();
+            for (int q0 = 0; q0 < cnt; q0 += S) {
+                const int q = q0 + ln.slot;
+                const int e = bcast(me, min(q, kWave - 1));
+                const float fc = bcast(mf, min(q, kWave - 1));
+                if (q < cnt) {
+                    float *x = a.x + size_t(e) * a.ldx;
+                    const bool on = fc != 0.0f;
+                    if (!side)
+                        for (int k = ln.c; k < kb; k += Ln::W)
+                            x[k] = on ? a.rb[size_t(e) * a.ldrb + k] : 0.0f;
+                    if (ln.act) {
+                        float Y[NQ];
+#pragma unroll
+                        for (int k = 0; k < NQ; ++k) Y[k] = Yc[q * LY + k];
+#pragma unroll
+                        for (int L = 1; L <= LQ; ++L) {
+                            const int st = L * L - 1;
+                            float p = 0.0f;
+#pragma unroll
+                            for (int m = 0; m < 2 * L + 1; ++m) p += Hn[st + m] * Y[st + m];
+                            if (side) p = (L & 1) ? -p : p;
+                            x[kb + side * LC + (L - 1) * C + ln.c] = on ? p : 0.0f;
+                        }
+                    }
                 }
-                x[a.kb + p] = pc;
-                x[a.kb + LC + p] = (L & 1) ? -pn : pn;
             }
         }
     }
 }
 
 // Messages and transported / injected direction states of centre i, then the
-// update input [RMSNorm(msg) | per-(L, c) squared norms of dir_out].
-__global__ void __launch_bounds__(kWave) k_eq_aggregate(EqArgs a) {
-    extern __shared__ float lds[];
-    const int H = a.H, G = a.G, C = a.C, nq = a.nq, lq = a.lq, gw = H / G, LC = lq * C;
-    const int CN = C * nq, NG = a.NG;
-    float *Ho = lds;          // [CN]
-    float *gL = Ho + CN;      // [NG] gates of the current record
-    float *Yl = gL + NG;      // [nq]
-    const int i = blockIdx.x, lane = threadIdx.x;
-    float macc[4] = {0, 0, 0, 0};
-    float dacc[kMaxOut];
-    int gT[kMaxOut], kk[kMaxOut];
-#pragma unroll
-    for (int t = 0; t < kMaxOut; ++t) {
-        dacc[t] = 0.0f;
-        int o = lane + kWave * t;
-        int c = o / nq, k = o - c * nq;
-        kk[t] = k;
-        gT[t] = o < CN ? G + (order_of(k) - 1) * C + c : 0;
-    }
-    float gn[kMaxG], vn[4], mxn[kMaxOut], yn = 0.0f;
-    auto fetch = [&](int e, int j) {
-#pragma unroll
-        for (int q = 0; q < kMaxG; ++q) {
-            int k = lane + kWave * q;
-            gn[q] = k < NG ? a.ag[size_t(e) * NG + k] : 0.0f;
-        }
-        yn = lane < nq ? a.harm[size_t(e) * nq + lane] : 0.0f;
-        const float *V = a.node + size_t(j) * a.NP + 2 * a.D;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            int c = lane + kWave * t;
-            vn[t] = c < H ? V[c] : 0.0f;
-        }
-#pragma unroll
-        for (int t = 0; t < kMaxOut; ++t) {
-            int o = lane + kWave * t;
-            mxn[t] = o < CN ? a.mixst[size_t(j) * CN + o] : 0.0f;
-        }
-    };
-    const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
-    for (int c0 = rb; c0 < re; c0 += kWave) {
-        const int cnt = min(kWave, re - c0);
+// update input [RMSNorm(msg) | per-(L, c) squared norms of dir_out].  The
+// neighbour rows (mixed state, values) are gathered for S records at a time.
+template <int LQ, int S>
+__global__ void __launch_bounds__(kBlock) k_eq_aggregate(EqArgs a) {
+    constexpr int NQ = LQ * (LQ + 2);
+    using Ln = Lanes<S>;
+    constexpr int HM = Ln::HM;
+    const int i = wave_atom(a.r);
+    if (i < 0) return;
+    const Ln ln(a.C);
+    const int H = a.H, G = a.G, C = a.C, CN = C * NQ, LC = LQ * C, NG = a.NG;
+    const int gw = H / G;
+    const int e_begin = a.r.view[4 * i], e_end = a.r.view[4 * i + 1];
+    float acc[NQ], macc[HM];
+    zero(acc);
+    zero(macc);
+    for (int t0 = e_begin; t0 < e_end; t0 += kWave) {
+        const int cnt = min(kWave, e_end - t0);
         int mj = 0;
         float mf = 0.0f;
-        if (lane < cnt) {
-            mj = a.r.nbr[c0 + lane];
-            mf = a.fc[c0 + lane];
+        if (ln.lane < cnt) {
+            mj = a.r.nbr[t0 + ln.lane];
+            mf = a.fc[t0 + ln.lane];
         }
-        fetch(c0, lane_i(mj, 0));
-        for (int u = 0; u < cnt; ++u) {
-            const float fc = lane_f(mf, u);
-            __syncthreads();
+        auto fetch = [&](int q, float (&y)[NQ], float (&mx)[NQ], float (&tt)[LQ],
+                         float (&ti)[LQ], float (&v)[HM], float (&g)[HM], float &f) {
+            const int j = bcast(mj, min(q, kWave - 1));
+            f = bcast(mf, min(q, kWave - 1));
+            if (q >= cnt) f = 0.0f;
+            if (f != 0.0f) {
+                const int e = t0 + q;
+                if (ln.act) {
+                    load_row(y, a.harm + size_t(e) * NQ);
+                    load_row(mx, a.mixst + size_t(j) * CN + ln.c * NQ);
+                    const float *gr = a.ag + size_t(e) * NG + G + ln.c;
 #pragma unroll
-            for (int q = 0; q < kMaxG; ++q)
-                if (lane + kWave * q < NG) gL[lane + kWave * q] = gn[q];
-            if (lane < nq) Yl[lane] = yn;
-            float vc[4], mx[kMaxOut];
+                    for (int L = 0; L < LQ; ++L) {
+                        tt[L] = gr[L * C];
+                        ti[L] = gr[LC + L * C];
+                    }
+                }
+                const float *Vr = a.node + size_t(j) * a.NP + 2 * a.D;
+                const float *gr = a.ag + size_t(e) * NG;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) vc[t] = vn[t];
-#pragma unroll
-            for (int t = 0; t < kMaxOut; ++t) mx[t] = mxn[t];
-            __syncthreads();
-            if (u + 1 < cnt) fetch(c0 + u + 1, lane_i(mj, u + 1));
-            if (fc == 0.0f) continue;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                int c = lane + kWave * t;
-                if (c < H) macc[t] += gL[c / gw] * fc * vc[t];
+                for (int u = 0; u < HM; ++u) {
+                    const int h = ln.c + Ln::W * u;
+                    v[u] = h < H ? Vr[h] : 0.0f;
+                    g[u] = h < H ? gr[h / gw] : 0.0f;
+                }
             }
+        };
+        float Y[NQ], M[NQ], tT[LQ], tI[LQ], V[HM], g[HM], fc;
+        fetch(ln.slot, Y, M, tT, tI, V, g, fc);
+        for (int q0 = 0; q0 < cnt; q0 += S) {
+            float Yn[NQ], Mn[NQ], tTn[LQ], tIn[LQ], Vn[HM], gn[HM], fcn;
+            fetch(q0 + S + ln.slot, Yn, Mn, tTn, tIn, Vn, gn, fcn);
+            if (fc != 0.0f) {
+                if (ln.act) {
 #pragma unroll
-            for (int t = 0; t < kMaxOut; ++t) {
-                int o = lane + kWave * t;
-                if (o < CN) dacc[t] += fc * (gL[gT[t]] * mx[t] + gL[gT[t] + LC] * Yl[kk[t]]);
+                    for (int L = 1; L <= LQ; ++L)
+#pragma unroll
+                        for (int m = 0; m < 2 * L + 1; ++m) {
+                            const int k = L * L - 1 + m;
+                            acc[k] += fc * (tT[L - 1] * M[k] + tI[L - 1] * Y[k]);
+                        }
+                }
+#pragma unroll
+                for (int u = 0; u < HM; ++u) macc[u] += g[u] * fc * V[u];
             }
+            copy(Y, Yn);
+            copy(M, Mn);
+            copy(tT, tTn);
+            copy(tI, tIn);
+            copy(V, Vn);
+            copy(g, gn);
+            fc = fcn;
         }
     }
-    __syncthreads();
+    fold_slots<S>(acc);
+    fold_slots<S>(macc);
+    const int ldu = H + LC;
+    if (ln.slot == 0 && ln.act) {
+        float v[NQ];
+        load_row(v, a.dir_in + size_t(i) * CN + ln.c * NQ);
 #pragma unroll
-    for (int t = 0; t < kMaxOut; ++t) {
-        int o = lane + kWave * t;
-        if (o < CN) {
-            float v = a.dir_in[size_t(i) * CN + o] + dacc[t];
-            a.dir_out[size_t(i) * CN + o] = v;
-            Ho[o] = v;
+        for (int k = 0; k < NQ; ++k) v[k] += acc[k];
+        store_row(v, a.dir_out + size_t(i) * CN + ln.c * NQ);
+#pragma unroll
+        for (int L = 1; L <= LQ; ++L) {
+            float s = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 2 * L + 1; ++m) s += v[L * L - 1 + m] * v[L * L - 1 + m];
+            a.uin[size_t(i) * ldu + H + (L - 1) * C + ln.c] = s;
         }
     }
     float ss = 0.0f;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        int c = lane + kWave * t;
-        if (c < H) {
-            a.msg[size_t(i) * H + c] = macc[t];
-            ss += macc[t] * macc[t];
-        }
-    }
-    ss = wave_sum(ss);
-    float r = 1.0f / sqrtf(ss / float(H) + a.eps);
-    if (lane == 0) a.rm[i] = r;
-    const int ldu = H + LC;
+    for (int u = 0; u < HM; ++u)
+        if (ln.c + Ln::W * u < H) ss += macc[u] * macc[u];
+    ss = group_sum(ss, Ln::W);
+    const float r = 1.0f / sqrtf(ss / float(H) + a.eps);
+    if (ln.lane == 0) a.rm[i] = r;
+    if (ln.slot == 0) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        int c = lane + kWave * t;
-        if (c < H) a.uin[size_t(i) * ldu + c] = macc[t] * r;
-    }
-    __syncthreads();
-    for (int p = lane; p < LC; p += kWave) {
-        int L = p / C + 1, c = p - (L - 1) * C, st = L * L - 1;
-        float s = 0.0f;
-        for (int m = 0; m < 2 * L + 1; ++m) s += Ho[c * nq + st + m] * Ho[c * nq + st + m];
-        a.uin[size_t(i) * ldu + H + p] = s;
+        for (int u = 0; u < HM; ++u) {
+            const int h = ln.c + Ln::W * u;
+            if (h < H) {
+                a.msg[size_t(i) * H + h] = macc[u];
+                a.uin[size_t(i) * ldu + h] = macc[u] * r;
+            }
+        }
     }
 }
 
@@ -302,371 +441,333 @@ __global__ void __launch_bounds__(kWave) k_eq_node_backward(EqArgs a) {
     }
 }
 
-// Gate adjoints and dE/dfc for the records of centre i.
-__global__ void __launch_bounds__(kWave) k_eq_edge_backward(EqArgs a) {
-    extern __shared__ float lds[];
-    const int H = a.H, G = a.G, C = a.C, nq = a.nq, lq = a.lq, gw = H / G, LC = lq * C;
-    const int CN = C * nq, NG = a.NG, ldc = nq | 1;
-    float *DH = lds;             // [C][ldc] dE/d(dir_out) of centre i
-    float *MX = DH + C * ldc;    // [C][ldc] mixed state of the current neighbour
-    float *pL = MX + C * ldc;    // [H] dmsg_i * V_j
-    float *gL = pL + H;          // [NG]
-    float *YL = gL + NG;         // [nq]
-    const int i = blockIdx.x, lane = threadIdx.x;
-    int so[kMaxOut];
-#pragma unroll
-    for (int t = 0; t < kMaxOut; ++t) {
-        int o = lane + kWave * t;
-        so[t] = o < CN ? (o / nq) * ldc + o % nq : -1;
-        if (so[t] >= 0) DH[so[t]] = a.dht[size_t(i) * CN + o];
-    }
-    float dm[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        int c = lane + kWave * t;
-        dm[t] = c < H ? a.dmsg[size_t(i) * H + c] : 0.0f;
-    }
-    float gn[kMaxG], vn[4], mxn[kMaxOut], yn = 0.0f;
-    auto fetch = [&](int e, int j) {
-#pragma unroll
-        for (int q = 0; q < kMaxG; ++q) {
-            int k = lane + kWave * q;
-            gn[q] = k < NG ? a.ag[size_t(e) * NG + k] : 0.0f;
-        }
-        yn = lane < nq ? a.harm[size_t(e) * nq + lane] : 0.0f;
-        const float *V = a.node + size_t(j) * a.NP + 2 * a.D;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            int c = lane + kWave * t;
-            vn[t] = c < H ? V[c] : 0.0f;
-        }
-#pragma unroll
-        for (int t = 0; t < kMaxOut; ++t)
-            mxn[t] = so[t] >= 0 ? a.mixst[size_t(j) * CN + lane + kWave * t] : 0.0f;
-    };
-    const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
-    for (int c0 = rb; c0 < re; c0 += kWave) {
-        const int cnt = min(kWave, re - c0);
-        int mj = 0;
-        float mf = 0.0f;
-        if (lane < cnt) {
-            mj = a.r.nbr[c0 + lane];
-            mf = a.fc[c0 + lane];
-        }
-        fetch(c0, lane_i(mj, 0));
-        for (int u = 0; u < cnt; ++u) {
-            const int e = c0 + u;
-            const float fc = lane_f(mf, u);
-            float *dg = a.dgg + size_t(e) * NG;
-            __syncthreads();
-#pragma unroll
-            for (int q = 0; q < kMaxG; ++q)
-                if (lane + kWave * q < NG) gL[lane + kWave * q] = gn[q];
-            if (lane < nq) YL[lane] = yn;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                int c = lane + kWave * t;
-                if (c < H) pL[c] = dm[t] * vn[t];
-            }
-#pragma unroll
-            for (int t = 0; t < kMaxOut; ++t)
-                if (so[t] >= 0) MX[so[t]] = mxn[t];
-            __syncthreads();
-            if (u + 1 < cnt) fetch(e + 1, lane_i(mj, u + 1));
-            if (fc == 0.0f) {
-                for (int k = lane; k < NG; k += kWave) dg[k] = 0.0f;
-                continue;
-            }
-            float dfc = 0.0f;
-            for (int p = lane; p < LC; p += kWave) {
-                int L = p / C + 1, c = p - (L - 1) * C, st = L * L - 1;
-                float sT = 0.0f, sI = 0.0f;
-                for (int m = 0; m < 2 * L + 1; ++m) {
-                    float d = DH[c * ldc + st + m];
-                    sT += d * MX[c * ldc + st + m];
-                    sI += d * YL[st + m];
-                }
-                float tT = gL[G + p], tI = gL[G + LC + p];
-                dg[G + p] = (1.0f - tT * tT) * fc * sT;
-                dg[G + LC + p] = (1.0f - tI * tI) * fc * sI;
-                dfc += tT * sT + tI * sI;
-            }
-            if (lane < G) {
-                float P = 0.0f;
-                for (int c = lane * gw; c < (lane + 1) * gw; ++c) P += pL[c];
-                float s = gL[lane];
-                dg[lane] = P * fc * s * (1.0f - s);
-                dfc += P * s;
-            }
-            dfc = wave_sum(dfc);
-            if (lane == 0) {
-                float d = a.r.vec[e].w;
-                float fcp = -0.5f * kPi / a.cutoff * sinf(kPi * d / a.cutoff);
-                a.dv[e].w += dfc * fcp;
-            }
-        }
-    }
+__device__ inline float cutoff_slope(float d, float rc) {
+    return -0.5f * kPi / rc * sinf(kPi * d / rc);
 }
 
-// Adjoints landing on neighbour j: mixed states and gathered values.
-__global__ void __launch_bounds__(kWave) k_eq_neighbor_backward(EqArgs a) {
-    extern __shared__ float gL[];   // [NG] gates of the current record
-    const int j = blockIdx.x, lane = threadIdx.x;
-    const int H = a.H, G = a.G, C = a.C, nq = a.nq, gw = H / G, CN = C * nq, NG = a.NG;
-    float macc[kMaxOut];
-    int gT[kMaxOut];
+// Reverse pass of the messages, walked from the neighbour side: the wave of
+// atom j holds its mixed state M_j and values V_j, gathers the centre's
+// dE/d(dir_out) and dE/dmsg once per record, and produces
+//   the gate adjoints dE/dgate[e, :] and dE/dfc (into dv[e].w),
+//   dE/dM_j = sum_e fc tT[e] dHt_i and dE/dV_j = sum_e fc s_e dmsg_i.
+// Group sums P_g = sum_{h in g} dmsg_i[h] V_j[h] take the lane layout's
+// shuffles (gmode 0: group width divides W; 1: W divides it) or, for other
+// widths, a per-slot LDS row (gmode 2).
+template <int LQ, int S>
+__global__ void __launch_bounds__(kBlock) k_eq_pair_backward(EqArgs a) {
+    constexpr int NQ = LQ * (LQ + 2);
+    using Ln = Lanes<S>;
+    constexpr int HM = Ln::HM, W = Ln::W;
+    extern __shared__ float lds[];
+    const int j = wave_atom(a.r);
+    if (j < 0) return;
+    const Ln ln(a.C);
+    const int H = a.H, G = a.G, C = a.C, CN = C * NQ, LC = LQ * C, NG = a.NG;
+    const int gw = H / G, gmode = a.gmode;
+    float *T = lds + (threadIdx.x >> 6) * S * H + ln.slot * H;
+    float MX[NQ], Vj[HM];
+    zero(MX);
+    if (ln.act) load_row(MX, a.mixst + size_t(j) * CN + ln.c * NQ);
 #pragma unroll
-    for (int t = 0; t < kMaxOut; ++t) {
-        macc[t] = 0.0f;
-        int o = lane + kWave * t;
-        int c = o / nq, k = o - c * nq;
-        gT[t] = o < CN ? G + (order_of(k) - 1) * C + c : 0;
+    for (int u = 0; u < HM; ++u) {
+        const int h = ln.c + W * u;
+        Vj[u] = h < H ? a.node[size_t(j) * a.NP + 2 * a.D + h] : 0.0f;
     }
-    float vacc[4] = {0, 0, 0, 0};
-    float gn[kMaxG], dhn[kMaxOut], dmn[4];
-    auto fetch = [&](int e, int i) {
-#pragma unroll
-        for (int q = 0; q < kMaxG; ++q) {
-            int k = lane + kWave * q;
-            gn[q] = k < NG ? a.ag[size_t(e) * NG + k] : 0.0f;
-        }
-#pragma unroll
-        for (int t = 0; t < kMaxOut; ++t) {
-            int o = lane + kWave * t;
-            dhn[t] = o < CN ? a.dht[size_t(i) * CN + o] : 0.0f;
-        }
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            int c = lane + kWave * t;
-            dmn[t] = c < H ? a.dmsg[size_t(i) * H + c] : 0.0f;
-        }
-    };
+    float acc[NQ], vacc[HM];
+    zero(acc);
+    zero(vacc);
     const int tb = a.r.tptr[j], te = a.r.tptr[j + 1];
-    for (int c0 = tb; c0 < te; c0 += kWave) {
-        const int cnt = min(kWave, te - c0);
-        int me = 0, mi = 0;
+    for (int t0 = tb; t0 < te; t0 += kWave) {
+        const int cnt = min(kWave, te - t0);
+        int me = -1, mi = 0;
         float mf = 0.0f;
-        if (lane < cnt) {
-            me = a.r.tidx[c0 + lane];
-            mi = a.r.ctr[me];
-            mf = a.fc[me];
+        if (ln.lane < cnt) {
+            me = a.r.tidx[t0 + ln.lane];
+            mi = a.r.tctr[t0 + ln.lane];
+            mf = a.tfc[t0 + ln.lane];
         }
-        fetch(lane_i(me, 0), lane_i(mi, 0));
-        for (int u = 0; u < cnt; ++u) {
-            const float fc = lane_f(mf, u);
-            __syncthreads();
-#pragma unroll
-            for (int q = 0; q < kMaxG; ++q)
-                if (lane + kWave * q < NG) gL[lane + kWave * q] = gn[q];
-            float dh[kMaxOut], dmc[4];
-#pragma unroll
-            for (int t = 0; t < kMaxOut; ++t) dh[t] = dhn[t];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) dmc[t] = dmn[t];
-            __syncthreads();
-            if (u + 1 < cnt) fetch(lane_i(me, u + 1), lane_i(mi, u + 1));
-            if (fc == 0.0f) continue;
-#pragma unroll
-            for (int q = 0; q < kMaxOut; ++q) {
-                int o = lane + kWave * q;
-                if (o < CN) macc[q] += fc * gL[gT[q]] * dh[q];
+        auto fetch = [&](int q, int &e, float (&dh)[NQ], float (&y)[NQ], float (&tt)[LQ],
+                         float (&ti)[LQ], float (&dm)[HM], float (&sg)[HM], float &f) {
+            e = bcast(me, min(q, kWave - 1));
+            const int i = bcast(mi, min(q, kWave - 1));
+            f = bcast(mf, min(q, kWave - 1));
+            if (q >= cnt) {
+                e = -1;
+                f = 0.0f;
             }
+            if (f != 0.0f) {
+                if (ln.act) {
+                    load_row(dh, a.dht + size_t(i) * CN + ln.c * NQ);
+                    load_row(y, a.harm + size_t(e) * NQ);
+                    const float *gr = a.ag + size_t(e) * NG + G + ln.c;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                int c = lane + kWave * q;
-                if (c < H) vacc[q] += gL[c / gw] * fc * dmc[q];
+                    for (int L = 0; L < LQ; ++L) {
+                        tt[L] = gr[L * C];
+                        ti[L] = gr[LC + L * C];
+                    }
+                }
+                const float *gr = a.ag + size_t(e) * NG;
+#pragma unroll
+                for (int u = 0; u < HM; ++u) {
+                    const int h = ln.c + W * u;
+                    dm[u] = h < H ? a.dmsg[size_t(i) * H + h] : 0.0f;
+                    sg[u] = h < H ? gr[h / gw] : 0.0f;
+                }
+            } else {
+                zero(dm);
             }
+        };
+        int e;
+        float DH[NQ], Y[NQ], tT[LQ], tI[LQ], dm[HM], sg[HM], fc;
+        fetch(ln.slot, e, DH, Y, tT, tI, dm, sg, fc);
+        for (int q0 = 0; q0 < cnt; q0 += S) {
+            int en;
+            float DHn[NQ], Yn[NQ], tTn[LQ], tIn[LQ], dmn[HM], sgn[HM], fcn;
+            fetch(q0 + S + ln.slot, en, DHn, Yn, tTn, tIn, dmn, sgn, fcn);
+            const bool on = fc != 0.0f;
+            float *dg = a.dgg + size_t(e >= 0 ? e : 0) * NG;
+            float contrib = 0.0f;
+            if (e >= 0 && ln.act) {
+#pragma unroll
+                for (int L = 1; L <= LQ; ++L) {
+                    const int st = L * L - 1;
+                    float sT = 0.0f, sI = 0.0f;
+                    if (on) {
+#pragma unroll
+                        for (int m = 0; m < 2 * L + 1; ++m) {
+                            sT += DH[st + m] * MX[st + m];
+                            sI += DH[st + m] * Y[st + m];
+                        }
+                    }
+                    const float t1 = on ? tT[L - 1] : 0.0f, t2 = on ? tI[L - 1] : 0.0f;
+                    dg[G + (L - 1) * C + ln.c] = on ? (1.0f - t1 * t1) * fc * sT : 0.0f;
+                    dg[G + LC + (L - 1) * C + ln.c] = on ? (1.0f - t2 * t2) * fc * sI : 0.0f;
+                    if (on) {
+                        contrib += t1 * sT + t2 * sI;
+#pragma unroll
+                        for (int m = 0; m < 2 * L + 1; ++m) acc[st + m] += fc * t1 * DH[st + m];
+                    }
+                }
+            }
+            if (on) {
+#pragma unroll
+                for (int u = 0; u < HM; ++u) vacc[u] += sg[u] * fc * dm[u];
+            }
+            // group gates: P_g, dE/dgate_g = P_g fc s (1 - s), dE/dfc += P_g s
+            if (gmode == 0) {
+#pragma unroll
+                for (int u = 0; u < HM; ++u) {
+                    if (W * u < H) {
+                        const float P = group_sum(dm[u] * Vj[u], gw);
+                        const int h = ln.c + W * u;
+                        if (e >= 0 && h < H && h % gw == 0) {
+                            const float s = on ? sg[u] : 0.0f;
+                            dg[h / gw] = on ? P * fc * s * (1.0f - s) : 0.0f;
+                            if (on) contrib += P * s;
+                        }
+                    }
+                }
+            } else if (gmode == 1) {
+                const int per = gw / W;
+                float run = 0.0f;
+#pragma unroll
+                for (int u = 0; u < HM; ++u) {
+                    if (W * u < H) {
+                        run += dm[u] * Vj[u];
+                        if ((u + 1) % per == 0) {
+                            const float P = group_sum(run, W);
+                            if (e >= 0 && ln.c == 0) {
+                                const float s = on ? sg[u] : 0.0f;
+                                dg[(W * u) / gw] = on ? P * fc * s * (1.0f - s) : 0.0f;
+                                if (on) contrib += P * s;
+                            }
+                            run = 0.0f;
+                        }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < HM; ++u) {
+                    const int h = ln.c + W * u;
+                    if (h < H) T[h] = dm[u] * Vj[u];
+                }
+                wave_sync();
+                if (e >= 0) {
+                    for (int g = ln.c; g < G; g += W) {
+                        float P = 0.0f;
+                        for (int h = g * gw; h < (g + 1) * gw; ++h) P += T[h];
+                        const float s = on ? a.ag[size_t(e) * NG + g] : 0.0f;
+                        dg[g] = on ? P * fc * s * (1.0f - s) : 0.0f;
+                        if (on) contrib += P * s;
+                    }
+                }
+                wave_sync();
+            }
+            contrib = group_sum(contrib, W);
+            if (on && ln.c == 0) a.dv[e].w += contrib * cutoff_slope(a.r.vec[e].w, a.cutoff);
+            e = en;
+            copy(DH, DHn);
+            copy(Y, Yn);
+            copy(tT, tTn);
+            copy(tI, tIn);
+            copy(dm, dmn);
+            copy(sg, sgn);
+            fc = fcn;
         }
     }
+    fold_slots<S>(acc);
+    fold_slots<S>(vacc);
+    if (ln.slot == 0) {
+        if (ln.act) store_row(acc, a.dmix + size_t(j) * CN + ln.c * NQ);
 #pragma unroll
-    for (int q = 0; q < kMaxOut; ++q) {
-        int o = lane + kWave * q;
-        if (o < CN) a.dmix[size_t(j) * CN + o] = macc[q];
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        int c = lane + kWave * q;
-        if (c < H) a.dnode[size_t(j) * a.NP + 2 * a.D + c] = vacc[q];
+        for (int u = 0; u < HM; ++u) {
+            const int h = ln.c + W * u;
+            if (h < H) a.dnode[size_t(j) * a.NP + 2 * a.D + h] = vacc[u];
+        }
     }
 }
 
-// Per-atom adjoints: context projections A (own records) and B (as neighbour),
-// and dE/d(dir_in) = identity + probes + channel mix.
-__global__ void __launch_bounds__(kWave) k_eq_atom_backward(EqArgs a) {
+// Per-atom adjoints of the edge features, from both sides of each record:
+//   dE/dA_n, dE/dB_n (context projections: sums of dE/du over the records of
+//   n as centre / as neighbour), dE/d(dir_in)_n = dHt_n + probe adjoints
+//   (+ the channel-mix adjoint that k_eq_mix already wrote to ddir_in), and
+//   dE/dY of each record: the centre side adds fc tI dHt_i + dprobe_c H_i,
+//   the neighbour side (-1)^L dprobe_n H_j, each into its own buffer.  The
+//   channel sums of the dE/dY shares go through a per-wave LDS tile.
+template <int LQ, int S>
+__global__ void __launch_bounds__(kBlock) k_eq_atom_backward(EqArgs a) {
+    constexpr int NQ = LQ * (LQ + 2), LD = NQ + 1;
+    using Ln = Lanes<S>;
+    constexpr int HM = Ln::HM, W = Ln::W;
     extern __shared__ float lds[];
-    const int C = a.C, nq = a.nq, lq = a.lq, LC = lq * C, CN = C * nq, D = a.D;
-    float *dxL = lds;          // [LC] probe adjoints of the current record
-    float *Yl = dxL + LC;      // [nq]
-    float *dmixL = Yl + nq;    // [CN]
-    const int n = blockIdx.x, lane = threadIdx.x;
-    float sa[4] = {0, 0, 0, 0}, sb[4] = {0, 0, 0, 0};
-    float g[kMaxOut];
-    int col[kMaxOut], kk[kMaxOut], LL[kMaxOut];
-#pragma unroll
-    for (int t = 0; t < kMaxOut; ++t) {
-        int o = lane + kWave * t;
-        int c = o / nq, k = o - c * nq, L = o < CN ? order_of(k) : 1;
-        kk[t] = k;
-        LL[t] = L;
-        col[t] = (L - 1) * C + c;
-        g[t] = o < CN ? a.dht[size_t(n) * CN + o] : 0.0f;
+    const int n = wave_atom(a.r);
+    if (n < 0) return;
+    const Ln ln(a.C);
+    float *T = lds + (threadIdx.x >> 6) * kWave * LD;
+    const int C = a.C, CN = C * NQ, LC = LQ * C, D = a.D, kb = a.kb, G = a.G, NG = a.NG;
+    float Hn[NQ], DHn[NQ], g[NQ];
+    zero(Hn);
+    zero(DHn);
+    zero(g);
+    if (ln.act) {
+        load_row(Hn, a.dir_in + size_t(n) * CN + ln.c * NQ);
+        load_row(DHn, a.dht + size_t(n) * CN + ln.c * NQ);
     }
-    float dun[4], dxn[4], yn = 0.0f;
-    auto fetch = [&](int e, int off) {
+    float sd[2][HM];
+    zero(sd[0]);
+    zero(sd[1]);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            int c = lane + kWave * q;
-            dun[q] = c < D ? a.due[size_t(e) * D + c] : 0.0f;
-            dxn[q] = c < LC ? a.dx[size_t(e) * a.ldx + a.kb + off + c] : 0.0f;
-        }
-        yn = lane < nq ? a.harm[size_t(e) * nq + lane] : 0.0f;
-    };
-    // own records: dA, probes_c adjoint (sign +1); records as neighbour: dB,
-    // probes_n adjoint (sign (-1)^L)
     for (int side = 0; side < 2; ++side) {
         const int b0 = side ? a.r.tptr[n] : a.r.view[4 * n];
         const int b1 = side ? a.r.tptr[n + 1] : a.r.view[4 * n + 1];
-        for (int c0 = b0; c0 < b1; c0 += kWave) {
-            const int cnt = min(kWave, b1 - c0);
-            int me = 0;
+        float *dyo = side ? a.dyn : a.dy;
+        for (int t0 = b0; t0 < b1; t0 += kWave) {
+            const int cnt = min(kWave, b1 - t0);
+            int me = -1;
             float mf = 0.0f;
-            if (lane < cnt) {
-                me = side ? a.r.tidx[c0 + lane] : c0 + lane;
-                mf = a.fc[me];
+            if (ln.lane < cnt) {
+                me = side ? a.r.tidx[t0 + ln.lane] : t0 + ln.lane;
+                mf = side ? a.tfc[t0 + ln.lane] : a.fc[t0 + ln.lane];
             }
-            fetch(lane_i(me, 0), side * LC);
-            for (int u = 0; u < cnt; ++u) {
-                const float fc = lane_f(mf, u);
-                __syncthreads();
+            auto fetch = [&](int q, int &e, float (&y)[NQ], float (&dxv)[LQ], float (&ti)[LQ],
+                             float (&du)[HM], float &f) {
+                e = bcast(me, min(q, kWave - 1));
+                f = bcast(mf, min(q, kWave - 1));
+                if (q >= cnt) {
+                    e = -1;
+                    f = 0.0f;
+                }
+                if (f != 0.0f) {
+                    if (ln.act) {
+                        load_row(y, a.harm + size_t(e) * NQ);
+                        const float *d = a.dx + size_t(e) * a.ldx + kb + side * LC + ln.c;
+                        const float *gr = a.ag + size_t(e) * NG + G + LC + ln.c;
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    if (lane + kWave * q < LC) dxL[lane + kWave * q] = dxn[q];
-                if (lane < nq) Yl[lane] = yn;
-                float du[4];
+                        for (int L = 0; L < LQ; ++L) {
+                            dxv[L] = d[L * C];
+                            ti[L] = side ? 0.0f : gr[L * C];
+                        }
+                    }
 #pragma unroll
-                for (int q = 0; q < 4; ++q) du[q] = dun[q];
-                __syncthreads();
-                if (u + 1 < cnt) fetch(lane_i(me, u + 1), side * LC);
-                if (fc == 0.0f) continue;
+                    for (int u = 0; u < HM; ++u) {
+                        const int dd = ln.c + W * u;
+                        du[u] = dd < D ? a.due[size_t(e) * D + dd] : 0.0f;
+                    }
+                }
+            };
+            int e;
+            float Y[NQ], dxv[LQ], tI[LQ], du[HM], fc;
+            fetch(ln.slot, e, Y, dxv, tI, du, fc);
+            for (int q0 = 0; q0 < cnt; q0 += S) {
+                int en;
+                float Yn[NQ], dxn[LQ], tIn[LQ], dun[HM], fcn;
+                fetch(q0 + S + ln.slot, en, Yn, dxn, tIn, dun, fcn);
+                const bool on = fc != 0.0f;
+                if (on) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    if (side)
-                        sb[q] += du[q];
-                    else
-                        sa[q] += du[q];
+                    for (int u = 0; u < HM; ++u) sd[side][u] += du[u];
                 }
 #pragma unroll
-                for (int t = 0; t < kMaxOut; ++t)
-                    if (lane + kWave * t < CN) {
-                        float v = dxL[col[t]] * Yl[kk[t]];
-                        g[t] += (side && (LL[t] & 1)) ? -v : v;
+                for (int L = 1; L <= LQ; ++L)
+#pragma unroll
+                    for (int m = 0; m < 2 * L + 1; ++m) {
+                        const int k = L * L - 1 + m;
+                        float yv = 0.0f;
+                        if (on && ln.act) {
+                            const float v = dxv[L - 1] * Y[k];
+                            g[k] += (side && (L & 1)) ? -v : v;
+                            yv = dxv[L - 1] * Hn[k];
+                            if (side)
+                                yv = (L & 1) ? -yv : yv;
+                            else
+                                yv = fc * tI[L - 1] * DHn[k] + yv;
+                        }
+                        T[ln.lane * LD + k] = yv;
                     }
+                wave_sync();
+                if (on) {
+                    for (int k = ln.c; k < NQ; k += W) {
+                        float s = 0.0f;
+                        for (int c = 0; c < C; ++c) s += T[(ln.slot * W + c) * LD + k];
+                        dyo[size_t(e) * NQ + k] += s;
+                    }
+                }
+                wave_sync();
+                e = en;
+                copy(Y, Yn);
+                copy(dxv, dxn);
+                copy(tI, tIn);
+                copy(du, dun);
+                fc = fcn;
             }
         }
     }
+    fold_slots<S>(g);
+    fold_slots<S>(sd[0]);
+    fold_slots<S>(sd[1]);
+    if (ln.slot == 0) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        int c = lane + kWave * q;
-        if (c < D) {
-            a.dnode[size_t(n) * a.NP + c] = sa[q];
-            a.dnode[size_t(n) * a.NP + D + c] = sb[q];
+        for (int u = 0; u < HM; ++u) {
+            const int dd = ln.c + W * u;
+            if (dd < D) {
+                a.dnode[size_t(n) * a.NP + dd] = sd[0][u];
+                a.dnode[size_t(n) * a.NP + D + dd] = sd[1][u];
+            }
         }
-    }
-    // channel mix adjoint: dH[c][k] += sum_c' M_L[c'][c] dMIX[c'][k]
-    __syncthreads();
-    for (int o = lane; o < CN; o += kWave) dmixL[o] = a.dmix[size_t(n) * CN + o];
-    __syncthreads();
+        if (ln.act) {
+            float mx[NQ];
+            float *out = a.ddir_in + size_t(n) * CN + ln.c * NQ;
+            load_row(mx, out);
 #pragma unroll
-    for (int t = 0; t < kMaxOut; ++t) {
-        int o = lane + kWave * t;
-        if (o >= CN) continue;
-        int c = col[t] - (LL[t] - 1) * C;
-        const float *M = a.mixw + size_t(LL[t] - 1) * C * C + c;
-        float s = 0.0f;
-        for (int cc = 0; cc < C; ++cc) s += M[cc * C] * dmixL[cc * nq + kk[t]];
-        a.ddir_in[size_t(n) * CN + o] = g[t] + s;
+            for (int k = 0; k < NQ; ++k) DHn[k] = (DHn[k] + g[k]) + mx[k];
+            store_row(DHn, out);
+        }
     }
 }
 
-// dE/dY of the records of centre i: the injected direction term
-// fc tI[L,c] dHt_i[c][k] and the probes of the centre and neighbour states.
-__global__ void __launch_bounds__(kWave) k_eq_probe_dy(EqArgs a) {
-    extern __shared__ float lds[];
-    const int C = a.C, nq = a.nq, LC = a.lq * C, CN = C * nq, G = a.G, NG = a.NG;
-    const int ldc = nq | 1;
-    float *Hi = lds;             // [C][ldc]
-    float *DH = Hi + C * ldc;    // [C][ldc]
-    float *Hj = DH + C * ldc;    // [C][ldc]
-    float *cf = Hj + C * ldc;    // [3 LC] injection gates | centre / neighbour probe adjoints
-    const int i = blockIdx.x, lane = threadIdx.x;
-    int so[kMaxOut];
-#pragma unroll
-    for (int t = 0; t < kMaxOut; ++t) {
-        int o = lane + kWave * t;
-        so[t] = o < CN ? (o / nq) * ldc + o % nq : -1;
-        if (so[t] >= 0) {
-            Hi[so[t]] = a.dir_in[size_t(i) * CN + o];
-            DH[so[t]] = a.dht[size_t(i) * CN + o];
-        }
-    }
-    // contraction layout: component k = lane % nq, channels c = cg, cg + ncg, ...
-    const int ncg = kWave / nq, k = lane % nq, cg = lane / nq, L = order_of(k);
-    float hn[kMaxOut], cn[kMaxOut];
-    auto fetch = [&](int e, int j) {
-#pragma unroll
-        for (int t = 0; t < kMaxOut; ++t)
-            hn[t] = so[t] >= 0 ? a.dir_in[size_t(j) * CN + lane + kWave * t] : 0.0f;
-#pragma unroll
-        for (int t = 0; t < kMaxOut; ++t) {
-            int q = lane + kWave * t;
-            float v = 0.0f;
-            if (q < LC)
-                v = a.ag[size_t(e) * NG + G + LC + q];
-            else if (q < 3 * LC)
-                v = a.dx[size_t(e) * a.ldx + a.kb + q - LC];
-            cn[t] = v;
-        }
-    };
-    const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
-    for (int c0 = rb; c0 < re; c0 += kWave) {
-        const int cnt = min(kWave, re - c0);
-        int mj = 0;
-        float mf = 0.0f;
-        if (lane < cnt) {
-            mj = a.r.nbr[c0 + lane];
-            mf = a.fc[c0 + lane];
-        }
-        fetch(c0, lane_i(mj, 0));
-        for (int u = 0; u < cnt; ++u) {
-            const int e = c0 + u;
-            const float fc = lane_f(mf, u);
-            __syncthreads();
-#pragma unroll
-            for (int t = 0; t < kMaxOut; ++t) {
-                if (so[t] >= 0) Hj[so[t]] = hn[t];
-                if (lane + kWave * t < 3 * LC) cf[lane + kWave * t] = cn[t];
-            }
-            __syncthreads();
-            if (u + 1 < cnt) fetch(e + 1, lane_i(mj, u + 1));
-            if (fc == 0.0f) continue;
-            float y = 0.0f;
-            if (cg < ncg) {
-                const float *ti = cf + (L - 1) * C, *dc = ti + LC, *dn = ti + 2 * LC;
-                float yi = 0.0f, yc = 0.0f, yn = 0.0f;
-                for (int c = cg; c < C; c += ncg) {
-                    yi += ti[c] * DH[c * ldc + k];
-                    yc += dc[c] * Hi[c * ldc + k];
-                    yn += dn[c] * Hj[c * ldc + k];
-                }
-                y = fc * yi + yc + ((L & 1) ? -yn : yn);
-            }
-            for (int s2 = 1; s2 < ncg; ++s2) {
-                float v = __shfl(y, min(lane + s2 * nq, kWave - 1), kWave);
-                if (cg == 0) y += v;
-            }
-            if (cg == 0) a.dy[size_t(e) * nq + k] += y;
-        }
-    }
+__global__ void k_gather_f(int64_t E, const int32_t *idx, const float *src, float *dst) {
+    int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t < E) dst[t] = src[idx[t]];
 }
 
 __global__ void __launch_bounds__(kWave) k_eq_encoder_backward(const float *ddir0,
@@ -690,7 +791,8 @@ __global__ void __launch_bounds__(kWave) k_eq_encoder_backward(const float *ddir
 
 // dE/du of the harmonics: sum_k dY_k scale_k db_k/du, added to dv.xyz.
 __global__ void k_eq_harmonic_backward(int64_t E, Records r, const float *fcv, const float *dy,
-                                       const float *ztab, EdgeZ zoff, int lq, int nq,
+                                       const float *dyn, const float *ztab, EdgeZ zoff, int lq,
+                                       int nq,
                                        const float *scale, float4 *dv) {
     int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (e >= E) return;
@@ -708,7 +810,7 @@ __global__ void k_eq_harmonic_backward(int64_t E, Records r, const float *fcv, c
         wr[k] = wr[k - 1] * x - wi[k - 1] * y;
         wi[k] = wr[k - 1] * y + wi[k - 1] * x;
     }
-    const float *g = dy + size_t(e) * nq;
+    const float *g = dy + size_t(e) * nq, *g2 = dyn + size_t(e) * nq;
     float dx = 0.0f, dyy = 0.0f, dz = 0.0f;
     int idx = 0;
     for (int L = 1; L <= lq; ++L) {
@@ -720,7 +822,7 @@ __global__ void k_eq_harmonic_backward(int64_t E, Records r, const float *fcv, c
                 if (q > 0) zfp += float(q) * Z[q] * zp[q - 1];
             }
             for (int part = 0; part < (n1 == 0 ? 1 : 2); ++part, ++idx) {
-                float w = g[idx] * scale[idx];
+                float w = (g[idx] + g2[idx]) * scale[idx];
                 if (n1 == 0) {
                     dz += w * zfp;
                 } else if (part == 0) {
@@ -750,16 +852,65 @@ __global__ void k_eq_harmonic_backward(int64_t E, Records r, const float *fcv, c
 
 static void expect(ModelImpl &m, const std::string &name, int64_t n) { m.expected[name] = n; }
 
+// Records per wave in the angular-state loops: slots of 64 / S lanes hold
+// one channel per lane.
+static int eq_slots(int C) { return C > 32 ? 1 : C > 16 ? 2 : 4; }
+
+// Launches kernel template k<LQ> for the runtime order lq (1..7).
+#define EQ_LAUNCH(k, lq, grid, block, lds, s, ...)                                         \
+    do {                                                                                  \
+        switch (lq) {                                                                     \
+        case 1: hipLaunchKernelGGL(k<1>, grid, block, lds, s, __VA_ARGS__); break;        \
+        case 2: hipLaunchKernelGGL(k<2>, grid, block, lds, s, __VA_ARGS__); break;        \
+        case 3: hipLaunchKernelGGL(k<3>, grid, block, lds, s, __VA_ARGS__); break;        \
+        case 4: hipLaunchKernelGGL(k<4>, grid, block, lds, s, __VA_ARGS__); break;        \
+        case 5: hipLaunchKernelGGL(k<5>, grid, block, lds, s, __VA_ARGS__); break;        \
+        case 6: hipLaunchKernelGGL(k<6>, grid, block, lds, s, __VA_ARGS__); break;        \
+        default: hipLaunchKernelGGL(k<7>, grid, block, lds, s, __VA_ARGS__); break;       \
+        }                                                                                 \
+        RUNE_HIP_CHECK(hipGetLastError());                                                \
+    } while (0)
+
+#define EQ_CASE_S(k, L, S, ...)                                                           \
+    case S: hipLaunchKernelGGL((k<L, S>), __VA_ARGS__); break;
+#define EQ_CASE_L(k, L, S, ...)                                                           \
+    case L:                                                                               \
+        switch (S) {                                                                      \
+        EQ_CASE_S(k, L, 1, __VA_ARGS__)                                                   \
+        EQ_CASE_S(k, L, 2, __VA_ARGS__)                                                   \
+        default: hipLaunchKernelGGL((k<L, 4>), __VA_ARGS__); break;                       \
+        }                                                                                 \
+        break;
+// Launches kernel template k<LQ, S> of the per-atom record loops.
+#define EQ_LAUNCH_S(k, lq, S, ...)                                                         \
+    do {                                                                                  \
+        switch (lq) {                                                                     \
+        EQ_CASE_L(k, 1, S, __VA_ARGS__)                                                   \
+        EQ_CASE_L(k, 2, S, __VA_ARGS__)                                                   \
+        EQ_CASE_L(k, 3, S, __VA_ARGS__)                                                   \
+        EQ_CASE_L(k, 4, S, __VA_ARGS__)                                                   \
+        EQ_CASE_L(k, 5, S, __VA_ARGS__)                                                   \
+        EQ_CASE_L(k, 6, S, __VA_ARGS__)                                                   \
+        EQ_CASE_L(k, 7, S, __VA_ARGS__)                                                   \
+        }                                                                                 \
+        RUNE_HIP_CHECK(hipGetLastError());                                                \
+    } while (0)
+
 void validate_equivariant(ModelImpl &m) {
     const rune_model_config &c = m.cfg;
     const int lq = c.equivariant_l_max, C = c.equivariant_channels;
     RUNE_REQUIRE(lq >= 1 && lq <= std::min(c.l_max, 7), RUNE_ERR_ARGUMENT,
                  "equivariant blocks support equivariant_l_max in 1..min(l_max, 7)");
-    RUNE_REQUIRE(C >= 1 && C * lq * (lq + 2) <= kWave * kMaxOut, RUNE_ERR_ARGUMENT,
-                 "equivariant_channels * l(l+2) must not exceed 768");
-    RUNE_REQUIRE(c.message_groups <= kWave, RUNE_ERR_ARGUMENT, "message_groups must be <= 64");
+    RUNE_REQUIRE(C >= 1 && C <= kWave, RUNE_ERR_ARGUMENT,
+                 "equivariant blocks support equivariant_channels in 1..64");
+    RUNE_REQUIRE(c.message_groups >= 1 && c.message_groups <= kWave, RUNE_ERR_ARGUMENT,
+                 "message_groups must be in 1..64");
+    RUNE_REQUIRE(c.hidden_dim <= 4 * kWave, RUNE_ERR_ARGUMENT,
+                 "equivariant blocks support hidden_dim <= 256");
     RUNE_REQUIRE(c.message_dim <= 4 * kWave, RUNE_ERR_ARGUMENT,
                  "equivariant blocks support message_dim <= 256");
+    RUNE_REQUIRE(c.hidden_dim % c.message_groups == 0, RUNE_ERR_ARGUMENT,
+                 "hidden_dim must be divisible by message_groups");
 }
 
 void define_expected_equivariant(ModelImpl &m) {
@@ -931,10 +1082,12 @@ MessagePlan plan_equivariant(ModelImpl &m, Arena &ar, int N, int64_t E) {
     p.o_dmom = ar.add(4 * n * m.desc.na * m.desc.nlm);
     p.i_rb = p.add(ar, 4 * e * p.ldrb);
     p.i_fc = p.add(ar, 4 * e);
+    p.i_tfc = p.add(ar, 4 * e);
     p.i_pair = p.add(ar, 4 * e);
     p.i_dv = p.add(ar, 16 * e);
     p.i_harm = p.add(ar, 4 * e * nq);
     p.i_dharm = p.add(ar, 4 * e * nq);
+    p.i_dharm_n = p.add(ar, 4 * e * nq);
     int dir0 = p.add(ar, 4 * n * CN);
     int x = p.add(ar, 4 * e * ldx);        // shared by the blocks (forward only)
     int eh = p.add(ar, 4 * e * D);         // shared
@@ -993,9 +1146,16 @@ static EqArgs eq_args(ModelImpl &m, MessagePlan &p, const Records &r, int b) {
     a.ldx = p.ldrb_x;
     a.na = m.desc.na;
     a.nlm = m.desc.nlm;
+    a.S = eq_slots(a.C);
+    {
+        const int W = kWave / a.S, gw = a.H / a.G;
+        const bool pow2 = (gw & (gw - 1)) == 0;
+        a.gmode = (pow2 && gw <= W) ? 0 : (gw % W == 0 ? 1 : 2);
+    }
     a.eps = float(c.norm_eps);
     a.cutoff = float(c.message_cutoff);
     a.fc = p.at(p.i_fc);
+    a.tfc = p.at(p.i_tfc);
     a.harm = p.at(p.i_harm);
     a.rb = p.at(p.i_rb);
     a.ldrb = p.ldrb;
@@ -1015,6 +1175,7 @@ static EqArgs eq_args(ModelImpl &m, MessagePlan &p, const Records &r, int b) {
     a.dgg = p.at(p.t_dgv);
     a.dv = reinterpret_cast<float4 *>(p.at(p.i_dv));
     a.dy = p.at(p.i_dharm);
+    a.dyn = p.at(p.i_dharm_n);
     a.dnode = p.at(p.t_dvs);
     a.dmix = p.at(p.t_dmix);
     a.due = p.at(p.t_due);
@@ -1031,8 +1192,15 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
     const int N = p.N, H = c.hidden_dim, D = c.message_dim, act = c.activation;
     const int lq = c.equivariant_l_max, C = c.equivariant_channels, nq = lq * (lq + 2);
     const int64_t E = p.E;
+    const int atom_grid = ceil_div(N, kWaves), mix_grid = std::max(1, std::min(N, 2048));
+    const size_t mix_lds = sizeof(float) * (size_t(lq) * C * C + size_t(C) * nq);
     edge_prep(m, p, r, types, s, p.at(p.i_harm), m.harm_scale, lq, nq);
-    if (E > 0) RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dharm), 0, 4 * size_t(E) * nq, s));
+    if (E > 0) {
+        hipLaunchKernelGGL(k_gather_f, dim3(ceil_div(E, 256)), dim3(256), 0, s, E, r.tidx,
+                           p.at(p.i_fc), p.at(p.i_tfc));
+        RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dharm), 0, 4 * size_t(E) * nq, s));
+        RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dharm_n), 0, 4 * size_t(E) * nq, s));
+    }
     hipLaunchKernelGGL(k_eq_encode, dim3(N), dim3(kWave), 0, s, N, moments, m.desc.na,
                        m.desc.nlm, m.enc_w, m.harm_scale, C, nq, p.at(p.blocks[0].dir_in));
     RUNE_HIP_CHECK(hipGetLastError());
@@ -1045,12 +1213,11 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
         Epilogue e0;
         e0.row_scale = p.at(bb.rin);
         gemm(N, w.NP, H, cur, H, w.node_f, H, p.at(bb.vs), w.NP, e0, s);
-        hipLaunchKernelGGL(k_eq_mix, dim3(N), dim3(kWave), 0, s, w.mix, p.at(bb.dir_in), C, nq,
-                           p.at(bb.mixstate));
+        EQ_LAUNCH(k_eq_mix, lq, dim3(mix_grid), dim3(256), mix_lds, s, N, w.mix,
+                  p.at(bb.dir_in), C, 0, p.at(bb.mixstate));
         if (E > 0) {
-            hipLaunchKernelGGL(k_eq_features, dim3(N), dim3(kWave),
-                               sizeof(float) * (2 * C * (nq | 1) + nq), s, a);
-            RUNE_HIP_CHECK(hipGetLastError());
+            EQ_LAUNCH_S(k_eq_features, lq, a.S, dim3(atom_grid), dim3(kBlock),
+                        sizeof(float) * kBlock * (nq + (nq % 4 == 0 ? 4 : 1)), s, a);
             Epilogue e1;
             e1.gtab[0] = p.at(bb.vs);
             e1.gidx[0] = r.ctr;
@@ -1073,9 +1240,7 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
             e2.act2 = RUNE_ACT_TANH;
             gemm(int(E), w.NG, D, p.at(bb.eh), D, w.gate, D, p.at(bb.gv), w.NG, e2, s);
         }
-        hipLaunchKernelGGL(k_eq_aggregate, dim3(N), dim3(kWave),
-                           sizeof(float) * (C * nq + w.NG + nq), s, a);
-        RUNE_HIP_CHECK(hipGetLastError());
+        EQ_LAUNCH_S(k_eq_aggregate, lq, a.S, dim3(atom_grid), dim3(kBlock), 0, s, a);
         const int NU = H + lq * C;
         Epilogue e3;
         e3.bias = w.up1_b;
@@ -1103,8 +1268,10 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
     const rune_model_config &c = m.cfg;
     const int N = p.N, H = c.hidden_dim, D = c.message_dim, act = c.activation;
     const int lq = c.equivariant_l_max, C = c.equivariant_channels, nq = lq * (lq + 2);
-    const int CN = C * nq, NU = H + lq * C;
+    const int NU = H + lq * C;
     const int64_t E = p.E;
+    const int atom_grid = ceil_div(N, kWaves), mix_grid = std::max(1, std::min(N, 2048));
+    const size_t mix_lds = sizeof(float) * (size_t(lq) * C * C + size_t(C) * nq);
     float *cur = dh;
     const float *ddir_out = nullptr;   // the last block's states feed only its invariants
     float *ddir_in = p.at(p.t_ddir0);
@@ -1122,11 +1289,11 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         Epilogue e1;
         gemm(N, NU, D, p.at(p.t_dz1), D, w.up1_fT, D, p.at(p.t_duin), NU, e1, s);
         hipLaunchKernelGGL(k_eq_node_backward, dim3(N), dim3(kWave), 0, s, a);
-        size_t lds = sizeof(float) * (2 * C * (nq | 1) + H + w.NG + nq);
-        hipLaunchKernelGGL(k_eq_edge_backward, dim3(N), dim3(kWave), lds, s, a);
-        hipLaunchKernelGGL(k_eq_neighbor_backward, dim3(N), dim3(kWave), sizeof(float) * w.NG,
-                           s, a);
-        RUNE_HIP_CHECK(hipGetLastError());
+        EQ_LAUNCH_S(k_eq_pair_backward, lq, a.S, dim3(atom_grid), dim3(kBlock),
+                    a.gmode == 2 ? sizeof(float) * kWaves * a.S * H : 0, s, a);
+        // channel-mix adjoint M^T dmix, completed by k_eq_atom_backward
+        EQ_LAUNCH(k_eq_mix, lq, dim3(mix_grid), dim3(256), mix_lds, s, N, w.mix, a.dmix, C, 1,
+                  a.ddir_in);
         if (E > 0) {
             Epilogue e2;
             e2.dact_from = p.at(bb.ue);
@@ -1137,12 +1304,8 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
             gemm(int(E), w.KX, D, p.at(p.t_due), D, w.edge_xT, D, p.at(p.t_dx), a.ldx, e3, s);
             edge_rb_backward(m, p, r, p.at(p.t_dx), a.ldx, s);
         }
-        const int LC = lq * C;
-        hipLaunchKernelGGL(k_eq_atom_backward, dim3(N), dim3(kWave),
-                           sizeof(float) * (LC + nq + CN), s, a);
-        hipLaunchKernelGGL(k_eq_probe_dy, dim3(N), dim3(kWave),
-                           sizeof(float) * (3 * C * (nq | 1) + 3 * LC), s, a);
-        RUNE_HIP_CHECK(hipGetLastError());
+        EQ_LAUNCH_S(k_eq_atom_backward, lq, a.S, dim3(atom_grid), dim3(kBlock),
+                    sizeof(float) * kBlock * (nq + 1), s, a);
         Epilogue e4;
         gemm(N, H, w.NP, p.at(p.t_dvs), w.NP, w.node_fT, w.NP, p.at(p.t_dz), H, e4, s);
         float *next = (cur == p.at(p.t_dh0)) ? p.at(p.t_dh1) : p.at(p.t_dh0);
@@ -1158,7 +1321,8 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         EdgeZ zo;
         for (int k = 0; k < kMaxL + 2; ++k) zo.off[k] = m.desc.z_off[k];
         hipLaunchKernelGGL(k_eq_harmonic_backward, dim3(ceil_div(E, 256)), dim3(256), 0, s, E, r,
-                           p.at(p.i_fc), p.at(p.i_dharm), m.desc.z, zo, lq, nq, m.harm_scale,
+                           p.at(p.i_fc), p.at(p.i_dharm), p.at(p.i_dharm_n), m.desc.z, zo,
+                           lq, nq, m.harm_scale,
                            reinterpret_cast<float4 *>(p.at(p.i_dv)));
     }
     RUNE_HIP_CHECK(hipGetLastError());

@@ -56,9 +56,11 @@ struct Records {
     const float4 *vec;            // [E] {x, y, z, |r|}
     const int32_t *tptr;          // [N+1]
     const int32_t *tidx;          // [E]
+    const int32_t *tctr;          // [E] centre of transposed record t
     const int32_t *ctr;           // [E] centre of each record
     const int32_t *sptr;          // [B+1]
     int n_structures;
+    const int32_t *order;         // [N] spatially coherent processing order, or null
 };
 
 // ---- descriptor (descriptor.hip) ----

@@ -335,9 +335,11 @@ static Records records_of(const rune_nlist *nl) {
     r.vec = nl->vec.as<float4>();
     r.tptr = nl->tptr.as<int32_t>();
     r.tidx = nl->tidx.as<int32_t>();
+    r.tctr = nl->tctr.as<int32_t>();
     r.ctr = nl->ctr.as<int32_t>();
     r.sptr = nl->sptr.as<int32_t>();
     r.n_structures = nl->n_structures;
+    r.order = nl->has_order ? nl->order.as<int32_t>() : nullptr;
     return r;
 }
 

@@ -87,6 +87,23 @@ __global__ void fill_bins(int n, const int32_t *atom_bin, const int32_t *bin_sta
     bin_atoms[bin_start[b] + slot] = i;
 }
 
+// Atoms listed bin by bin in the rank order perm (bins of all structures):
+// rank_count[r] = atoms of bin perm[r], then (after a scan) the copy.
+__global__ void rank_counts(int nbins, const int32_t *perm, const int32_t *bin_count,
+                            int32_t *rank_count) {
+    int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r < nbins) rank_count[r] = bin_count[perm[r]];
+}
+
+__global__ void order_atoms(int nbins, const int32_t *perm, const int32_t *bin_start,
+                            const int32_t *bin_count, const int32_t *rank_start,
+                            const int32_t *bin_atoms, int32_t *order) {
+    int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= nbins) return;
+    const int b = perm[r], src = bin_start[b], dst = rank_start[r];
+    for (int q = 0; q < bin_count[b]; ++q) order[dst + q] = bin_atoms[src + q];
+}
+
 // Exact fp64 squared distance of image (j, S) seen from i.
 __device__ inline double pair_d2(const double *pos, const Geo &g, int i, int j, const int *S,
                                  double *v) {
@@ -294,6 +311,13 @@ __global__ void fill_in(int64_t e, const int32_t *nbr, const int32_t *tptr, int3
     tidx[tptr[a] + slot] = int(r);
 }
 
+// Centre of each transposed record (tctr[t] = ctr[tidx[t]]).
+__global__ void transpose_centres(int64_t e, const int32_t *tidx, const int32_t *ctr,
+                                  int32_t *tctr) {
+    int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t < e) tctr[t] = ctr[tidx[t]];
+}
+
 __global__ void sort_in(int n, const int32_t *tptr, int32_t *tidx) {
     int a = blockIdx.x * blockDim.x + threadIdx.x;
     if (a >= n) return;
@@ -335,6 +359,30 @@ void cross(const double *a, const double *b, double *o) {
 }
 
 double norm3(const double *a) { return std::sqrt(a[0] * a[0] + a[1] * a[1] + a[2] * a[2]); }
+
+// Spreads the low 10 bits of v to every third bit.
+static uint32_t spread3(uint32_t v) {
+    v &= 0x3ff;
+    v = (v | (v << 16)) & 0x030000ff;
+    v = (v | (v << 8)) & 0x0300f00f;
+    v = (v | (v << 4)) & 0x030c30c3;
+    v = (v | (v << 2)) & 0x09249249;
+    return v;
+}
+
+// Flat bin ids of one structure in Morton (Z-curve) order of their cell
+// coordinates: consecutive ranks are spatially compact at every scale.
+static void morton_bins(const int nb[3], int bin_offset, std::vector<int32_t> &out) {
+    std::vector<std::pair<uint32_t, int32_t>> keys;
+    keys.reserve(size_t(nb[0]) * nb[1] * nb[2]);
+    for (int a = 0; a < nb[0]; ++a)
+        for (int b = 0; b < nb[1]; ++b)
+            for (int c = 0; c < nb[2]; ++c)
+                keys.push_back({spread3(a) | (spread3(b) << 1) | (spread3(c) << 2),
+                                bin_offset + (a * nb[1] + b) * nb[2] + c});
+    std::sort(keys.begin(), keys.end());
+    for (const auto &k : keys) out.push_back(k.second);
+}
 
 // Geometry of one structure: bins of width >= rc, stencil reach, capped bin count.
 Geo make_geo(const double *cell_in, const int32_t *pbc, double rc, int n_atoms, int bin_offset,
@@ -415,6 +463,11 @@ void build_transpose(rune_nlist *nl, int32_t *indeg, int32_t *scan_tmp, hipStrea
         hipLaunchKernelGGL(sort_in, dim3(ceil_div(n, kThreads)), dim3(kThreads), 0, s, n,
                            nl->tptr.as<int32_t>(), nl->tidx.as<int32_t>());
     }
+    nl->tctr.reserve(sizeof(int32_t) * std::max<int64_t>(e, 1));
+    if (e > 0)
+        hipLaunchKernelGGL(transpose_centres, dim3(ceil_div(e, kThreads)), dim3(kThreads), 0, s,
+                           e, nl->tidx.as<int32_t>(), nl->ctr.as<int32_t>(),
+                           nl->tctr.as<int32_t>());
     RUNE_HIP_CHECK(hipGetLastError());
 }
 
@@ -520,6 +573,9 @@ extern "C" int rune_nlist_build(rune_nlist *nl, int64_t n_atoms, const double *d
         size_t o_flag = ar.add(16);
         size_t o_scan = ar.add(4 * scan_tmp_ints(std::max(n, total_bins) + 1));
         size_t o_indeg = ar.add(4 * size_t(n + 1));
+        size_t o_perm = ar.add(4 * size_t(total_bins + 1));
+        size_t o_rcnt = ar.add(4 * size_t(total_bins + 1));
+        size_t o_rst = ar.add(4 * size_t(total_bins + 2));
         nl->work.reserve(ar.total);
         char *base = nl->work.as<char>();
         Work w;
@@ -598,6 +654,28 @@ extern "C" int rune_nlist_build(rune_nlist *nl, int64_t n_atoms, const double *d
         }
         RUNE_HIP_CHECK(hipGetLastError());
         build_transpose(nl, w.indeg, w.scan_tmp, s);
+        // processing order: atoms bin by bin, bins in Morton order
+        nl->order.reserve(4 * size_t(std::max(n, 1)));
+        if (n > 0) {
+            std::vector<int32_t> &perm = nl->h_perm;   // outlives the asynchronous upload
+            perm.clear();
+            perm.reserve(total_bins);
+            for (int b = 0; b < n_structures; ++b) morton_bins(geo[b].nb, geo[b].bin_offset, perm);
+            int32_t *d_perm = reinterpret_cast<int32_t *>(base + o_perm);
+            int32_t *rcnt = reinterpret_cast<int32_t *>(base + o_rcnt);
+            int32_t *rst = reinterpret_cast<int32_t *>(base + o_rst);
+            RUNE_HIP_CHECK(hipMemcpyAsync(d_perm, perm.data(), 4 * perm.size(),
+                                          hipMemcpyHostToDevice, s));
+            const int bg = ceil_div(total_bins, kThreads);
+            hipLaunchKernelGGL(rank_counts, dim3(bg), dim3(kThreads), 0, s, total_bins, d_perm,
+                               w.bin_count, rcnt);
+            exclusive_scan(rcnt, rst, total_bins, w.scan_tmp, s);
+            hipLaunchKernelGGL(order_atoms, dim3(bg), dim3(kThreads), 0, s, total_bins, d_perm,
+                               w.bin_start, w.bin_count, rst, w.bin_atoms,
+                               nl->order.as<int32_t>());
+            RUNE_HIP_CHECK(hipGetLastError());
+        }
+        nl->has_order = true;
         if (n_records) *n_records = e;
     });
 }
@@ -614,6 +692,7 @@ extern "C" int rune_nlist_from_padded(rune_nlist *nl, int64_t n_atoms, const flo
         hipStream_t s = as_stream(stream);
         set_structures(nl, n_atoms, n_structures, h_struct_ptr, s);
         nl->from_padded = true;
+        nl->has_order = false;
         const int n = int(n_atoms);
         Arena ar;
         size_t o_cu = ar.add(4 * size_t(n + 1));

@@ -21,7 +21,13 @@ struct rune_nlist {
     // transpose: records whose neighbour is atom a, ascending record id
     rune::DeviceBuffer tptr;     // int32 [N+1]
     rune::DeviceBuffer tidx;     // int32 [E]
+    rune::DeviceBuffer tctr;     // int32 [E] centre of each transposed record
     rune::DeviceBuffer sptr;     // int32 [B+1] device copy of structure ranges
+    // atoms in cell-bin order (spatially coherent processing order); empty
+    // for lists made from padded tensors
+    rune::DeviceBuffer order;    // int32 [N]
+    bool has_order = false;
+    std::vector<int32_t> h_perm; // host bin ranks behind the last order upload
     // working memory of the builder
     rune::DeviceBuffer work;
     rune::DeviceBuffer keys;     // uint64 [E]
