@@ -81,6 +81,19 @@ __device__ inline void load_stage(float4 (&r)[kRows * 8 / 256], const float *__r
     }
 }
 
+// A full K stage (k0 + 32 <= K) of the vector path: no guards.  Rows past
+// nrows read row nrows - 1 instead; their products land only in output rows
+// or columns that the epilogue never stores.
+template <int kRows>
+__device__ inline void load_stage_full(float4 (&r)[kRows * 8 / 256], const float *__restrict__ X,
+                                       int ld, int row0, int nrows, int k0, int tid) {
+#pragma unroll
+    for (int it = 0; it < kRows * 8 / 256; ++it) {
+        int q = tid + 256 * it, row = min(row0 + (q >> 3), nrows - 1), c4 = q & 7;
+        r[it] = *reinterpret_cast<const float4 *>(X + size_t(row) * ld + k0 + 4 * c4);
+    }
+}
+
 template <int kRows>
 __device__ inline void store_stage(const float4 (&r)[kRows * 8 / 256], float *S, int tid) {
 #pragma unroll
@@ -117,16 +130,21 @@ __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *
 #pragma unroll
         for (int b = 0; b < WN; ++b) acc[a][b] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     float4 ra[kBM * 8 / 256], rb[BN * 8 / 256];
-    load_stage<kBM, kVec>(ra, A, lda, m0, M, 0, K, tid);
-    load_stage<BN, kVec>(rb, Bt, ldb, n0, N, 0, K, tid);
+    auto fetch = [&](int k0) {
+        if (kVec && k0 + kBK <= K) {
+            load_stage_full<kBM>(ra, A, lda, m0, M, k0, tid);
+            load_stage_full<BN>(rb, Bt, ldb, n0, N, k0, tid);
+        } else {
+            load_stage<kBM, kVec>(ra, A, lda, m0, M, k0, K, tid);
+            load_stage<BN, kVec>(rb, Bt, ldb, n0, N, k0, K, tid);
+        }
+    };
+    fetch(0);
     for (int k0 = 0; k0 < K; k0 += kBK) {
         store_stage<kBM>(ra, As, tid);
         store_stage<BN>(rb, Bs, tid);
         __syncthreads();
-        if (k0 + kBK < K) {
-            load_stage<kBM, kVec>(ra, A, lda, m0, M, k0 + kBK, K, tid);
-            load_stage<BN, kVec>(rb, Bt, ldb, n0, N, k0 + kBK, K, tid);
-        }
+        if (k0 + kBK < K) fetch(k0 + kBK);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             float4 fa[WM], fb[WN];

@@ -74,7 +74,7 @@ struct EqArgs {
     Records r;
     int H, D, G, C, lq, nq, NG, NP, KX, kb, ldx, na, nlm;
     int S;                    // records in flight per wave (lane slots of 64 / S lanes)
-    int gmode;                // group-sum method of k_eq_pair_backward
+    int gmode;                // group-sum method of k_eq_pair_grp
     float eps, cutoff;
     const float *fc;          // [E]
     const float *tfc;         // [E] fc of transposed record t (fc[tidx[t]])
@@ -96,6 +96,7 @@ struct EqArgs {
     const float *ddir_out;    // [N, C*nq] from later blocks, or null
     float *dgg;               // [E, NG]
     float4 *dv;               // [E]
+    float *dfc;               // [E] dE/dfc of the message terms, all blocks
     float *dy;                // [E, nq] dE/dY, centre-side shares
     float *dyn;               // [E, nq] dE/dY, neighbour-side shares
     float *dnode;             // [N, NP]
@@ -213,12 +214,12 @@ __global__ void __launch_bounds__(256) k_eq_mix(int N, const float *mixw, const 
                                                 int trans, float *out) {
     constexpr int NQ = LQ * (LQ + 2);
     extern __shared__ float lds[];
-    const int CN = C * NQ, CC = C * C;
-    float *Wl = lds;                  // [LQ][c][c'] as applied
-    float *row = lds + LQ * CC;       // [C][NQ] input row of the current atom
+    const int CN = C * NQ, CC = C * C, LW = C + 1;
+    float *Wl = lds;                  // [LQ][c][c'] as applied, rows padded to C + 1
+    float *row = lds + LQ * C * LW;   // [C][NQ] input row of the current atom
     for (int o = threadIdx.x; o < LQ * CC; o += blockDim.x) {
         const int L = o / CC, r = o - L * CC, c = r / C, cc = r - c * C;
-        Wl[o] = trans ? mixw[size_t(L) * CC + cc * C + c] : mixw[o];
+        Wl[(L * C + c) * LW + cc] = trans ? mixw[size_t(L) * CC + cc * C + c] : mixw[o];
     }
     for (int n = blockIdx.x; n < N; n += gridDim.x) {
         __syncthreads();
@@ -226,7 +227,7 @@ __global__ void __launch_bounds__(256) k_eq_mix(int N, const float *mixw, const 
         __syncthreads();
         for (int o = threadIdx.x; o < CN; o += blockDim.x) {
             const int c = o / NQ, k = o - c * NQ;
-            const float *w = Wl + size_t((order_of(k) - 1) * C + c) * C;
+            const float *w = Wl + size_t((order_of(k) - 1) * C + c) * LW;
             float acc = 0.0f;
             for (int cc = 0; cc < C; ++cc) acc += w[cc] * row[cc * NQ + k];
             out[size_t(n) * CN + o] = acc;
@@ -445,49 +446,48 @@ __device__ inline float cutoff_slope(float d, float rc) {
     return -0.5f * kPi / rc * sinf(kPi * d / rc);
 }
 
-// Reverse pass of the messages, walked from the neighbour side: the wave of
-// atom j holds its mixed state M_j and values V_j, gathers the centre's
-// dE/d(dir_out) and dE/dmsg once per record, and produces
-//   the gate adjoints dE/dgate[e, :] and dE/dfc (into dv[e].w),
-//   dE/dM_j = sum_e fc tT[e] dHt_i and dE/dV_j = sum_e fc s_e dmsg_i.
-// Group sums P_g = sum_{h in g} dmsg_i[h] V_j[h] take the lane layout's
-// shuffles (gmode 0: group width divides W; 1: W divides it) or, for other
-// widths, a per-slot LDS row (gmode 2).
+// Reverse pass of the angular messages, walked from the neighbour side: the
+// wave of atom j holds its mixed state M_j, gathers the centre's
+// dE/d(dir_out) once per record and produces the direction-gate adjoints
+// dE/dgate[e, G:], their share of dE/dfc (into dv[e].w) and
+// dE/dM_j = sum_e fc tT[e] dHt_i.  Harmonic rows of a 64-record chunk are
+// staged in LDS with one parallel load.
 template <int LQ, int S>
-__global__ void __launch_bounds__(kBlock) k_eq_pair_backward(EqArgs a) {
-    constexpr int NQ = LQ * (LQ + 2);
+__global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
+    constexpr int NQ = LQ * (LQ + 2), LY = NQ + (NQ % 4 == 0 ? 4 : 1);
     using Ln = Lanes<S>;
-    constexpr int HM = Ln::HM, W = Ln::W;
+    constexpr int W = Ln::W;
     extern __shared__ float lds[];
     const int j = wave_atom(a.r);
     if (j < 0) return;
     const Ln ln(a.C);
-    const int H = a.H, G = a.G, C = a.C, CN = C * NQ, LC = LQ * C, NG = a.NG;
-    const int gw = H / G, gmode = a.gmode;
-    float *T = lds + (threadIdx.x >> 6) * S * H + ln.slot * H;
-    float MX[NQ], Vj[HM];
+    float *Yc = lds + (threadIdx.x >> 6) * kWave * LY;
+    const int G = a.G, C = a.C, CN = C * NQ, LC = LQ * C, NG = a.NG;
+    float MX[NQ], acc[NQ];
     zero(MX);
-    if (ln.act) load_row(MX, a.mixst + size_t(j) * CN + ln.c * NQ);
-#pragma unroll
-    for (int u = 0; u < HM; ++u) {
-        const int h = ln.c + W * u;
-        Vj[u] = h < H ? a.node[size_t(j) * a.NP + 2 * a.D + h] : 0.0f;
-    }
-    float acc[NQ], vacc[HM];
     zero(acc);
-    zero(vacc);
+    if (ln.act) load_row(MX, a.mixst + size_t(j) * CN + ln.c * NQ);
     const int tb = a.r.tptr[j], te = a.r.tptr[j + 1];
     for (int t0 = tb; t0 < te; t0 += kWave) {
         const int cnt = min(kWave, te - t0);
         int me = -1, mi = 0;
-        float mf = 0.0f;
+        float mf = 0.0f, md = 0.0f;
+        wave_sync();
         if (ln.lane < cnt) {
             me = a.r.tidx[t0 + ln.lane];
             mi = a.r.tctr[t0 + ln.lane];
             mf = a.tfc[t0 + ln.lane];
+            md = a.dfc[me];
+            if (mf != 0.0f) {
+                float y[NQ];
+                load_row(y, a.harm + size_t(me) * NQ);
+#pragma unroll
+                for (int k = 0; k < NQ; ++k) Yc[ln.lane * LY + k] = y[k];
+            }
         }
-        auto fetch = [&](int q, int &e, float (&dh)[NQ], float (&y)[NQ], float (&tt)[LQ],
-                         float (&ti)[LQ], float (&dm)[HM], float (&sg)[HM], float &f) {
+        wave_sync();
+        auto fetch = [&](int q, int &e, float (&dh)[NQ], float (&tt)[LQ], float (&ti)[LQ],
+                         float &f) {
             e = bcast(me, min(q, kWave - 1));
             const int i = bcast(mi, min(q, kWave - 1));
             f = bcast(mf, min(q, kWave - 1));
@@ -495,156 +495,220 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_backward(EqArgs a) {
                 e = -1;
                 f = 0.0f;
             }
-            if (f != 0.0f) {
-                if (ln.act) {
-                    load_row(dh, a.dht + size_t(i) * CN + ln.c * NQ);
-                    load_row(y, a.harm + size_t(e) * NQ);
-                    const float *gr = a.ag + size_t(e) * NG + G + ln.c;
+            if (f != 0.0f && ln.act) {
+                load_row(dh, a.dht + size_t(i) * CN + ln.c * NQ);
+                const float *gr = a.ag + size_t(e) * NG + G + ln.c;
 #pragma unroll
-                    for (int L = 0; L < LQ; ++L) {
-                        tt[L] = gr[L * C];
-                        ti[L] = gr[LC + L * C];
-                    }
+                for (int L = 0; L < LQ; ++L) {
+                    tt[L] = gr[L * C];
+                    ti[L] = gr[LC + L * C];
                 }
-                const float *gr = a.ag + size_t(e) * NG;
-#pragma unroll
-                for (int u = 0; u < HM; ++u) {
-                    const int h = ln.c + W * u;
-                    dm[u] = h < H ? a.dmsg[size_t(i) * H + h] : 0.0f;
-                    sg[u] = h < H ? gr[h / gw] : 0.0f;
-                }
-            } else {
-                zero(dm);
             }
         };
         int e;
-        float DH[NQ], Y[NQ], tT[LQ], tI[LQ], dm[HM], sg[HM], fc;
-        fetch(ln.slot, e, DH, Y, tT, tI, dm, sg, fc);
+        float DH[NQ], tT[LQ], tI[LQ], fc;
+        fetch(ln.slot, e, DH, tT, tI, fc);
         for (int q0 = 0; q0 < cnt; q0 += S) {
+            const int q = q0 + ln.slot;
             int en;
-            float DHn[NQ], Yn[NQ], tTn[LQ], tIn[LQ], dmn[HM], sgn[HM], fcn;
-            fetch(q0 + S + ln.slot, en, DHn, Yn, tTn, tIn, dmn, sgn, fcn);
+            float DHn[NQ], tTn[LQ], tIn[LQ], fcn;
+            fetch(q + S, en, DHn, tTn, tIn, fcn);
             const bool on = fc != 0.0f;
-            float *dg = a.dgg + size_t(e >= 0 ? e : 0) * NG;
             float contrib = 0.0f;
             if (e >= 0 && ln.act) {
+                float *dg = a.dgg + size_t(e) * NG + G + ln.c;
+                if (on) {
+                    float Y[NQ];
 #pragma unroll
-                for (int L = 1; L <= LQ; ++L) {
-                    const int st = L * L - 1;
-                    float sT = 0.0f, sI = 0.0f;
-                    if (on) {
+                    for (int k = 0; k < NQ; ++k) Y[k] = Yc[q * LY + k];
+#pragma unroll
+                    for (int L = 1; L <= LQ; ++L) {
+                        const int st = L * L - 1;
+                        float sT = 0.0f, sI = 0.0f;
 #pragma unroll
                         for (int m = 0; m < 2 * L + 1; ++m) {
                             sT += DH[st + m] * MX[st + m];
                             sI += DH[st + m] * Y[st + m];
                         }
-                    }
-                    const float t1 = on ? tT[L - 1] : 0.0f, t2 = on ? tI[L - 1] : 0.0f;
-                    dg[G + (L - 1) * C + ln.c] = on ? (1.0f - t1 * t1) * fc * sT : 0.0f;
-                    dg[G + LC + (L - 1) * C + ln.c] = on ? (1.0f - t2 * t2) * fc * sI : 0.0f;
-                    if (on) {
+                        const float t1 = tT[L - 1], t2 = tI[L - 1];
+                        dg[(L - 1) * C] = (1.0f - t1 * t1) * fc * sT;
+                        dg[LC + (L - 1) * C] = (1.0f - t2 * t2) * fc * sI;
                         contrib += t1 * sT + t2 * sI;
 #pragma unroll
                         for (int m = 0; m < 2 * L + 1; ++m) acc[st + m] += fc * t1 * DH[st + m];
                     }
+                } else {
+#pragma unroll
+                    for (int L = 0; L < LQ; ++L) {
+                        dg[L * C] = 0.0f;
+                        dg[LC + L * C] = 0.0f;
+                    }
                 }
             }
+            contrib = group_sum(contrib, W);
+            const float dold = bcast(md, min(q, kWave - 1));
+            if (on && ln.c == 0) a.dfc[e] = dold + contrib;
+            e = en;
+            copy(DH, DHn);
+            copy(tT, tTn);
+            copy(tI, tIn);
+            fc = fcn;
+        }
+    }
+    fold_slots<S>(acc);
+    if (ln.slot == 0 && ln.act) store_row(acc, a.dmix + size_t(j) * CN + ln.c * NQ);
+}
+
+// Reverse pass of the scalar messages from the neighbour side: the wave of
+// atom j holds V_j (lanes over hidden units), gathers dE/dmsg of the centre
+// once per record and produces the group-gate adjoints dE/dgate[e, :G],
+// their share of dE/dfc and dE/dV_j = sum_e fc s_e dmsg_i.  Group sums
+// P_g = sum_{h in g} dmsg_i[h] V_j[h]: lane reductions when the group width
+// is a power of two up to 64 (gmode 0) or a multiple of 64 (gmode 1), else a
+// per-wave LDS row (gmode 2).
+__global__ void __launch_bounds__(kBlock) k_eq_pair_grp(EqArgs a) {
+    extern __shared__ float lds[];
+    const int j = wave_atom(a.r);
+    if (j < 0) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int H = a.H, G = a.G, NG = a.NG, gw = H / G, gmode = a.gmode;
+    float *T = lds + (threadIdx.x >> 6) * H;
+    float Vj[4], vacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int h = lane + kWave * u;
+        Vj[u] = h < H ? a.node[size_t(j) * a.NP + 2 * a.D + h] : 0.0f;
+    }
+    const int tb = a.r.tptr[j], te = a.r.tptr[j + 1];
+    for (int t0 = tb; t0 < te; t0 += kWave) {
+        const int cnt = min(kWave, te - t0);
+        int me = -1, mi = 0;
+        float mf = 0.0f, md = 0.0f;
+        if (lane < cnt) {
+            me = a.r.tidx[t0 + lane];
+            mi = a.r.tctr[t0 + lane];
+            mf = a.tfc[t0 + lane];
+            md = a.dfc[me];
+        }
+        auto fetch = [&](int q, int &e, float (&dm)[4], float (&sg)[4], float &f) {
+            e = bcast(me, min(q, kWave - 1));
+            const int i = bcast(mi, min(q, kWave - 1));
+            f = bcast(mf, min(q, kWave - 1));
+            if (q >= cnt) {
+                e = -1;
+                f = 0.0f;
+            }
+            zero(dm);
+            zero(sg);
+            if (f != 0.0f) {
+                const float *dr = a.dmsg + size_t(i) * H;
+                const float *gr = a.ag + size_t(e) * NG;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int h = lane + kWave * u;
+                    if (h < H) {
+                        dm[u] = dr[h];
+                        sg[u] = gr[h / gw];
+                    }
+                }
+            }
+        };
+        int e, e1;
+        float dm[4], sg[4], fc, dm1[4], sg1[4], fc1;
+        fetch(0, e, dm, sg, fc);
+        fetch(1, e1, dm1, sg1, fc1);
+        for (int q = 0; q < cnt; ++q) {
+            int en;
+            float dmn[4], sgn[4], fcn;
+            fetch(q + 2, en, dmn, sgn, fcn);
+            const bool on = fc != 0.0f;
+            float *dg = a.dgg + size_t(e) * NG;
+            float contrib = 0.0f;
             if (on) {
 #pragma unroll
-                for (int u = 0; u < HM; ++u) vacc[u] += sg[u] * fc * dm[u];
+                for (int u = 0; u < 4; ++u) vacc[u] += sg[u] * fc * dm[u];
             }
-            // group gates: P_g, dE/dgate_g = P_g fc s (1 - s), dE/dfc += P_g s
             if (gmode == 0) {
 #pragma unroll
-                for (int u = 0; u < HM; ++u) {
-                    if (W * u < H) {
+                for (int u = 0; u < 4; ++u) {
+                    if (kWave * u < H) {
                         const float P = group_sum(dm[u] * Vj[u], gw);
-                        const int h = ln.c + W * u;
-                        if (e >= 0 && h < H && h % gw == 0) {
-                            const float s = on ? sg[u] : 0.0f;
-                            dg[h / gw] = on ? P * fc * s * (1.0f - s) : 0.0f;
-                            if (on) contrib += P * s;
+                        const int h = lane + kWave * u;
+                        if (h < H && h % gw == 0) {
+                            dg[h / gw] = on ? P * fc * sg[u] * (1.0f - sg[u]) : 0.0f;
+                            contrib += P * sg[u];
                         }
                     }
                 }
             } else if (gmode == 1) {
-                const int per = gw / W;
-                float run = 0.0f;
+                float P = 0.0f;
 #pragma unroll
-                for (int u = 0; u < HM; ++u) {
-                    if (W * u < H) {
-                        run += dm[u] * Vj[u];
-                        if ((u + 1) % per == 0) {
-                            const float P = group_sum(run, W);
-                            if (e >= 0 && ln.c == 0) {
-                                const float s = on ? sg[u] : 0.0f;
-                                dg[(W * u) / gw] = on ? P * fc * s * (1.0f - s) : 0.0f;
-                                if (on) contrib += P * s;
+                for (int u = 0; u < 4; ++u) {
+                    if (kWave * u < H) {
+                        P += wave_sum(dm[u] * Vj[u]);
+                        if ((kWave * (u + 1)) % gw == 0) {
+                            if (lane == 0) {
+                                dg[(kWave * u) / gw] = on ? P * fc * sg[u] * (1.0f - sg[u]) : 0.0f;
+                                contrib += P * sg[u];
                             }
-                            run = 0.0f;
+                            P = 0.0f;
                         }
                     }
                 }
             } else {
 #pragma unroll
-                for (int u = 0; u < HM; ++u) {
-                    const int h = ln.c + W * u;
+                for (int u = 0; u < 4; ++u) {
+                    const int h = lane + kWave * u;
                     if (h < H) T[h] = dm[u] * Vj[u];
                 }
                 wave_sync();
-                if (e >= 0) {
-                    for (int g = ln.c; g < G; g += W) {
-                        float P = 0.0f;
-                        for (int h = g * gw; h < (g + 1) * gw; ++h) P += T[h];
-                        const float s = on ? a.ag[size_t(e) * NG + g] : 0.0f;
-                        dg[g] = on ? P * fc * s * (1.0f - s) : 0.0f;
-                        if (on) contrib += P * s;
-                    }
+                for (int g = lane; g < G; g += kWave) {
+                    float P = 0.0f;
+                    for (int h = g * gw; h < (g + 1) * gw; ++h) P += T[h];
+                    const float s = on ? a.ag[size_t(e) * NG + g] : 0.0f;
+                    dg[g] = on ? P * fc * s * (1.0f - s) : 0.0f;
+                    contrib += P * s;
                 }
                 wave_sync();
             }
-            contrib = group_sum(contrib, W);
-            if (on && ln.c == 0) a.dv[e].w += contrib * cutoff_slope(a.r.vec[e].w, a.cutoff);
-            e = en;
-            copy(DH, DHn);
-            copy(Y, Yn);
-            copy(tT, tTn);
-            copy(tI, tIn);
-            copy(dm, dmn);
-            copy(sg, sgn);
-            fc = fcn;
+            contrib = wave_sum(contrib);
+            const float dold = bcast(md, q);
+            if (on && lane == 0) a.dfc[e] = dold + contrib;
+            e = e1;
+            copy(dm, dm1);
+            copy(sg, sg1);
+            fc = fc1;
+            e1 = en;
+            copy(dm1, dmn);
+            copy(sg1, sgn);
+            fc1 = fcn;
         }
     }
-    fold_slots<S>(acc);
-    fold_slots<S>(vacc);
-    if (ln.slot == 0) {
-        if (ln.act) store_row(acc, a.dmix + size_t(j) * CN + ln.c * NQ);
 #pragma unroll
-        for (int u = 0; u < HM; ++u) {
-            const int h = ln.c + W * u;
-            if (h < H) a.dnode[size_t(j) * a.NP + 2 * a.D + h] = vacc[u];
-        }
+    for (int u = 0; u < 4; ++u) {
+        const int h = lane + kWave * u;
+        if (h < H) a.dnode[size_t(j) * a.NP + 2 * a.D + h] = vacc[u];
     }
 }
 
-// Per-atom adjoints of the edge features, from both sides of each record:
-//   dE/dA_n, dE/dB_n (context projections: sums of dE/du over the records of
-//   n as centre / as neighbour), dE/d(dir_in)_n = dHt_n + probe adjoints
-//   (+ the channel-mix adjoint that k_eq_mix already wrote to ddir_in), and
-//   dE/dY of each record: the centre side adds fc tI dHt_i + dprobe_c H_i,
-//   the neighbour side (-1)^L dprobe_n H_j, each into its own buffer.  The
-//   channel sums of the dE/dY shares go through a per-wave LDS tile.
+// Angular adjoints of the edge features, from both sides of each record:
+// dE/d(dir_in)_n = dHt_n + probe adjoints (+ the channel-mix adjoint that
+// k_eq_mix already wrote to ddir_in), and dE/dY of each record: the centre
+// side adds fc tI dHt_i + dprobe_c H_i, the neighbour side (-1)^L dprobe_n
+// H_j, each into its own buffer.  Harmonic rows of a chunk are staged in LDS;
+// the channel sums of the dE/dY shares go through a per-wave LDS tile.
 template <int LQ, int S>
-__global__ void __launch_bounds__(kBlock) k_eq_atom_backward(EqArgs a) {
-    constexpr int NQ = LQ * (LQ + 2), LD = NQ + 1;
+__global__ void __launch_bounds__(kBlock) k_eq_atom_dir(EqArgs a) {
+    constexpr int NQ = LQ * (LQ + 2), LD = NQ + 1, LY = NQ + (NQ % 4 == 0 ? 4 : 1);
     using Ln = Lanes<S>;
-    constexpr int HM = Ln::HM, W = Ln::W;
+    constexpr int W = Ln::W;
     extern __shared__ float lds[];
     const int n = wave_atom(a.r);
     if (n < 0) return;
     const Ln ln(a.C);
-    float *T = lds + (threadIdx.x >> 6) * kWave * LD;
-    const int C = a.C, CN = C * NQ, LC = LQ * C, D = a.D, kb = a.kb, G = a.G, NG = a.NG;
+    float *T = lds + (threadIdx.x >> 6) * kWave * (LD + LY);
+    float *Yc = T + kWave * LD;
+    const int C = a.C, CN = C * NQ, LC = LQ * C, kb = a.kb, G = a.G, NG = a.NG;
     float Hn[NQ], DHn[NQ], g[NQ];
     zero(Hn);
     zero(DHn);
@@ -653,9 +717,6 @@ __global__ void __launch_bounds__(kBlock) k_eq_atom_backward(EqArgs a) {
         load_row(Hn, a.dir_in + size_t(n) * CN + ln.c * NQ);
         load_row(DHn, a.dht + size_t(n) * CN + ln.c * NQ);
     }
-    float sd[2][HM];
-    zero(sd[0]);
-    zero(sd[1]);
 #pragma unroll
     for (int side = 0; side < 2; ++side) {
         const int b0 = side ? a.r.tptr[n] : a.r.view[4 * n];
@@ -665,12 +726,21 @@ __global__ void __launch_bounds__(kBlock) k_eq_atom_backward(EqArgs a) {
             const int cnt = min(kWave, b1 - t0);
             int me = -1;
             float mf = 0.0f;
+            wave_sync();
             if (ln.lane < cnt) {
                 me = side ? a.r.tidx[t0 + ln.lane] : t0 + ln.lane;
                 mf = side ? a.tfc[t0 + ln.lane] : a.fc[t0 + ln.lane];
+                if (mf != 0.0f) {
+                    float y[NQ];
+                    load_row(y, a.harm + size_t(me) * NQ);
+#pragma unroll
+                    for (int k = 0; k < NQ; ++k) Yc[ln.lane * LY + k] = y[k];
+                }
             }
-            auto fetch = [&](int q, int &e, float (&y)[NQ], float (&dxv)[LQ], float (&ti)[LQ],
-                             float (&du)[HM], float &f) {
+            wave_sync();
+            constexpr int KQ = (NQ + W - 1) / W;   // dE/dY components per lane
+            auto fetch = [&](int q, int &e, float (&dxv)[LQ], float (&ti)[LQ], float (&yo)[KQ],
+                             float &f) {
                 e = bcast(me, min(q, kWave - 1));
                 f = bcast(mf, min(q, kWave - 1));
                 if (q >= cnt) {
@@ -678,42 +748,41 @@ __global__ void __launch_bounds__(kBlock) k_eq_atom_backward(EqArgs a) {
                     f = 0.0f;
                 }
                 if (f != 0.0f) {
-                    if (ln.act) {
-                        load_row(y, a.harm + size_t(e) * NQ);
-                        const float *d = a.dx + size_t(e) * a.ldx + kb + side * LC + ln.c;
-                        const float *gr = a.ag + size_t(e) * NG + G + LC + ln.c;
 #pragma unroll
-                        for (int L = 0; L < LQ; ++L) {
-                            dxv[L] = d[L * C];
-                            ti[L] = side ? 0.0f : gr[L * C];
-                        }
+                    for (int u = 0; u < KQ; ++u) {
+                        const int k = ln.c + W * u;
+                        yo[u] = k < NQ ? dyo[size_t(e) * NQ + k] : 0.0f;
                     }
+                }
+                if (f != 0.0f && ln.act) {
+                    const float *d = a.dx + size_t(e) * a.ldx + kb + side * LC + ln.c;
+                    const float *gr = a.ag + size_t(e) * NG + G + LC + ln.c;
 #pragma unroll
-                    for (int u = 0; u < HM; ++u) {
-                        const int dd = ln.c + W * u;
-                        du[u] = dd < D ? a.due[size_t(e) * D + dd] : 0.0f;
+                    for (int L = 0; L < LQ; ++L) {
+                        dxv[L] = d[L * C];
+                        ti[L] = side ? 0.0f : gr[L * C];
                     }
                 }
             };
             int e;
-            float Y[NQ], dxv[LQ], tI[LQ], du[HM], fc;
-            fetch(ln.slot, e, Y, dxv, tI, du, fc);
+            float dxv[LQ], tI[LQ], yo[KQ], fc;
+            fetch(ln.slot, e, dxv, tI, yo, fc);
             for (int q0 = 0; q0 < cnt; q0 += S) {
+                const int q = q0 + ln.slot;
                 int en;
-                float Yn[NQ], dxn[LQ], tIn[LQ], dun[HM], fcn;
-                fetch(q0 + S + ln.slot, en, Yn, dxn, tIn, dun, fcn);
-                const bool on = fc != 0.0f;
-                if (on) {
+                float dxn[LQ], tIn[LQ], yon[KQ], fcn;
+                fetch(q + S, en, dxn, tIn, yon, fcn);
+                const bool on = fc != 0.0f && ln.act;
+                float Y[NQ];
 #pragma unroll
-                    for (int u = 0; u < HM; ++u) sd[side][u] += du[u];
-                }
+                for (int k = 0; k < NQ; ++k) Y[k] = on ? Yc[q * LY + k] : 0.0f;
 #pragma unroll
                 for (int L = 1; L <= LQ; ++L)
 #pragma unroll
                     for (int m = 0; m < 2 * L + 1; ++m) {
                         const int k = L * L - 1 + m;
                         float yv = 0.0f;
-                        if (on && ln.act) {
+                        if (on) {
                             const float v = dxv[L - 1] * Y[k];
                             g[k] += (side && (L & 1)) ? -v : v;
                             yv = dxv[L - 1] * Hn[k];
@@ -725,42 +794,88 @@ __global__ void __launch_bounds__(kBlock) k_eq_atom_backward(EqArgs a) {
                         T[ln.lane * LD + k] = yv;
                     }
                 wave_sync();
-                if (on) {
-                    for (int k = ln.c; k < NQ; k += W) {
-                        float s = 0.0f;
-                        for (int c = 0; c < C; ++c) s += T[(ln.slot * W + c) * LD + k];
-                        dyo[size_t(e) * NQ + k] += s;
+                if (fc != 0.0f) {
+#pragma unroll
+                    for (int u = 0; u < KQ; ++u) {
+                        const int k = ln.c + W * u;
+                        if (k < NQ) {
+                            float s = 0.0f;
+                            for (int c = 0; c < C; ++c) s += T[(ln.slot * W + c) * LD + k];
+                            dyo[size_t(e) * NQ + k] = yo[u] + s;
+                        }
                     }
                 }
                 wave_sync();
                 e = en;
-                copy(Y, Yn);
                 copy(dxv, dxn);
                 copy(tI, tIn);
-                copy(du, dun);
+                copy(yo, yon);
                 fc = fcn;
             }
         }
     }
     fold_slots<S>(g);
-    fold_slots<S>(sd[0]);
-    fold_slots<S>(sd[1]);
-    if (ln.slot == 0) {
+    if (ln.slot == 0 && ln.act) {
+        float mx[NQ];
+        float *out = a.ddir_in + size_t(n) * CN + ln.c * NQ;
+        load_row(mx, out);
 #pragma unroll
-        for (int u = 0; u < HM; ++u) {
-            const int dd = ln.c + W * u;
-            if (dd < D) {
-                a.dnode[size_t(n) * a.NP + dd] = sd[0][u];
-                a.dnode[size_t(n) * a.NP + D + dd] = sd[1][u];
+        for (int k = 0; k < NQ; ++k) DHn[k] = (DHn[k] + g[k]) + mx[k];
+        store_row(DHn, out);
+    }
+}
+
+// Context-projection adjoints: dE/dA_n = sum of dE/du over the records of n
+// as centre, dE/dB_n over the records that see n as neighbour (records with
+// fc = 0 excluded).  Lanes over the message width, two records in flight.
+__global__ void __launch_bounds__(kBlock) k_eq_atom_sums(EqArgs a) {
+    const int n = wave_atom(a.r);
+    if (n < 0) return;
+    const int lane = threadIdx.x & (kWave - 1), D = a.D;
+#pragma unroll
+    for (int side = 0; side < 2; ++side) {
+        const int b0 = side ? a.r.tptr[n] : a.r.view[4 * n];
+        const int b1 = side ? a.r.tptr[n + 1] : a.r.view[4 * n + 1];
+        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int t0 = b0; t0 < b1; t0 += kWave) {
+            const int cnt = min(kWave, b1 - t0);
+            int me = -1;
+            float mf = 0.0f;
+            if (lane < cnt) {
+                me = side ? a.r.tidx[t0 + lane] : t0 + lane;
+                mf = side ? a.tfc[t0 + lane] : a.fc[t0 + lane];
+            }
+            auto fetch = [&](int q, float (&du)[4]) {
+                const int e = bcast(me, min(q, kWave - 1));
+                const float f = bcast(mf, min(q, kWave - 1));
+                zero(du);
+                if (q < cnt && f != 0.0f) {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int d = lane + kWave * u;
+                        if (d < D) du[u] = a.due[size_t(e) * D + d];
+                    }
+                }
+            };
+            float du0[4], du1[4];
+            fetch(0, du0);
+            fetch(1, du1);
+            for (int q = 0; q < cnt; q += 2) {
+                float dn0[4], dn1[4];
+                fetch(q + 2, dn0);
+                fetch(q + 3, dn1);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) s[u] += du0[u];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) s[u] += du1[u];
+                copy(du0, dn0);
+                copy(du1, dn1);
             }
         }
-        if (ln.act) {
-            float mx[NQ];
-            float *out = a.ddir_in + size_t(n) * CN + ln.c * NQ;
-            load_row(mx, out);
 #pragma unroll
-            for (int k = 0; k < NQ; ++k) DHn[k] = (DHn[k] + g[k]) + mx[k];
-            store_row(DHn, out);
+        for (int u = 0; u < 4; ++u) {
+            const int d = lane + kWave * u;
+            if (d < D) a.dnode[size_t(n) * a.NP + side * D + d] = s[u];
         }
     }
 }
@@ -790,39 +905,48 @@ __global__ void __launch_bounds__(kWave) k_eq_encoder_backward(const float *ddir
 }
 
 // dE/du of the harmonics: sum_k dY_k scale_k db_k/du, added to dv.xyz.
+template <int LQ>
 __global__ void k_eq_harmonic_backward(int64_t E, Records r, const float *fcv, const float *dy,
-                                       const float *dyn, const float *ztab, EdgeZ zoff, int lq,
-                                       int nq,
-                                       const float *scale, float4 *dv) {
+                                       const float *dyn, const float *dfc, float cutoff,
+                                       const float *ztab, EdgeZ zoff, const float *scale,
+                                       float4 *dv) {
+    constexpr int NQ = LQ * (LQ + 2);
     int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (e >= E) return;
     int i = r.ctr[e];
     if (!(e >= r.view[4 * i] && e < r.view[4 * i + 1])) return;
+    float gs[NQ], g2[NQ];
+    load_row(gs, dy + size_t(e) * NQ);
+    load_row(g2, dyn + size_t(e) * NQ);
     float4 v = r.vec[e];
     float inv = 1.0f / fmaxf(v.w, 1.0e-12f);
     float x = v.x * inv, y = v.y * inv, z = v.z * inv;
-    float zp[kMaxL + 1], wr[kMaxL + 1], wi[kMaxL + 1];
+    float zp[LQ + 1], wr[LQ + 1], wi[LQ + 1];
     zp[0] = 1.0f;
     wr[0] = 1.0f;
     wi[0] = 0.0f;
-    for (int k = 1; k <= lq; ++k) {
+#pragma unroll
+    for (int k = 1; k <= LQ; ++k) {
         zp[k] = zp[k - 1] * z;
         wr[k] = wr[k - 1] * x - wi[k - 1] * y;
         wi[k] = wr[k - 1] * y + wi[k - 1] * x;
     }
-    const float *g = dy + size_t(e) * nq, *g2 = dyn + size_t(e) * nq;
     float dx = 0.0f, dyy = 0.0f, dz = 0.0f;
     int idx = 0;
-    for (int L = 1; L <= lq; ++L) {
+#pragma unroll
+    for (int L = 1; L <= LQ; ++L) {
+#pragma unroll
         for (int n1 = 0; n1 <= L; ++n1) {
             const float *Z = ztab + zoff.off[L] + n1 * (L + 1);
             float zf = 0.0f, zfp = 0.0f;
+#pragma unroll
             for (int q = ((L + n1) & 1); q <= L - n1; q += 2) {
                 zf += Z[q] * zp[q];
                 if (q > 0) zfp += float(q) * Z[q] * zp[q - 1];
             }
+#pragma unroll
             for (int part = 0; part < (n1 == 0 ? 1 : 2); ++part, ++idx) {
-                float w = (g[idx] + g2[idx]) * scale[idx];
+                float w = (gs[idx] + g2[idx]) * scale[idx];
                 if (n1 == 0) {
                     dz += w * zfp;
                 } else if (part == 0) {
@@ -841,6 +965,7 @@ __global__ void k_eq_harmonic_backward(int64_t E, Records r, const float *fcv, c
     acc.x += dx;
     acc.y += dyy;
     acc.z += dz;
+    if (fcv[e] != 0.0f) acc.w += dfc[e] * cutoff_slope(v.w, cutoff);
     dv[e] = acc;
 }
 
@@ -1088,6 +1213,7 @@ MessagePlan plan_equivariant(ModelImpl &m, Arena &ar, int N, int64_t E) {
     p.i_harm = p.add(ar, 4 * e * nq);
     p.i_dharm = p.add(ar, 4 * e * nq);
     p.i_dharm_n = p.add(ar, 4 * e * nq);
+    p.i_dfc = p.add(ar, 4 * e);
     int dir0 = p.add(ar, 4 * n * CN);
     int x = p.add(ar, 4 * e * ldx);        // shared by the blocks (forward only)
     int eh = p.add(ar, 4 * e * D);         // shared
@@ -1148,9 +1274,9 @@ static EqArgs eq_args(ModelImpl &m, MessagePlan &p, const Records &r, int b) {
     a.nlm = m.desc.nlm;
     a.S = eq_slots(a.C);
     {
-        const int W = kWave / a.S, gw = a.H / a.G;
+        const int gw = a.H / a.G;
         const bool pow2 = (gw & (gw - 1)) == 0;
-        a.gmode = (pow2 && gw <= W) ? 0 : (gw % W == 0 ? 1 : 2);
+        a.gmode = (pow2 && gw <= kWave) ? 0 : (gw % kWave == 0 ? 1 : 2);
     }
     a.eps = float(c.norm_eps);
     a.cutoff = float(c.message_cutoff);
@@ -1174,6 +1300,7 @@ static EqArgs eq_args(ModelImpl &m, MessagePlan &p, const Records &r, int b) {
     a.dht = p.at(p.t_dvsum);
     a.dgg = p.at(p.t_dgv);
     a.dv = reinterpret_cast<float4 *>(p.at(p.i_dv));
+    a.dfc = p.at(p.i_dfc);
     a.dy = p.at(p.i_dharm);
     a.dyn = p.at(p.i_dharm_n);
     a.dnode = p.at(p.t_dvs);
@@ -1193,13 +1320,14 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
     const int lq = c.equivariant_l_max, C = c.equivariant_channels, nq = lq * (lq + 2);
     const int64_t E = p.E;
     const int atom_grid = ceil_div(N, kWaves), mix_grid = std::max(1, std::min(N, 2048));
-    const size_t mix_lds = sizeof(float) * (size_t(lq) * C * C + size_t(C) * nq);
+    const size_t mix_lds = sizeof(float) * (size_t(lq) * C * (C + 1) + size_t(C) * nq);
     edge_prep(m, p, r, types, s, p.at(p.i_harm), m.harm_scale, lq, nq);
     if (E > 0) {
         hipLaunchKernelGGL(k_gather_f, dim3(ceil_div(E, 256)), dim3(256), 0, s, E, r.tidx,
                            p.at(p.i_fc), p.at(p.i_tfc));
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dharm), 0, 4 * size_t(E) * nq, s));
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dharm_n), 0, 4 * size_t(E) * nq, s));
+        RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dfc), 0, 4 * size_t(E), s));
     }
     hipLaunchKernelGGL(k_eq_encode, dim3(N), dim3(kWave), 0, s, N, moments, m.desc.na,
                        m.desc.nlm, m.enc_w, m.harm_scale, C, nq, p.at(p.blocks[0].dir_in));
@@ -1271,7 +1399,7 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
     const int NU = H + lq * C;
     const int64_t E = p.E;
     const int atom_grid = ceil_div(N, kWaves), mix_grid = std::max(1, std::min(N, 2048));
-    const size_t mix_lds = sizeof(float) * (size_t(lq) * C * C + size_t(C) * nq);
+    const size_t mix_lds = sizeof(float) * (size_t(lq) * C * (C + 1) + size_t(C) * nq);
     float *cur = dh;
     const float *ddir_out = nullptr;   // the last block's states feed only its invariants
     float *ddir_in = p.at(p.t_ddir0);
@@ -1289,8 +1417,11 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         Epilogue e1;
         gemm(N, NU, D, p.at(p.t_dz1), D, w.up1_fT, D, p.at(p.t_duin), NU, e1, s);
         hipLaunchKernelGGL(k_eq_node_backward, dim3(N), dim3(kWave), 0, s, a);
-        EQ_LAUNCH_S(k_eq_pair_backward, lq, a.S, dim3(atom_grid), dim3(kBlock),
-                    a.gmode == 2 ? sizeof(float) * kWaves * a.S * H : 0, s, a);
+        EQ_LAUNCH_S(k_eq_pair_dir, lq, a.S, dim3(atom_grid), dim3(kBlock),
+                    sizeof(float) * kBlock * (nq + (nq % 4 == 0 ? 4 : 1)), s, a);
+        hipLaunchKernelGGL(k_eq_pair_grp, dim3(atom_grid), dim3(kBlock),
+                           a.gmode == 2 ? sizeof(float) * kWaves * H : 0, s, a);
+        RUNE_HIP_CHECK(hipGetLastError());
         // channel-mix adjoint M^T dmix, completed by k_eq_atom_backward
         EQ_LAUNCH(k_eq_mix, lq, dim3(mix_grid), dim3(256), mix_lds, s, N, w.mix, a.dmix, C, 1,
                   a.ddir_in);
@@ -1304,8 +1435,10 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
             gemm(int(E), w.KX, D, p.at(p.t_due), D, w.edge_xT, D, p.at(p.t_dx), a.ldx, e3, s);
             edge_rb_backward(m, p, r, p.at(p.t_dx), a.ldx, s);
         }
-        EQ_LAUNCH_S(k_eq_atom_backward, lq, a.S, dim3(atom_grid), dim3(kBlock),
-                    sizeof(float) * kBlock * (nq + 1), s, a);
+        EQ_LAUNCH_S(k_eq_atom_dir, lq, a.S, dim3(atom_grid), dim3(kBlock),
+                    sizeof(float) * kBlock * (2 * nq + 1 + (nq % 4 == 0 ? 4 : 1)), s, a);
+        hipLaunchKernelGGL(k_eq_atom_sums, dim3(atom_grid), dim3(kBlock), 0, s, a);
+        RUNE_HIP_CHECK(hipGetLastError());
         Epilogue e4;
         gemm(N, H, w.NP, p.at(p.t_dvs), w.NP, w.node_fT, w.NP, p.at(p.t_dz), H, e4, s);
         float *next = (cur == p.at(p.t_dh0)) ? p.at(p.t_dh1) : p.at(p.t_dh0);
@@ -1320,10 +1453,10 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
     if (E > 0) {
         EdgeZ zo;
         for (int k = 0; k < kMaxL + 2; ++k) zo.off[k] = m.desc.z_off[k];
-        hipLaunchKernelGGL(k_eq_harmonic_backward, dim3(ceil_div(E, 256)), dim3(256), 0, s, E, r,
-                           p.at(p.i_fc), p.at(p.i_dharm), p.at(p.i_dharm_n), m.desc.z, zo,
-                           lq, nq, m.harm_scale,
-                           reinterpret_cast<float4 *>(p.at(p.i_dv)));
+        EQ_LAUNCH(k_eq_harmonic_backward, lq, dim3(ceil_div(E, 256)), dim3(256), 0, s, E, r,
+                  p.at(p.i_fc), p.at(p.i_dharm), p.at(p.i_dharm_n), p.at(p.i_dfc),
+                  float(c.message_cutoff), m.desc.z, zo, m.harm_scale,
+                  reinterpret_cast<float4 *>(p.at(p.i_dv)));
     }
     RUNE_HIP_CHECK(hipGetLastError());
     edge_direct(p, r, s);
