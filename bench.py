@@ -99,11 +99,92 @@ def phase_model(ev, prep, n_records, n_short, params):
     return out
 
 
+def group_model(ev, prep, n_records, params):
+    """Work of the kernel groups per call: FLOPs of the per-record GEMMs and
+    compulsory bytes of the per-record message kernels (fp32 values, int32
+    indices; each array a kernel reads or writes counted once per kernel,
+    read-modify-write counted twice; weights excluded).  None without
+    message blocks."""
+    p = params
+    if ev.family != 0 or int(p.get("message_layers", 0)) == 0:
+        return None
+    N, E = prep.n_atoms, n_records
+    B, H, D, G = p["message_layers"], p["hidden_dim"], p["message_dim"], p["message_groups"]
+    kb = p["message_basis_size"]
+    ldrb = (kb + 3) // 4 * 4
+    prep_bytes = E * (16 + 4 + 4 + 4 * ldrb + 4 + 4 + 16) + N * (16 + 4)
+    direct = E * (16 + 16 + 16)
+    rb_bwd = E * (4 + 16 + 4 * kb + 8)
+    if p["message_mode"] == "equivariant":
+        C, lq = p["equivariant_channels"], p["equivariant_l_max"]
+        nq, LC = lq * (lq + 2), lq * p["equivariant_channels"]
+        CN, KX, NG = C * nq, kb + 2 * LC, G + 2 * LC
+        flops = B * 4 * E * D * (KX + NG)
+        prep_bytes += E * 4 * nq + E * 12            # harmonics out; transposed fc
+        per_block = (
+            # features: harm, rb, fc/tfc/tidx, ptr/tptr, dir_in in; x out
+            E * (4 * nq + 4 * kb + 12 + 4 * KX) + N * (8 + 4 * CN)
+            # aggregate: harm, mixed states, gates, values, dir_in, fc, nbr in; states, msg out
+            + E * (4 * nq + 4 * NG + 8) + N * (4 * CN * 3 + 4 * H * 2 + 4 + 4 * (H + LC) + 16)
+            # pair_dir: dHt, mixed states, harm, direction gates, metadata, dE/dfc r/w; dg, dmix
+            + E * (4 * nq + 8 * 2 * LC + 12 + 8) + N * 4 * CN * 3
+            # pair_grp: dmsg, values, group gates, metadata, dE/dfc r/w; dg, dV
+            + E * (8 * G + 12 + 8) + N * 4 * H * 3
+            # rb reverse
+            + rb_bwd
+            # atom_dir: dir_in, dHt, ddir_in r/w; harm, probe adjoints, injection gates,
+            # metadata, dE/dY (two buffers) r/w
+            + N * 4 * CN * 4 + E * (4 * nq + 4 * 3 * LC + 12 + 16 * nq)
+            # atom_sums: dE/du rows, metadata; dA, dB out
+            + E * (4 * D + 12) + N * 8 * D)
+        once = prep_bytes + direct + E * (8 * nq + 16 + 8 + 12 + 32) + N * 16
+    else:
+        vc = p["vector_channels"]
+        NP, NG = H + vc, G + vc
+        flops = B * 4 * E * D * (kb + NG)
+        per_block = (
+            # aggregate: gates, vec, fc, nbr in; values; msg, vsum, mixed, uin out
+            E * (4 * NG + 16 + 8) + N * (4 * NP + 16 + 4 * H + 4 + 24 * vc + 4 * (H + vc))
+            # edge reverse: gates, vec, fc, nbr, dv r/w; dgv out; dmsg, dvsum, values
+            + E * (8 * NG + 16 + 8 + 32) + N * (4 * H + 12 * vc + 4 * NP)
+            # neighbour reverse: gates, transpose, fc, vec; dmsg, dvsum; dvs out
+            + E * (4 * NG + 8 + 4 + 16) + N * (4 * H + 12 * vc + 4 * NP)
+            + rb_bwd)
+        once = prep_bytes + direct
+    return {"edge_gemm": ("mfma", flops), "edge_kernels": ("hbm", B * per_block + once)}
+
+
+def measured_traffic(workload, group):
+    """HBM bytes per launch of a kernel group from the committed counter
+    summary (rocprofv3 FETCH_SIZE / WRITE_SIZE runs, calibrated by a plain copy
+    kernel), or None."""
+    path = ROOT / "profiles" / f"traffic_{workload}.json"
+    if not path.exists():
+        return None
+    data = json.loads(path.read_text())
+    entry = data.get("groups", {}).get(group)
+    return None if entry is None else entry.get("bytes_per_launch")
+
+
+def copy_calibration(device):
+    """A plain device-to-device copy of known size (256 MiB read + 256 MiB
+    written): the FETCH_SIZE / WRITE_SIZE counters of its kernel calibrate the
+    counters of the workload's kernels."""
+    import torch
+    src = torch.ones(64 << 20, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def run_gpu(args):
     import torch
     device = torch.device("cuda:0")
     ev, structures, params, state, family = build_workload(args.workload, device)
     prep = ev.prepare(structures)
+    if args.copy_calibration:
+        copy_calibration(device)
     torch.cuda.synchronize()
     for _ in range(args.warmup):
         ev.evaluate(prep)
@@ -121,6 +202,7 @@ def run_gpu(args):
     wall = time.perf_counter() - t0
     gpu_ms = start.elapsed_time(stop)
     phases, calls = ev.native.timing_read()
+    groups = ev.native.timing_groups()
     ev.native.timing(False)
     # neighbour build alone (events around the call, includes its count readback)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -151,21 +233,50 @@ def run_gpu(args):
                              frac=round(ach / FP32_PEAK, 4))
         per_phase[name] = entry
     per_phase["neighbors"] = {"ms": round(statistics.median(nl_ms), 4)}
-    # dominant measured phase that has a work model
-    cands = [(v["ms"], k) for k, v in per_phase.items() if "frac" in v]
-    dom = max(cands)[1]
-    d = per_phase[dom]
+    # kernel groups: per-launch averages from the events around each launch
+    gmodel = group_model(ev, prep, n_records, params)
+    per_group = {}
+    if gmodel:
+        for name, (ms, launches) in groups.items():
+            if launches == 0:
+                continue
+            bound, work = gmodel[name]
+            work_launch = work * calls / launches       # model is per call
+            avg = ms / launches
+            ach = work_launch / (avg / 1e3)
+            g = {"launches_per_step": launches / calls, "ms_per_step": round(ms / calls, 4),
+                 "avg_ms": round(avg, 4), "bound": bound}
+            if bound == "hbm":
+                g.update(bytes_per_launch=int(work_launch), achieved_GBs=round(ach / 1e9, 1),
+                         frac=round(ach / HBM_PEAK, 4))
+            else:
+                g.update(flops_per_launch=int(work_launch), achieved_TFs=round(ach / 1e12, 2),
+                         frac=round(ach / FP32_PEAK, 4))
+            per_group[name] = g
+    # roofline of the dominant measured kernel group (or phase, without message blocks)
+    if per_group:
+        dom = max(per_group, key=lambda k: per_group[k]["ms_per_step"])
+        d = dict(per_group[dom], ms=per_group[dom]["avg_ms"])
+        if "bytes_per_launch" in d:
+            d["bytes"] = d["bytes_per_launch"]
+        else:
+            d["flops"] = d["flops_per_launch"]
+    else:
+        cands = [(v["ms"], k) for k, v in per_phase.items() if "frac" in v]
+        dom = max(cands)[1]
+        d = per_phase[dom]
+    traffic = measured_traffic(args.workload, dom)
     if d["bound"] == "hbm":
         roof = {"kernel": dom, "bound": "hbm", "achieved": d["achieved_GBs"],
-                "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": d["frac"], "traffic": None,
+                "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": d["frac"], "traffic": traffic,
                 "algorithmic_bytes": d["bytes"], "avg_ms": d["ms"]}
     else:
         roof = {"kernel": dom, "bound": "mfma", "achieved": d["achieved_TFs"],
-                "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s", "frac": d["frac"], "traffic": None,
-                "algorithmic_flops": d["flops"], "avg_ms": d["ms"]}
+                "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s", "frac": d["frac"],
+                "traffic": traffic, "algorithmic_flops": d["flops"], "avg_ms": d["ms"]}
     return {
         "value": value, "ms_per_step": ms_per_step, "n_atoms": n_atoms, "n_records": n_records,
-        "roofline": roof, "phases": per_phase,
+        "roofline": roof, "phases": per_phase, "groups": per_group,
         "energy": float(out["energy"].double().sum().cpu()),
     }
 
@@ -230,6 +341,8 @@ def main():
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run a plain 256 MiB device copy once (reference for HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build evaluates on one GPU only; the multi-GPU "
@@ -246,6 +359,7 @@ def main():
         "config": {"workload": args.workload, "description": WORKLOADS[args.workload],
                    "n_atoms": res["n_atoms"], "records": res["n_records"]},
         "roofline": res["roofline"], "cpu_baseline": cpu, "phases": res["phases"],
+        "groups": res["groups"],
     }
     print(json.dumps(line), flush=True)
 

@@ -196,6 +196,19 @@ enum {
 int rune_model_timing(rune_model *model, int32_t enable);
 int rune_model_timing_read(rune_model *model, double *ms_per_phase, int64_t *calls);
 
+/* Kernel-group timing (no counterpart in the reference; it feeds the roofline
+ * measurement).  While timing is enabled, every launch of a group is bracketed
+ * by two HIP events on the launch stream.  rune_model_timing_groups waits for
+ * them and returns, per group, the summed milliseconds and the number of
+ * launches since timing was enabled. */
+enum {
+    RUNE_GROUP_EDGE_GEMM = 0,     /* per-record MLP / gate GEMMs of MP and EQ blocks */
+    RUNE_GROUP_EDGE_KERNELS = 1,  /* per-record message kernels (gather / transform /
+                                     scatter, their reverse passes, edge preparation) */
+    RUNE_N_GROUPS = 2
+};
+int rune_model_timing_groups(rune_model *model, double *ms_per_group, int64_t *launches);
+
 #ifdef __cplusplus
 }
 #endif

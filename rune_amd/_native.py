@@ -81,6 +81,7 @@ def library():
         "rune_model_workspace_bytes": (i64, [vp]),
         "rune_model_timing": (C.c_int, [vp, i32]),
         "rune_model_timing_read": (C.c_int, [vp, C.POINTER(C.c_double), C.POINTER(i64)]),
+        "rune_model_timing_groups": (C.c_int, [vp, C.POINTER(C.c_double), C.POINTER(i64)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -314,6 +315,15 @@ class NativeModel:
         calls = C.c_int64()
         check(library().rune_model_timing_read(self._h, ms, C.byref(calls)))
         return dict(zip(self.PHASES, list(ms))), calls.value
+
+    GROUPS = ("edge_gemm", "edge_kernels")
+
+    def timing_groups(self):
+        """Summed milliseconds and launch counts per kernel group since timing was enabled."""
+        ms = (C.c_double * len(self.GROUPS))()
+        n = (C.c_int64 * len(self.GROUPS))()
+        check(library().rune_model_timing_groups(self._h, ms, n))
+        return {g: (ms[k], n[k]) for k, g in enumerate(self.GROUPS)}
 
 
 def version():

@@ -1321,10 +1321,16 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
     const int64_t E = p.E;
     const int atom_grid = ceil_div(N, kWaves), mix_grid = std::max(1, std::min(N, 2048));
     const size_t mix_lds = sizeof(float) * (size_t(lq) * C * (C + 1) + size_t(C) * nq);
-    edge_prep(m, p, r, types, s, p.at(p.i_harm), m.harm_scale, lq, nq);
+    {
+        Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+        edge_prep(m, p, r, types, s, p.at(p.i_harm), m.harm_scale, lq, nq);
+    }
     if (E > 0) {
-        hipLaunchKernelGGL(k_gather_f, dim3(ceil_div(E, 256)), dim3(256), 0, s, E, r.tidx,
-                           p.at(p.i_fc), p.at(p.i_tfc));
+        {
+            Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+            hipLaunchKernelGGL(k_gather_f, dim3(ceil_div(E, 256)), dim3(256), 0, s, E, r.tidx,
+                               p.at(p.i_fc), p.at(p.i_tfc));
+        }
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dharm), 0, 4 * size_t(E) * nq, s));
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dharm_n), 0, 4 * size_t(E) * nq, s));
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dfc), 0, 4 * size_t(E), s));
@@ -1344,8 +1350,11 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
         EQ_LAUNCH(k_eq_mix, lq, dim3(mix_grid), dim3(256), mix_lds, s, N, w.mix,
                   p.at(bb.dir_in), C, 0, p.at(bb.mixstate));
         if (E > 0) {
-            EQ_LAUNCH_S(k_eq_features, lq, a.S, dim3(atom_grid), dim3(kBlock),
-                        sizeof(float) * kBlock * (nq + (nq % 4 == 0 ? 4 : 1)), s, a);
+            {
+                Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+                EQ_LAUNCH_S(k_eq_features, lq, a.S, dim3(atom_grid), dim3(kBlock),
+                            sizeof(float) * kBlock * (nq + (nq % 4 == 0 ? 4 : 1)), s, a);
+            }
             Epilogue e1;
             e1.gtab[0] = p.at(bb.vs);
             e1.gidx[0] = r.ctr;
@@ -1359,16 +1368,25 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
             e1.pre = p.at(bb.ue);
             e1.ldp = D;
             e1.act = act;
-            gemm(int(E), D, w.KX, p.at(bb.xe), a.ldx, w.edge_x, w.ld_edge_x, p.at(bb.eh), D, e1,
-                 s);
+            {
+                Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
+                gemm(int(E), D, w.KX, p.at(bb.xe), a.ldx, w.edge_x, w.ld_edge_x, p.at(bb.eh),
+                     D, e1, s);
+            }
             Epilogue e2;
             e2.bias = w.gate_b;
             e2.act = kActSigmoid;
             e2.act_split = c.message_groups;
             e2.act2 = RUNE_ACT_TANH;
-            gemm(int(E), w.NG, D, p.at(bb.eh), D, w.gate, D, p.at(bb.gv), w.NG, e2, s);
+            {
+                Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
+                gemm(int(E), w.NG, D, p.at(bb.eh), D, w.gate, D, p.at(bb.gv), w.NG, e2, s);
+            }
         }
-        EQ_LAUNCH_S(k_eq_aggregate, lq, a.S, dim3(atom_grid), dim3(kBlock), 0, s, a);
+        {
+            Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+            EQ_LAUNCH_S(k_eq_aggregate, lq, a.S, dim3(atom_grid), dim3(kBlock), 0, s, a);
+        }
         const int NU = H + lq * C;
         Epilogue e3;
         e3.bias = w.up1_b;
@@ -1417,10 +1435,16 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         Epilogue e1;
         gemm(N, NU, D, p.at(p.t_dz1), D, w.up1_fT, D, p.at(p.t_duin), NU, e1, s);
         hipLaunchKernelGGL(k_eq_node_backward, dim3(N), dim3(kWave), 0, s, a);
-        EQ_LAUNCH_S(k_eq_pair_dir, lq, a.S, dim3(atom_grid), dim3(kBlock),
-                    sizeof(float) * kBlock * (nq + (nq % 4 == 0 ? 4 : 1)), s, a);
-        hipLaunchKernelGGL(k_eq_pair_grp, dim3(atom_grid), dim3(kBlock),
-                           a.gmode == 2 ? sizeof(float) * kWaves * H : 0, s, a);
+        {
+            Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+            EQ_LAUNCH_S(k_eq_pair_dir, lq, a.S, dim3(atom_grid), dim3(kBlock),
+                        sizeof(float) * kBlock * (nq + (nq % 4 == 0 ? 4 : 1)), s, a);
+        }
+        {
+            Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+            hipLaunchKernelGGL(k_eq_pair_grp, dim3(atom_grid), dim3(kBlock),
+                               a.gmode == 2 ? sizeof(float) * kWaves * H : 0, s, a);
+        }
         RUNE_HIP_CHECK(hipGetLastError());
         // channel-mix adjoint M^T dmix, completed by k_eq_atom_backward
         EQ_LAUNCH(k_eq_mix, lq, dim3(mix_grid), dim3(256), mix_lds, s, N, w.mix, a.dmix, C, 1,
@@ -1430,14 +1454,29 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
             e2.dact_from = p.at(bb.ue);
             e2.ldu = D;
             e2.dact = act;
-            gemm(int(E), D, w.NG, p.at(p.t_dgv), w.NG, w.gate_T, w.NG, p.at(p.t_due), D, e2, s);
+            {
+                Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
+                gemm(int(E), D, w.NG, p.at(p.t_dgv), w.NG, w.gate_T, w.NG, p.at(p.t_due), D, e2, s);
+            }
             Epilogue e3;
-            gemm(int(E), w.KX, D, p.at(p.t_due), D, w.edge_xT, D, p.at(p.t_dx), a.ldx, e3, s);
-            edge_rb_backward(m, p, r, p.at(p.t_dx), a.ldx, s);
+            {
+                Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
+                gemm(int(E), w.KX, D, p.at(p.t_due), D, w.edge_xT, D, p.at(p.t_dx), a.ldx, e3, s);
+            }
+            {
+                Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+                edge_rb_backward(m, p, r, p.at(p.t_dx), a.ldx, s);
+            }
         }
-        EQ_LAUNCH_S(k_eq_atom_dir, lq, a.S, dim3(atom_grid), dim3(kBlock),
-                    sizeof(float) * kBlock * (2 * nq + 1 + (nq % 4 == 0 ? 4 : 1)), s, a);
-        hipLaunchKernelGGL(k_eq_atom_sums, dim3(atom_grid), dim3(kBlock), 0, s, a);
+        {
+            Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+            EQ_LAUNCH_S(k_eq_atom_dir, lq, a.S, dim3(atom_grid), dim3(kBlock),
+                        sizeof(float) * kBlock * (2 * nq + 1 + (nq % 4 == 0 ? 4 : 1)), s, a);
+        }
+        {
+            Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+            hipLaunchKernelGGL(k_eq_atom_sums, dim3(atom_grid), dim3(kBlock), 0, s, a);
+        }
         RUNE_HIP_CHECK(hipGetLastError());
         Epilogue e4;
         gemm(N, H, w.NP, p.at(p.t_dvs), w.NP, w.node_fT, w.NP, p.at(p.t_dz), H, e4, s);
@@ -1453,13 +1492,19 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
     if (E > 0) {
         EdgeZ zo;
         for (int k = 0; k < kMaxL + 2; ++k) zo.off[k] = m.desc.z_off[k];
-        EQ_LAUNCH(k_eq_harmonic_backward, lq, dim3(ceil_div(E, 256)), dim3(256), 0, s, E, r,
-                  p.at(p.i_fc), p.at(p.i_dharm), p.at(p.i_dharm_n), p.at(p.i_dfc),
-                  float(c.message_cutoff), m.desc.z, zo, m.harm_scale,
-                  reinterpret_cast<float4 *>(p.at(p.i_dv)));
+        {
+            Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+            EQ_LAUNCH(k_eq_harmonic_backward, lq, dim3(ceil_div(E, 256)), dim3(256), 0, s, E, r,
+                      p.at(p.i_fc), p.at(p.i_dharm), p.at(p.i_dharm_n), p.at(p.i_dfc),
+                      float(c.message_cutoff), m.desc.z, zo, m.harm_scale,
+                      reinterpret_cast<float4 *>(p.at(p.i_dv)));
+        }
     }
     RUNE_HIP_CHECK(hipGetLastError());
-    edge_direct(p, r, s);
+    {
+        Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+        edge_direct(p, r, s);
+    }
     p.g_direct_used = E > 0;
     p.dmom_used = true;
     return cur;

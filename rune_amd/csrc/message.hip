@@ -654,7 +654,10 @@ float *messages_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Recor
     const int N = p.N, H = c.hidden_dim, D = c.message_dim, act = c.activation;
     const int64_t E = p.E;
     (void)keep;
-    edge_prep(m, p, r, types, s, nullptr, nullptr, 0, 0);
+    {
+        Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+        edge_prep(m, p, r, types, s, nullptr, nullptr, 0, 0);
+    }
     float *cur = h;
     for (int b = 0; b < c.message_layers; ++b) {
         const MessageWeights &w = m.msg[b];
@@ -671,14 +674,23 @@ float *messages_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Recor
             e1.pre = p.at(bb.ue);
             e1.ldp = D;
             e1.act = act;
-            gemm(int(E), D, w.KX, p.at(p.i_rb), p.ldrb, w.edge_x, w.ld_edge_x, p.at(bb.eh), D, e1,
-                 s);
+            {
+                Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
+                gemm(int(E), D, w.KX, p.at(p.i_rb), p.ldrb, w.edge_x, w.ld_edge_x, p.at(bb.eh),
+                     D, e1, s);
+            }
             Epilogue e2;
             e2.bias = w.gate_b;
-            gemm(int(E), w.NG, D, p.at(bb.eh), D, w.gate, D, p.at(bb.gv), w.NG, e2, s);
+            {
+                Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
+                gemm(int(E), w.NG, D, p.at(bb.eh), D, w.gate, D, p.at(bb.gv), w.NG, e2, s);
+            }
         }
         MpArgs a = mp_args(m, p, r, b);
-        hipLaunchKernelGGL(k_mp_aggregate, dim3(N), dim3(kWave), 0, s, a);
+        {
+            Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+            hipLaunchKernelGGL(k_mp_aggregate, dim3(N), dim3(kWave), 0, s, a);
+        }
         RUNE_HIP_CHECK(hipGetLastError());
         Epilogue e3;
         e3.bias = w.up1_b;
@@ -720,18 +732,33 @@ float *messages_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Reco
         MpArgs a = mp_args(m, p, r, b);
         hipLaunchKernelGGL(k_mp_node_backward, dim3(N), dim3(kWave), 0, s, a);
         size_t lds = sizeof(float) * (H + 3 * std::max(c.vector_channels, 1));
-        hipLaunchKernelGGL(k_mp_edge_backward, dim3(N), dim3(kWave), lds, s, a);
-        hipLaunchKernelGGL(k_mp_neighbor_backward, dim3(N), dim3(kWave), 0, s, a);
+        {
+            Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+            hipLaunchKernelGGL(k_mp_edge_backward, dim3(N), dim3(kWave), lds, s, a);
+        }
+        {
+            Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+            hipLaunchKernelGGL(k_mp_neighbor_backward, dim3(N), dim3(kWave), 0, s, a);
+        }
         RUNE_HIP_CHECK(hipGetLastError());
         if (E > 0) {
             Epilogue e2;
             e2.dact_from = p.at(bb.ue);
             e2.ldu = D;
             e2.dact = act;
-            gemm(int(E), D, w.NG, p.at(p.t_dgv), w.NG, w.gate_T, w.NG, p.at(p.t_due), D, e2, s);
+            {
+                Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
+                gemm(int(E), D, w.NG, p.at(p.t_dgv), w.NG, w.gate_T, w.NG, p.at(p.t_due), D, e2, s);
+            }
             Epilogue e3;
-            gemm(int(E), w.KX, D, p.at(p.t_due), D, w.edge_xT, D, p.at(p.t_drb), p.ldrb, e3, s);
-            edge_rb_backward(m, p, r, p.at(p.t_drb), p.ldrb, s);
+            {
+                Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
+                gemm(int(E), w.KX, D, p.at(p.t_due), D, w.edge_xT, D, p.at(p.t_drb), p.ldrb, e3, s);
+            }
+            {
+                Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+                edge_rb_backward(m, p, r, p.at(p.t_drb), p.ldrb, s);
+            }
         }
         Epilogue e4;
         gemm(N, H, w.NP, p.at(p.t_dvs), w.NP, w.node_fT, w.NP, p.at(p.t_dz), H, e4, s);
@@ -739,7 +766,10 @@ float *messages_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Reco
         rms_backward(N, H, hin, H, p.at(bb.rin), p.at(p.t_dz), H, cur, H, next, H, s);
         cur = next;
     }
-    edge_direct(p, r, s);
+    {
+        Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+        edge_direct(p, r, s);
+    }
     p.g_direct_used = E > 0;
     return cur;
 }

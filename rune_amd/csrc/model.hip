@@ -452,6 +452,24 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
 
 ModelImpl::~ModelImpl() {
     for (auto &e : events) (void)hipEventDestroy(e);
+    for (auto &e : span_ev) (void)hipEventDestroy(e);
+}
+
+int ModelImpl::span_begin(int group, hipStream_t s) {
+    if (!timing || span_n >= kMaxSpans) return -1;
+    while (span_ev.size() < 2 * (span_n + 1)) {
+        hipEvent_t e;
+        RUNE_HIP_CHECK(hipEventCreate(&e));
+        span_ev.push_back(e);
+    }
+    if (span_grp.size() < span_n + 1) span_grp.resize(span_n + 1);
+    span_grp[span_n] = group;
+    RUNE_HIP_CHECK(hipEventRecord(span_ev[2 * span_n], s));
+    return int(span_n++);
+}
+
+void ModelImpl::span_end(int k, hipStream_t s) {
+    if (k >= 0) (void)hipEventRecord(span_ev[2 * size_t(k) + 1], s);
 }
 
 // ---- local (descriptor network) part ----
@@ -659,6 +677,26 @@ extern "C" int rune_model_timing(rune_model *model, int32_t enable) {
         RUNE_REQUIRE(model, RUNE_ERR_ARGUMENT, "null model");
         model->timing = enable != 0;
         model->timed_calls = 0;
+        model->span_n = 0;
+    });
+}
+
+extern "C" int rune_model_timing_groups(rune_model *model, double *ms, int64_t *launches) {
+    return guarded([&] {
+        RUNE_REQUIRE(model && ms, RUNE_ERR_ARGUMENT, "null argument");
+        for (int k = 0; k < RUNE_N_GROUPS; ++k) {
+            ms[k] = 0.0;
+            if (launches) launches[k] = 0;
+        }
+        for (size_t k = 0; k < model->span_n; ++k) {
+            RUNE_HIP_CHECK(hipEventSynchronize(model->span_ev[2 * k + 1]));
+            float t = 0.0f;
+            RUNE_HIP_CHECK(hipEventElapsedTime(&t, model->span_ev[2 * k],
+                                               model->span_ev[2 * k + 1]));
+            const int g = model->span_grp[k];
+            ms[g] += t;
+            if (launches) ++launches[g];
+        }
     });
 }
 

@@ -114,11 +114,31 @@ struct ModelImpl {
     bool timing = false;
     std::vector<hipEvent_t> events;       // kTimingRing x (RUNE_N_PHASES + 1)
     int64_t timed_calls = 0;
+    // kernel-group spans: events 2k, 2k + 1 bracket launch k of group span_grp[k]
+    std::vector<hipEvent_t> span_ev;
+    std::vector<int> span_grp;
+    size_t span_n = 0;
+    int span_begin(int group, hipStream_t s);
+    void span_end(int k, hipStream_t s);
     const std::vector<float> &tensor(const std::string &name) const;
     ~ModelImpl();
 };
 
 constexpr int kTimingRing = 256;
+constexpr size_t kMaxSpans = 1 << 16;
+
+// Brackets the launches issued in its scope with a group span (no-op unless
+// timing is enabled).
+struct Span {
+    ModelImpl &m;
+    hipStream_t s;
+    int k;
+    Span(ModelImpl &model, int group, hipStream_t stream)
+        : m(model), s(stream), k(model.span_begin(group, stream)) {}
+    ~Span() { m.span_end(k, s); }
+    Span(const Span &) = delete;
+    Span &operator=(const Span &) = delete;
+};
 
 using PackedLookup = std::function<const float *(const std::string &)>;
 
