@@ -9,8 +9,8 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-// GEMM tiling: 4 waves in 2x2, each wave (16*WM) x (16*WN) of the output;
-// block tile (32*WM) x (32*WN); K advances kBK = 32 per LDS stage.
+// GEMM tiling: 4 waves in WMW x (4 / WMW), each wave (16*WM) x (16*WN) of the
+// output; K advances kBK = 32 per LDS stage.
 constexpr int kBK = 32, kLdk = kBK + 4;
 
 // Logistic function from the hardware exp2 and reciprocal (v_exp_f32,
@@ -103,78 +103,23 @@ __device__ inline void store_stage(const float4 (&r)[kRows * 8 / 256], float *S,
     }
 }
 
-// C[M,N] = A[M,K] Bt[N,K]^T with the fused epilogue.  256 threads.
-// MFMA operand layout (v_mfma_f32_16x16x4f32): lane l supplies A[l%16][l/16]
-// and B[l/16][l%16]; accumulator register v of lane l is C[4*(l/16)+v][l%16].
-// The k index l/16 of MFMA step s in half h is LDS column 16h + 4(l/16) + s, so
-// each lane fetches its four steps with one 16-byte LDS read.  Row stride
-// kLdk = 36 floats keeps those reads free of bank conflicts.
-// Block b covers row tile b / nbn and column tile b % nbn.
-template <int WM, int WN, bool kVec>
-__global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *__restrict__ A,
-                                              int lda, const float *__restrict__ Bt, int ldb,
-                                              float *__restrict__ C, int ldc, Epilogue ep,
-                                              int nbn) {
-    constexpr int kBM = 32 * WM, BN = 32 * WN, kLdo = BN + 4;
-    static_assert(32 * kLdo <= (kBM + BN) * kLdk, "epilogue staging exceeds the tile LDS");
-    __shared__ __attribute__((aligned(16))) float smem[(kBM + BN) * kLdk];
-    float *As = smem, *Bs = smem + kBM * kLdk;
+// Epilogue of a (32*WM) x (32*WN) tile through LDS, 32 rows of the tile at a
+// time: the waves owning those rows store their accumulators (row stride
+// kLdo = BN + 4 puts the four lane groups on distinct banks); the rows' own
+// data goes to LDS; then all 256 threads apply the epilogue row-contiguously,
+// kB elements per thread at once so that each term's loads are issued
+// together.  Out-of-range elements load from clamped indices and store
+// nothing.  smem must hold 32 * (32 * WN + 4) floats and be free to reuse.
+template <int WM, int WN, int WMW>
+__device__ inline void tile_epilogue(floatx4 (&acc)[WM][WN], float *smem, int M, int N,
+                                     float *__restrict__ C, int ldc, const Epilogue &ep,
+                                     int m0, int n0) {
+    constexpr int WNW = 4 / WMW;
+    constexpr int kBM = 16 * WM * WMW, BN = 16 * WN * WNW, kLdo = BN + 4;
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
-    const int m0 = (blockIdx.x / nbn) * kBM, n0 = (blockIdx.x % nbn) * BN;
-    const int wm = (wave >> 1) * 16 * WM, wn = (wave & 1) * 16 * WN;
+    const int wn = (wave % WNW) * 16 * WN;
     const int g = lane >> 4, rr = lane & 15;
-    floatx4 acc[WM][WN];
-#pragma unroll
-    for (int a = 0; a < WM; ++a)
-#pragma unroll
-        for (int b = 0; b < WN; ++b) acc[a][b] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    float4 ra[kBM * 8 / 256], rb[BN * 8 / 256];
-    auto fetch = [&](int k0) {
-        if (kVec && k0 + kBK <= K) {
-            load_stage_full<kBM>(ra, A, lda, m0, M, k0, tid);
-            load_stage_full<BN>(rb, Bt, ldb, n0, N, k0, tid);
-        } else {
-            load_stage<kBM, kVec>(ra, A, lda, m0, M, k0, K, tid);
-            load_stage<BN, kVec>(rb, Bt, ldb, n0, N, k0, K, tid);
-        }
-    };
-    fetch(0);
-    for (int k0 = 0; k0 < K; k0 += kBK) {
-        store_stage<kBM>(ra, As, tid);
-        store_stage<BN>(rb, Bs, tid);
-        __syncthreads();
-        if (k0 + kBK < K) fetch(k0 + kBK);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            float4 fa[WM], fb[WN];
-#pragma unroll
-            for (int a = 0; a < WM; ++a)
-                fa[a] = *reinterpret_cast<const float4 *>(As + (wm + 16 * a + rr) * kLdk +
-                                                          16 * h + 4 * g);
-#pragma unroll
-            for (int b = 0; b < WN; ++b)
-                fb[b] = *reinterpret_cast<const float4 *>(Bs + (wn + 16 * b + rr) * kLdk +
-                                                          16 * h + 4 * g);
-#pragma unroll
-            for (int a = 0; a < WM; ++a)
-#pragma unroll
-                for (int b = 0; b < WN; ++b) {
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a].x, fb[b].x, acc[a][b], 0, 0, 0);
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a].y, fb[b].y, acc[a][b], 0, 0, 0);
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a].z, fb[b].z, acc[a][b], 0, 0, 0);
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a].w, fb[b].w, acc[a][b], 0, 0, 0);
-                }
-        }
-        __syncthreads();
-    }
-    // Epilogue through LDS, 32 rows of the tile at a time: the waves owning
-    // those rows store their accumulators (row stride kLdo = BN + 4 puts
-    // the four lane groups on distinct banks); the rows' own data goes to
-    // LDS; then all 256 threads apply the epilogue row-contiguously, kB
-    // elements per thread at once so that each term's loads are issued
-    // together.  Out-of-range elements load from clamped indices and store
-    // nothing.
     constexpr int kE = 32 * BN / 256;
     constexpr int kB = kE % 12 == 0 ? 12 : kE % 10 == 0 ? 10 : kE % 8 == 0 ? 8 : 4;
     static_assert(kE % kB == 0, "epilogue batch must divide the per-thread count");
@@ -185,7 +130,7 @@ __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *
         // accumulator row block a of this wave is 16-row block blk of the tile
 #pragma unroll
         for (int a = 0; a < WM; ++a) {
-            const int blk = (wave >> 1) * WM + a;
+            const int blk = (wave / WNW) * WM + a;
             if ((blk >> 1) == part) {
 #pragma unroll
                 for (int b = 0; b < WN; ++b)
@@ -257,6 +202,76 @@ __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *
         }
         __syncthreads();
     }
+}
+
+// C[M,N] = A[M,K] Bt[N,K]^T with the fused epilogue.  256 threads in WMW x
+// (4 / WMW) waves, each (16*WM) x (16*WN) of the output.
+// MFMA operand layout (v_mfma_f32_16x16x4f32): lane l supplies A[l%16][l/16]
+// and B[l/16][l%16]; accumulator register v of lane l is C[4*(l/16)+v][l%16].
+// The k index l/16 of MFMA step s in half h is LDS column 16h + 4(l/16) + s, so
+// each lane fetches its four steps with one 16-byte LDS read.  Row stride
+// kLdk = 36 floats keeps those reads free of bank conflicts.
+// Block b covers row tile b / nbn and column tile b % nbn.
+template <int WM, int WN, int WMW, bool kVec>
+__global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *__restrict__ A,
+                                              int lda, const float *__restrict__ Bt, int ldb,
+                                              float *__restrict__ C, int ldc, Epilogue ep,
+                                              int nbn) {
+    constexpr int WNW = 4 / WMW;
+    constexpr int kBM = 16 * WM * WMW, BN = 16 * WN * WNW, kLdo = BN + 4;
+    static_assert(32 * kLdo <= (kBM + BN) * kLdk, "epilogue staging exceeds the tile LDS");
+    __shared__ __attribute__((aligned(16))) float smem[(kBM + BN) * kLdk];
+    float *As = smem, *Bs = smem + kBM * kLdk;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int m0 = (blockIdx.x / nbn) * kBM, n0 = (blockIdx.x % nbn) * BN;
+    const int wm = (wave / WNW) * 16 * WM, wn = (wave % WNW) * 16 * WN;
+    const int g = lane >> 4, rr = lane & 15;
+    floatx4 acc[WM][WN];
+#pragma unroll
+    for (int a = 0; a < WM; ++a)
+#pragma unroll
+        for (int b = 0; b < WN; ++b) acc[a][b] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    float4 ra[kBM * 8 / 256], rb[BN * 8 / 256];
+    auto fetch = [&](int k0) {
+        if (kVec && k0 + kBK <= K) {
+            load_stage_full<kBM>(ra, A, lda, m0, M, k0, tid);
+            load_stage_full<BN>(rb, Bt, ldb, n0, N, k0, tid);
+        } else {
+            load_stage<kBM, kVec>(ra, A, lda, m0, M, k0, K, tid);
+            load_stage<BN, kVec>(rb, Bt, ldb, n0, N, k0, K, tid);
+        }
+    };
+    fetch(0);
+    for (int k0 = 0; k0 < K; k0 += kBK) {
+        store_stage<kBM>(ra, As, tid);
+        store_stage<BN>(rb, Bs, tid);
+        __syncthreads();
+        if (k0 + kBK < K) fetch(k0 + kBK);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float4 fa[WM], fb[WN];
+#pragma unroll
+            for (int a = 0; a < WM; ++a)
+                fa[a] = *reinterpret_cast<const float4 *>(As + (wm + 16 * a + rr) * kLdk +
+                                                          16 * h + 4 * g);
+#pragma unroll
+            for (int b = 0; b < WN; ++b)
+                fb[b] = *reinterpret_cast<const float4 *>(Bs + (wn + 16 * b + rr) * kLdk +
+                                                          16 * h + 4 * g);
+#pragma unroll
+            for (int a = 0; a < WM; ++a)
+#pragma unroll
+                for (int b = 0; b < WN; ++b) {
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a].x, fb[b].x, acc[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a].y, fb[b].y, acc[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a].z, fb[b].z, acc[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a].w, fb[b].w, acc[a][b], 0, 0, 0);
+                }
+        }
+        __syncthreads();
+    }
+    tile_epilogue<WM, WN, WMW>(acc, smem, M, N, C, ldc, ep, m0, n0);
 }
 
 __device__ inline float wave_sum(float v) {
@@ -350,32 +365,26 @@ __global__ void k_nep_mlp(int M, int Q, int Hn, const float *q, int ldq, const i
 
 }  // namespace
 
-// Column tile 32*WN with the least padding of N; ties go to the wider tile.
-static int pick_wn(int N) {
-    const int opts[4] = {9, 6, 4, 2};
-    int best = 2, waste = 1 << 30;
-    for (int wn : opts) {
-        int bn = 32 * wn, w = ceil_div(N, bn) * bn - N;
-        if (w < waste) {
-            waste = w;
-            best = wn;
-        }
-    }
-    return best;
-}
+// Block tiles are 64 rows by 64 or 32 columns: narrow tiles keep each wave
+// at 16-32 accumulator rows and 4-7 waves per SIMD, which hides the operand
+// and epilogue latency better than wide tiles (measured on the per-record
+// GEMMs: 64x64 / 64x32 beat 64x192 / 64x288 by 15-25 %).  The 32-column
+// tile is taken when it pads N less.
+static bool narrow_tile(int N) { return ceil_div(N, 32) * 32 < ceil_div(N, 64) * 64; }
 
-template <int WM, int WN>
+template <int WM, int WN, int WMW = 2>
 static void launch_gemm(bool vec, int M, int N, int K, const float *A, int lda, const float *Bt,
                         int ldb, float *C, int ldc, const Epilogue &ep, hipStream_t s) {
-    int nbn = ceil_div(N, 32 * WN);
-    int64_t blocks = int64_t(ceil_div(M, 32 * WM)) * nbn;
+    constexpr int kBM = 16 * WM * WMW, BN = 16 * WN * (4 / WMW);
+    int nbn = ceil_div(N, BN);
+    int64_t blocks = int64_t(ceil_div(M, kBM)) * nbn;
     if (blocks > 0x7fffffff) throw Error(RUNE_ERR_ARGUMENT, "gemm: problem too large");
     if (vec)
-        hipLaunchKernelGGL((k_gemm<WM, WN, true>), dim3(unsigned(blocks)), dim3(256), 0, s, M, N,
-                           K, A, lda, Bt, ldb, C, ldc, ep, nbn);
-    else
-        hipLaunchKernelGGL((k_gemm<WM, WN, false>), dim3(unsigned(blocks)), dim3(256), 0, s, M,
+        hipLaunchKernelGGL((k_gemm<WM, WN, WMW, true>), dim3(unsigned(blocks)), dim3(256), 0, s, M,
                            N, K, A, lda, Bt, ldb, C, ldc, ep, nbn);
+    else
+        hipLaunchKernelGGL((k_gemm<WM, WN, WMW, false>), dim3(unsigned(blocks)), dim3(256), 0, s,
+                           M, N, K, A, lda, Bt, ldb, C, ldc, ep, nbn);
 }
 
 void gemm(int M, int N, int K, const float *A, int lda, const float *Bt, int ldb, float *C,
@@ -383,12 +392,10 @@ void gemm(int M, int N, int K, const float *A, int lda, const float *Bt, int ldb
     if (M == 0 || N == 0) return;
     bool vec = lda % 4 == 0 && ldb % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
                (reinterpret_cast<uintptr_t>(Bt) & 15) == 0;
-    switch (pick_wn(N)) {
-    case 9: launch_gemm<2, 9>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s); break;
-    case 6: launch_gemm<2, 6>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s); break;
-    case 4: launch_gemm<2, 4>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s); break;
-    default: launch_gemm<2, 2>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s); break;
-    }
+    if (narrow_tile(N))
+        launch_gemm<1, 2, 4>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s);
+    else
+        launch_gemm<2, 2, 2>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s);
     RUNE_HIP_CHECK(hipGetLastError());
 }
 
