@@ -97,6 +97,8 @@ struct EqArgs {
     float *dgg;               // [E, NG]
     float4 *dv;               // [E]
     float *dfc;               // [E] dE/dfc of the message terms, all blocks
+    float *dd;                // [E] dE/dd of the radial-basis inputs, all blocks
+    const float *rbd;         // [E, ldrb] distance derivative of the radial basis
     float *dy;                // [E, nq] dE/dY, centre-side shares
     float *dyn;               // [E, nq] dE/dY, neighbour-side shares
     float *dnode;             // [N, NP]
@@ -725,11 +727,12 @@ __global__ void __launch_bounds__(kBlock) k_eq_atom_dir(EqArgs a) {
         for (int t0 = b0; t0 < b1; t0 += kWave) {
             const int cnt = min(kWave, b1 - t0);
             int me = -1;
-            float mf = 0.0f;
+            float mf = 0.0f, mdd = 0.0f;
             wave_sync();
             if (ln.lane < cnt) {
                 me = side ? a.r.tidx[t0 + ln.lane] : t0 + ln.lane;
                 mf = side ? a.tfc[t0 + ln.lane] : a.fc[t0 + ln.lane];
+                if (!side) mdd = a.dd[me];
                 if (mf != 0.0f) {
                     float y[NQ];
                     load_row(y, a.harm + size_t(me) * NQ);
@@ -739,13 +742,19 @@ __global__ void __launch_bounds__(kBlock) k_eq_atom_dir(EqArgs a) {
             }
             wave_sync();
             constexpr int KQ = (NQ + W - 1) / W;   // dE/dY components per lane
+            // centre side: radial-basis adjoint terms dE/drb_k drb_k/dd (k = c, c + W)
             auto fetch = [&](int q, int &e, float (&dxv)[LQ], float (&ti)[LQ], float (&yo)[KQ],
-                             float &f) {
+                             float &rbt, float &f) {
                 e = bcast(me, min(q, kWave - 1));
                 f = bcast(mf, min(q, kWave - 1));
+                rbt = 0.0f;
                 if (q >= cnt) {
                     e = -1;
                     f = 0.0f;
+                }
+                if (!side && f != 0.0f) {
+                    for (int k = ln.c; k < kb; k += W)
+                        rbt += a.dx[size_t(e) * a.ldx + k] * a.rbd[size_t(e) * a.ldrb + k];
                 }
                 if (f != 0.0f) {
 #pragma unroll
@@ -765,13 +774,18 @@ __global__ void __launch_bounds__(kBlock) k_eq_atom_dir(EqArgs a) {
                 }
             };
             int e;
-            float dxv[LQ], tI[LQ], yo[KQ], fc;
-            fetch(ln.slot, e, dxv, tI, yo, fc);
+            float dxv[LQ], tI[LQ], yo[KQ], rbt, fc;
+            fetch(ln.slot, e, dxv, tI, yo, rbt, fc);
             for (int q0 = 0; q0 < cnt; q0 += S) {
                 const int q = q0 + ln.slot;
                 int en;
-                float dxn[LQ], tIn[LQ], yon[KQ], fcn;
-                fetch(q + S, en, dxn, tIn, yon, fcn);
+                float dxn[LQ], tIn[LQ], yon[KQ], rbtn, fcn;
+                fetch(q + S, en, dxn, tIn, yon, rbtn, fcn);
+                if (!side) {
+                    const float sum = group_sum(rbt, W);
+                    const float dold = bcast(mdd, min(q, kWave - 1));
+                    if (fc != 0.0f && ln.c == 0) a.dd[e] = dold + sum;
+                }
                 const bool on = fc != 0.0f && ln.act;
                 float Y[NQ];
 #pragma unroll
@@ -810,6 +824,7 @@ __global__ void __launch_bounds__(kBlock) k_eq_atom_dir(EqArgs a) {
                 copy(dxv, dxn);
                 copy(tI, tIn);
                 copy(yo, yon);
+                rbt = rbtn;
                 fc = fcn;
             }
         }
@@ -907,7 +922,8 @@ __global__ void __launch_bounds__(kWave) k_eq_encoder_backward(const float *ddir
 // dE/du of the harmonics: sum_k dY_k scale_k db_k/du, added to dv.xyz.
 template <int LQ>
 __global__ void k_eq_harmonic_backward(int64_t E, Records r, const float *fcv, const float *dy,
-                                       const float *dyn, const float *dfc, float cutoff,
+                                       const float *dyn, const float *dfc, const float *dd,
+                                       float cutoff,
                                        const float *ztab, EdgeZ zoff, const float *scale,
                                        float4 *dv) {
     constexpr int NQ = LQ * (LQ + 2);
@@ -965,7 +981,7 @@ __global__ void k_eq_harmonic_backward(int64_t E, Records r, const float *fcv, c
     acc.x += dx;
     acc.y += dyy;
     acc.z += dz;
-    if (fcv[e] != 0.0f) acc.w += dfc[e] * cutoff_slope(v.w, cutoff);
+    if (fcv[e] != 0.0f) acc.w += dfc[e] * cutoff_slope(v.w, cutoff) + dd[e];
     dv[e] = acc;
 }
 
@@ -1214,6 +1230,8 @@ MessagePlan plan_equivariant(ModelImpl &m, Arena &ar, int N, int64_t E) {
     p.i_dharm = p.add(ar, 4 * e * nq);
     p.i_dharm_n = p.add(ar, 4 * e * nq);
     p.i_dfc = p.add(ar, 4 * e);
+    p.i_dd = p.add(ar, 4 * e);
+    p.i_rbd = p.add(ar, 4 * e * p.ldrb);
     int dir0 = p.add(ar, 4 * n * CN);
     int x = p.add(ar, 4 * e * ldx);        // shared by the blocks (forward only)
     int eh = p.add(ar, 4 * e * D);         // shared
@@ -1301,6 +1319,8 @@ static EqArgs eq_args(ModelImpl &m, MessagePlan &p, const Records &r, int b) {
     a.dgg = p.at(p.t_dgv);
     a.dv = reinterpret_cast<float4 *>(p.at(p.i_dv));
     a.dfc = p.at(p.i_dfc);
+    a.dd = p.at(p.i_dd);
+    a.rbd = p.at(p.i_rbd);
     a.dy = p.at(p.i_dharm);
     a.dyn = p.at(p.i_dharm_n);
     a.dnode = p.at(p.t_dvs);
@@ -1334,6 +1354,7 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dharm), 0, 4 * size_t(E) * nq, s));
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dharm_n), 0, 4 * size_t(E) * nq, s));
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dfc), 0, 4 * size_t(E), s));
+        RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dd), 0, 4 * size_t(E), s));
     }
     hipLaunchKernelGGL(k_eq_encode, dim3(N), dim3(kWave), 0, s, N, moments, m.desc.na,
                        m.desc.nlm, m.enc_w, m.harm_scale, C, nq, p.at(p.blocks[0].dir_in));
@@ -1463,10 +1484,6 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
                 Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
                 gemm(int(E), w.KX, D, p.at(p.t_due), D, w.edge_xT, D, p.at(p.t_dx), a.ldx, e3, s);
             }
-            {
-                Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
-                edge_rb_backward(m, p, r, p.at(p.t_dx), a.ldx, s);
-            }
         }
         {
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
@@ -1496,7 +1513,7 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
             EQ_LAUNCH(k_eq_harmonic_backward, lq, dim3(ceil_div(E, 256)), dim3(256), 0, s, E, r,
                       p.at(p.i_fc), p.at(p.i_dharm), p.at(p.i_dharm_n), p.at(p.i_dfc),
-                      float(c.message_cutoff), m.desc.z, zo, m.harm_scale,
+                      p.at(p.i_dd), float(c.message_cutoff), m.desc.z, zo, m.harm_scale,
                       reinterpret_cast<float4 *>(p.at(p.i_dv)));
         }
     }

@@ -28,44 +28,77 @@ __device__ inline float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // ---- shared edge preparation ----
 
-__global__ void k_edge_prep(EdgePrepArgs a) {
-    int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (e >= a.E) return;
-    int i = a.r.ctr[e];
-    bool in_r = e >= a.r.view[4 * i] && e < a.r.view[4 * i + 1];
-    float4 v = a.r.vec[e];
-    float d = v.w;
-    float rc = a.cutoff;
-    float fc = 0.0f;
-    float *rb = a.rb + size_t(e) * a.ldrb;
-    for (int k = 0; k < a.ldrb; ++k) rb[k] = 0.0f;
-    if (in_r && d < rc) {
-        fc = 0.5f * cosf(kPi * d / rc) + 0.5f;
-        float x = 2.0f * (d / rc - 1.0f) * (d / rc - 1.0f) - 1.0f;
-        float half = 0.5f * fc;
-        float t2 = 1.0f, t1 = x;
-        rb[0] = 2.0f * half;
-        if (a.kb > 1) rb[1] = (x + 1.0f) * half;
-        for (int k = 2; k < a.kb; ++k) {
-            float t = 2.0f * x * t1 - t2;
-            t2 = t1;
-            t1 = t;
-            rb[k] = (t + 1.0f) * half;
+// One block of 256 threads prepares 256 consecutive records: each thread
+// forms its record's rows (masked Chebyshev basis, its distance derivative,
+// normalised harmonics) in LDS, then the block writes the tiles out as
+// contiguous float4 streams.
+__global__ void __launch_bounds__(256) k_edge_prep(EdgePrepArgs a) {
+    extern __shared__ float tile[];
+    const int ld = a.ldrb, nq = a.harm ? a.nq : 0;
+    float *rbL = tile, *rdL = rbL + 256 * ld, *yL = rdL + (a.rbd ? 256 * ld : 0);
+    const int64_t e0 = int64_t(blockIdx.x) * 256;
+    const int t = threadIdx.x;
+    const int64_t e = e0 + t;
+    const int rows = int(min<int64_t>(256, a.E - e0));
+    if (e < a.E) {
+        int i = a.r.ctr[e];
+        bool in_r = e >= a.r.view[4 * i] && e < a.r.view[4 * i + 1];
+        float4 v = a.r.vec[e];
+        float d = v.w;
+        float rc = a.cutoff;
+        float fc = 0.0f;
+        float *rb = rbL + t * ld, *rd = rdL + t * ld;
+        for (int k = 0; k < ld; ++k) rb[k] = 0.0f;
+        if (a.rbd)
+            for (int k = 0; k < ld; ++k) rd[k] = 0.0f;
+        if (in_r && d < rc) {
+            fc = 0.5f * cosf(kPi * d / rc) + 0.5f;
+            const float fp = -0.5f * kPi / rc * sinf(kPi * d / rc);
+            const float rs = d / rc - 1.0f;
+            const float x = 2.0f * rs * rs - 1.0f, dxdr = 4.0f * rs / rc;
+            float half = 0.5f * fc;
+            float t2 = 1.0f, t1 = x, u2 = 1.0f, u1 = 2.0f * x;
+            rb[0] = 2.0f * half;
+            if (a.kb > 1) rb[1] = (x + 1.0f) * half;
+            if (a.rbd) {
+                rd[0] = fp;
+                if (a.kb > 1) rd[1] = 0.5f * dxdr * fc + 0.5f * (x + 1.0f) * fp;
+            }
+            for (int k = 2; k < a.kb; ++k) {
+                float tn = 2.0f * x * t1 - t2;
+                float un = 2.0f * x * u1 - u2;
+                rb[k] = (tn + 1.0f) * half;
+                if (a.rbd) rd[k] = 0.5f * float(k) * u1 * dxdr * fc + 0.5f * (tn + 1.0f) * fp;
+                t2 = t1;
+                t1 = tn;
+                u2 = u1;
+                u1 = un;
+            }
+        }
+        a.fc[e] = fc;
+        a.pair[e] = a.types[i] * a.n_types + a.types[a.r.nbr[e]];
+        a.dv[e] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (a.harm) {
+            // normalised real harmonics Y = b(r_hat) * scale (descriptor.py:643-648)
+            float *y = yL + t * nq;
+            if (!in_r) {
+                for (int c = 0; c < nq; ++c) y[c] = 0.0f;
+            } else {
+                float inv = 1.0f / fmaxf(d, 1.0e-12f);
+                harmonics(a.z, a.z_off, a.lq, v.x * inv, v.y * inv, v.z * inv, a.scale, y);
+            }
         }
     }
-    a.fc[e] = fc;
-    a.pair[e] = a.types[i] * a.n_types + a.types[a.r.nbr[e]];
-    a.dv[e] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (a.harm) {
-        // normalised real harmonics Y = b(r_hat) * scale (descriptor.py:643-648)
-        float *y = a.harm + size_t(e) * a.nq;
-        if (!in_r) {
-            for (int c = 0; c < a.nq; ++c) y[c] = 0.0f;
-        } else {
-            float inv = 1.0f / fmaxf(d, 1.0e-12f);
-            harmonics(a.z, a.z_off, a.lq, v.x * inv, v.y * inv, v.z * inv, a.scale, y);
-        }
+    __syncthreads();
+    // ld is a multiple of 4; the harmonic rows are copied as plain floats
+    const int n4 = rows * ld / 4;
+    for (int q = t; q < n4; q += 256) {
+        reinterpret_cast<float4 *>(a.rb + size_t(e0) * ld)[q] = reinterpret_cast<float4 *>(rbL)[q];
+        if (a.rbd)
+            reinterpret_cast<float4 *>(a.rbd + size_t(e0) * ld)[q] =
+                reinterpret_cast<float4 *>(rdL)[q];
     }
+    for (int q = t; q < rows * nq; q += 256) a.harm[size_t(e0) * nq + q] = yL[q];
 }
 
 // d/dr of the masked Chebyshev basis, accumulated into dv.w:  sum_k drb_k f_k'(d)
@@ -585,6 +618,7 @@ void edge_prep(ModelImpl &m, MessagePlan &p, const Records &r, const int32_t *ty
     a.kb = m.cfg.message_basis_size;
     a.ldrb = p.ldrb;
     a.rb = p.at(p.i_rb);
+    a.rbd = p.i_rbd >= 0 ? p.at(p.i_rbd) : nullptr;
     a.fc = p.at(p.i_fc);
     a.pair = reinterpret_cast<int32_t *>(p.at(p.i_pair));
     a.dv = reinterpret_cast<float4 *>(p.at(p.i_dv));
@@ -594,7 +628,15 @@ void edge_prep(ModelImpl &m, MessagePlan &p, const Records &r, const int32_t *ty
     a.nq = nq;
     a.z = m.desc.z;
     for (int k = 0; k < kMaxL + 2; ++k) a.z_off[k] = m.desc.z_off[k];
-    hipLaunchKernelGGL(k_edge_prep, dim3(edge_grid(p.E)), dim3(256), 0, s, a);
+    const size_t lds = sizeof(float) * 256 * ((a.rbd ? 2 : 1) * size_t(a.ldrb) + (harm ? nq : 0));
+    static bool raised = false;   // LDS beyond the default dynamic limit (large nq)
+    if (!raised) {
+        RUNE_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_edge_prep),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           160 * 1024));
+        raised = true;
+    }
+    hipLaunchKernelGGL(k_edge_prep, dim3(edge_grid(p.E)), dim3(256), lds, s, a);
     RUNE_HIP_CHECK(hipGetLastError());
 }
 

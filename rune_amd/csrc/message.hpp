@@ -13,6 +13,7 @@ struct EdgePrepArgs {
     float cutoff;          // message_cutoff
     int kb, ldrb;          // message basis size, row stride of rb
     float *rb;             // [E, ldrb] masked Chebyshev basis (message.py:108-110)
+    float *rbd;            // [E, ldrb] its derivative with respect to the distance, or null
     float *fc;             // [E] cosine cutoff, 0 outside the radial list
     int32_t *pair;         // [E] t_i * T + t_j
     float4 *dv;            // [E] zeroed: (dE/du, dE/dd) accumulators

@@ -77,7 +77,7 @@ struct MessagePlan {
     size_t o_gd = 0, o_dmom = 0;
     int ldrb = 0, ldrb_x = 0;
     int i_rb = -1, i_fc = -1, i_tfc = -1, i_pair = -1, i_dv = -1, i_harm = -1, i_dharm = -1, i_dharm_n = -1;
-    int i_dfc = -1;
+    int i_dfc = -1, i_dd = -1, i_rbd = -1;
     std::vector<BlockBuffers> blocks;
     // reverse-pass temporaries shared by the blocks
     int t_dz1 = -1, t_duin = -1, t_dmsg = -1, t_dvsum = -1, t_dgv = -1, t_due = -1;
