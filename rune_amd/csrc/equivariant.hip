@@ -12,6 +12,7 @@
 // at L*L-1 .. L*L+2L-1), matching direction[..., start:stop] of the reference.
 #include <cmath>
 
+#include "activation.hpp"
 #include "message.hpp"
 
 namespace rune {
@@ -86,7 +87,14 @@ struct EqArgs {
     float *dir_out;           // [N, C*nq]
     const float *mixw;        // [lq, C, C]
     float *mixst;             // [N, C*nq] channel-mixed dir_in
-    float *x;                 // [E, ldx] edge features
+    int act;                  // activation of the edge MLP
+    int wlds;                 // LDS floats per wave of the edge-MLP kernels
+    const int32_t *pair;      // [E] pair type index
+    const float *pair_proj;   // [T*T, D]
+    const float *wpc, *wpn;   // [lq*C, D] probe weights (neighbour side signed)
+    const float *wrb;         // [kb, D] radial-basis weights
+    int ldd;                  // row stride of ue, eh, due (a multiple of 64 DMC)
+    float *ue, *eh;           // [E, D] edge MLP pre-activation, activation
     const float *ag;          // [E, NG] activated gates (sigmoid | tanh)
     float *msg, *rm, *uin;    // [N, H], [N], [N, H + lq*C]
     // reverse
@@ -243,69 +251,241 @@ __global__ void __launch_bounds__(256) k_eq_mix(int N, const float *mixw, const 
 __device__ inline int bcast(int v, int src) { return __shfl(v, src, kWave); }
 __device__ inline float bcast(float v, int src) { return __shfl(v, src, kWave); }
 
-// Edge features [rb | probes_c | probes_n] = [rb | H_i.Y | (-1)^L H_j.Y].
-// The wave of atom n holds H_n in registers and fills the probes of its own
-// records (n = centre: rb and probes_c, all records of the segment) and of
-// the records that see it as neighbour (probes_n), so no state row is
-// gathered.
-template <int LQ, int S>
-__global__ void __launch_bounds__(kBlock) k_eq_features(EqArgs a) {
+__device__ inline int lane_get(int v, int q) { return __builtin_amdgcn_readlane(v, q); }
+__device__ inline float lane_get(float v, int q) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), q));
+}
+
+// ---- factored edge MLP ----
+// The probe columns of edge_mlp.0 act on p_c[L, c] = sum_m H_i[c, Lm] Y[Lm]
+// and p_n[L, c] = (-1)^L sum_m H_j[c, Lm] Y[Lm] (equivariant.py:169-180).
+// Contracting the channels first, W_pc p_c = sum_k Y[k] Qc_i[k, :] with
+// Qc_i[k, d] = sum_c W_pc[d, (L(k), c)] H_i[c, k], and likewise Qn_j with
+// the sign folded into the packed weights: NQ terms per record and output
+// column instead of 2 LQ C.  The wave of an atom builds its Q in registers
+// from its state row, so no per-record feature row is stored.
+//
+// Lanes own output columns d = d0 + lane + 64 u (u < DMC); a launch covers
+// D in gridDim.y column blocks of 64 DMC, and the per-record [E, D] arrays
+// have a row stride ldd that is a multiple of 64 DMC, so every lane loads and
+// stores without a branch (loads of columns >= D read column D - 1, and the
+// padding columns hold values nobody reads).  Branch-free loads keep the
+// compiler's memory-counter waits exact, so prefetched loads stay in flight.
+
+// Radial-basis weights held in registers; a longer basis reads the rest from L2.
+constexpr int kRbRegs = 20;
+
+template <int DMC>
+struct EdgeCols {
+    int d[DMC];    // owned column (store index, < ldd)
+    int dl[DMC];   // clamped column (load index, < D)
+    __device__ explicit EdgeCols(int D) {
+        const int d0 = int(blockIdx.y) * kWave * DMC + int(threadIdx.x & (kWave - 1));
+#pragma unroll
+        for (int u = 0; u < DMC; ++u) {
+            d[u] = d0 + kWave * u;
+            dl[u] = min(d[u], D - 1);
+        }
+    }
+};
+
+// Q[k][u] = sum_c Hs[c, k] Wp[(L(k) - 1) C + c, dl[u]], Hs the atom's state
+// row [C, NQ] staged in the wave's LDS.  The weights of channel c + 1 are
+// loaded while channel c is applied.
+template <int LQ, int DMC>
+__device__ inline void project_state(const float *Hs, const float *__restrict__ Wp, int C, int D,
+                                     const int (&dl)[DMC], float (&Q)[LQ * (LQ + 2)][DMC]) {
+    constexpr int NQ = LQ * (LQ + 2);
+#pragma unroll
+    for (int k = 0; k < NQ; ++k)
+#pragma unroll
+        for (int u = 0; u < DMC; ++u) Q[k][u] = 0.0f;
+#pragma unroll
+    for (int L = 1; L <= LQ; ++L) {
+        const int st = L * L - 1;
+        const float *wl = Wp + size_t(L - 1) * C * D;
+        float w[DMC];
+#pragma unroll
+        for (int u = 0; u < DMC; ++u) w[u] = wl[dl[u]];
+        for (int c = 0; c < C; ++c) {
+            float wn[DMC];
+            const int cn = min(c + 1, C - 1);
+#pragma unroll
+            for (int u = 0; u < DMC; ++u) wn[u] = wl[size_t(cn) * D + dl[u]];
+#pragma unroll
+            for (int m = 0; m < 2 * L + 1; ++m) {
+                const float h = Hs[c * NQ + st + m];
+#pragma unroll
+                for (int u = 0; u < DMC; ++u) Q[st + m][u] += h * w[u];
+            }
+#pragma unroll
+            for (int u = 0; u < DMC; ++u) w[u] = wn[u];
+        }
+    }
+}
+
+__device__ inline void stage_state(float *Hs, const float *__restrict__ row, int CN) {
+    const int lane = threadIdx.x & (kWave - 1);
+    for (int o = lane; o < CN; o += kWave) Hs[o] = row[o];
+    wave_sync();
+}
+
+// Harmonic row (and radial-basis row when R) of record e into the wave's LDS
+// slot of lane q: every lane of the chunk loads (the rows of records with
+// fc = 0 are finite and their results are discarded).
+template <int NQ, int LY>
+__device__ inline void stage_record(const EqArgs &a, int e, float *Yc, float *Rc, int q) {
+    float y[NQ];
+    load_row(y, a.harm + size_t(e) * NQ);
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) Yc[q * LY + k] = y[k];
+    if (Rc) {
+        const float4 *rb = reinterpret_cast<const float4 *>(a.rb + size_t(e) * a.ldrb);
+        for (int k = 0; k < a.ldrb / 4; ++k)
+            reinterpret_cast<float4 *>(Rc + q * a.ldrb)[k] = rb[k];
+    }
+}
+
+// Neighbour side: for every record e that sees atom j as neighbour,
+// ue[e, :] = B_j + pair_proj[pair_e] + (fc != 0: Qn_j Y_e + W_rb rb_e).  The
+// harmonic and radial-basis rows of a chunk of 64 records are gathered into
+// LDS with one lane-parallel load; the pair row (a small table) of the next
+// record is loaded while the current one is computed.
+template <int LQ, int DMC>
+__global__ void __launch_bounds__(kBlock) k_eq_edge_nbr(EqArgs a) {
     constexpr int NQ = LQ * (LQ + 2), LY = NQ + (NQ % 4 == 0 ? 4 : 1);
-    using Ln = Lanes<S>;
     extern __shared__ float lds[];
-    const int n = wave_atom(a.r);
-    if (n < 0) return;
-    const Ln ln(a.C);
-    const int C = a.C, CN = C * NQ, LC = LQ * C, kb = a.kb;
-    // harmonic rows of the current chunk of 64 records, one row per record
-    float *Yc = lds + (threadIdx.x >> 6) * kWave * LY;
-    float Hn[NQ];
-    zero(Hn);
-    if (ln.act) load_row(Hn, a.dir_in + size_t(n) * CN + ln.c * NQ);
+    const int j = wave_atom(a.r);
+    if (j < 0) return;
+    const int lane = threadIdx.x & (kWave - 1), C = a.C, D = a.D, CN = C * NQ, kb = a.kb;
+    const int LR = a.ldrb, ldd = a.ldd;
+    float *Yc = lds + (threadIdx.x >> 6) * a.wlds;
+    float *Rc = Yc + kWave * LY;
+    const EdgeCols<DMC> col(D);
+    float Q[NQ][DMC];
+    stage_state(Yc, a.dir_in + size_t(j) * CN, CN);
+    project_state<LQ, DMC>(Yc, a.wpn, C, D, col.dl, Q);
+    float wr[kRbRegs][DMC], Bj[DMC];
 #pragma unroll
-    for (int side = 0; side < 2; ++side) {
-        const int b0 = side ? a.r.tptr[n] : a.r.ptr[n];
-        const int b1 = side ? a.r.tptr[n + 1] : a.r.ptr[n + 1];
-        for (int t0 = b0; t0 < b1; t0 += kWave) {
-            const int cnt = min(kWave, b1 - t0);
-            int me = -1;
-            float mf = 0.0f;
-            wave_sync();
-            if (ln.lane < cnt) {
-                me = side ? a.r.tidx[t0 + ln.lane] : t0 + ln.lane;
-                mf = side ? a.tfc[t0 + ln.lane] : a.fc[t0 + ln.lane];
-                float y[NQ];
-                load_row(y, a.harm + size_t(me) * NQ);
+    for (int k = 0; k < kRbRegs; ++k)
 #pragma unroll
-                for (int k = 0; k < NQ; ++k) Yc[ln.lane * LY + k] = y[k];
+        for (int u = 0; u < DMC; ++u)
+            wr[k][u] = k < kb ? a.wrb[size_t(k) * D + col.dl[u]] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < DMC; ++u) Bj[u] = a.node[size_t(j) * a.NP + D + col.dl[u]];
+    const int tb = a.r.tptr[j], te = a.r.tptr[j + 1];
+    for (int t0 = tb; t0 < te; t0 += kWave) {
+        const int cnt = min(kWave, te - t0);
+        int me = 0, mp = 0;
+        float mf = 0.0f;
+        wave_sync();
+        if (lane < cnt) {
+            me = a.r.tidx[t0 + lane];
+            mf = a.tfc[t0 + lane];
+            mp = a.pair[me];
+            stage_record<NQ, LY>(a, me, Yc, Rc, lane);
+        }
+        wave_sync();
+        float P[DMC];
+        {
+            const int pr = lane_get(mp, 0);
+#pragma unroll
+            for (int u = 0; u < DMC; ++u) P[u] = a.pair_proj[size_t(pr) * D + col.dl[u]];
+        }
+        for (int q = 0; q < cnt; ++q) {
+            float Pn[DMC];
+            const int pr = lane_get(mp, min(q + 1, cnt - 1));
+#pragma unroll
+            for (int u = 0; u < DMC; ++u) Pn[u] = a.pair_proj[size_t(pr) * D + col.dl[u]];
+            const int e = lane_get(me, q);
+            float acc[DMC];
+#pragma unroll
+            for (int u = 0; u < DMC; ++u) acc[u] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < NQ; ++k) {
+                const float y = Yc[q * LY + k];
+#pragma unroll
+                for (int u = 0; u < DMC; ++u) acc[u] += y * Q[k][u];
             }
-            wave_sync();
-            for (int q0 = 0; q0 < cnt; q0 += S) {
-                const int q = q0 + ln.slot;
-                const int e = bcast(me, min(q, kWave - 1));
-                const float fc = bcast(mf, min(q, kWave - 1));
-                if (q < cnt) {
-                    float *x = a.x + size_t(e) * a.ldx;
-                    const bool on = fc != 0.0f;
-                    if (!side)
-                        for (int k = ln.c; k < kb; k += Ln::W)
-                            x[k] = on ? a.rb[size_t(e) * a.ldrb + k] : 0.0f;
-                    if (ln.act) {
-                        float Y[NQ];
 #pragma unroll
-                        for (int k = 0; k < NQ; ++k) Y[k] = Yc[q * LY + k];
+            for (int k = 0; k < kRbRegs; ++k) {
+                const float r = Rc[q * LR + min(k, LR - 1)];
 #pragma unroll
-                        for (int L = 1; L <= LQ; ++L) {
-                            const int st = L * L - 1;
-                            float p = 0.0f;
-#pragma unroll
-                            for (int m = 0; m < 2 * L + 1; ++m) p += Hn[st + m] * Y[st + m];
-                            if (side) p = (L & 1) ? -p : p;
-                            x[kb + side * LC + (L - 1) * C + ln.c] = on ? p : 0.0f;
-                        }
-                    }
-                }
+                for (int u = 0; u < DMC; ++u) acc[u] += r * wr[k][u];
             }
+            for (int k = kRbRegs; k < kb; ++k) {
+                const float r = Rc[q * LR + k];
+#pragma unroll
+                for (int u = 0; u < DMC; ++u) acc[u] += r * a.wrb[size_t(k) * D + col.dl[u]];
+            }
+            const bool on = lane_get(mf, q) != 0.0f;
+#pragma unroll
+            for (int u = 0; u < DMC; ++u)
+                a.ue[size_t(e) * ldd + col.d[u]] = (Bj[u] + P[u]) + (on ? acc[u] : 0.0f);
+            copy(P, Pn);
+        }
+    }
+}
+
+// Centre side: u = A_i + (the neighbour pass's row) + (fc != 0: Qc_i Y_e),
+// stored as ue (pre-activation) and eh = act(u).  The records of a centre are
+// contiguous, so the rows of the next two are loaded while one is computed.
+template <int LQ, int DMC>
+__global__ void __launch_bounds__(kBlock) k_eq_edge_centre(EqArgs a) {
+    constexpr int NQ = LQ * (LQ + 2), LY = NQ + (NQ % 4 == 0 ? 4 : 1);
+    extern __shared__ float lds[];
+    const int i = wave_atom(a.r);
+    if (i < 0) return;
+    const int lane = threadIdx.x & (kWave - 1), C = a.C, D = a.D, CN = C * NQ, act = a.act;
+    const int ldd = a.ldd;
+    float *Yc = lds + (threadIdx.x >> 6) * a.wlds;
+    const EdgeCols<DMC> col(D);
+    float Q[NQ][DMC], A[DMC];
+    stage_state(Yc, a.dir_in + size_t(i) * CN, CN);
+    project_state<LQ, DMC>(Yc, a.wpc, C, D, col.dl, Q);
+#pragma unroll
+    for (int u = 0; u < DMC; ++u) A[u] = a.node[size_t(i) * a.NP + col.dl[u]];
+    const int b0 = a.r.ptr[i], b1 = a.r.ptr[i + 1];
+    if (b1 == b0) return;
+    auto fetch = [&](int e, float (&X)[DMC]) {
+        const size_t row = size_t(min(e, b1 - 1)) * ldd;
+#pragma unroll
+        for (int u = 0; u < DMC; ++u) X[u] = a.ue[row + col.d[u]];
+    };
+    float X0[DMC], X1[DMC];
+    fetch(b0, X0);
+    fetch(b0 + 1, X1);
+    for (int t0 = b0; t0 < b1; t0 += kWave) {
+        const int cnt = min(kWave, b1 - t0);
+        float mf = 0.0f;
+        wave_sync();
+        if (lane < cnt) {
+            mf = a.fc[t0 + lane];
+            stage_record<NQ, LY>(a, t0 + lane, Yc, nullptr, lane);
+        }
+        wave_sync();
+        for (int q = 0; q < cnt; ++q) {
+            const int e = t0 + q;
+            float X2[DMC];
+            fetch(e + 2, X2);
+            float acc[DMC];
+#pragma unroll
+            for (int u = 0; u < DMC; ++u) acc[u] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < NQ; ++k) {
+                const float y = Yc[q * LY + k];
+#pragma unroll
+                for (int u = 0; u < DMC; ++u) acc[u] += y * Q[k][u];
+            }
+            const bool on = lane_get(mf, q) != 0.0f;
+#pragma unroll
+            for (int u = 0; u < DMC; ++u) {
+                const float v = (A[u] + X0[u]) + (on ? acc[u] : 0.0f);
+                a.ue[size_t(e) * ldd + col.d[u]] = v;
+                a.eh[size_t(e) * ldd + col.d[u]] = act_f(act, v);
+            }
+            copy(X0, X1);
+            copy(X1, X2);
         }
     }
 }
@@ -868,7 +1048,7 @@ __global__ void __launch_bounds__(kBlock) k_eq_atom_sums(EqArgs a) {
 #pragma unroll
                     for (int u = 0; u < 4; ++u) {
                         const int d = lane + kWave * u;
-                        if (d < D) du[u] = a.due[size_t(e) * D + d];
+                        if (d < D) du[u] = a.due[size_t(e) * a.ldd + d];
                     }
                 }
             };
@@ -1037,6 +1217,65 @@ static int eq_slots(int C) { return C > 32 ? 1 : C > 16 ? 2 : 4; }
         RUNE_HIP_CHECK(hipGetLastError());                                                \
     } while (0)
 
+// Output columns per lane of the edge-MLP kernels: up to 4 (64 each), fewer
+// when the per-atom factor and the radial-basis weights would not fit in
+// about 140 registers.
+static int edge_dmc(int lq, int D) {
+    const int nq = lq * (lq + 2);
+    int c = std::min(ceil_div(D, kWave), 4);
+    while (c > 1 && (nq + kRbRegs) * c > 140) --c;
+    return c;
+}
+
+#define EQ_CASE_D(k, L, D, grid, block, lds, s, ...)                                      \
+    case D:                                                                               \
+        if ((lds) > 65536)                                                                \
+            RUNE_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&k<L, D>), \
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                               int(lds)));                                \
+        hipLaunchKernelGGL((k<L, D>), grid, block, lds, s, __VA_ARGS__);                  \
+        break;
+#define EQ_CASE_L4(k, L, dmc, ...)                                                        \
+    case L:                                                                               \
+        switch (dmc) {                                                                    \
+        EQ_CASE_D(k, L, 4, __VA_ARGS__)                                                   \
+        EQ_CASE_D(k, L, 3, __VA_ARGS__)                                                   \
+        EQ_CASE_D(k, L, 2, __VA_ARGS__)                                                   \
+        default: EQ_CASE_D(k, L, 1, __VA_ARGS__)                                          \
+        }                                                                                 \
+        break;
+#define EQ_CASE_L3(k, L, dmc, ...)                                                        \
+    case L:                                                                               \
+        switch (dmc) {                                                                    \
+        EQ_CASE_D(k, L, 3, __VA_ARGS__)                                                   \
+        EQ_CASE_D(k, L, 2, __VA_ARGS__)                                                   \
+        default: EQ_CASE_D(k, L, 1, __VA_ARGS__)                                          \
+        }                                                                                 \
+        break;
+#define EQ_CASE_L2(k, L, dmc, ...)                                                        \
+    case L:                                                                               \
+        switch (dmc) {                                                                    \
+        EQ_CASE_D(k, L, 2, __VA_ARGS__)                                                   \
+        default: EQ_CASE_D(k, L, 1, __VA_ARGS__)                                          \
+        }                                                                                 \
+        break;
+// Launches kernel template k<LQ, DMC> (the pairs edge_dmc can choose).
+#define EQ_LAUNCH_D(k, lq, dmc, ...)                                                       \
+    do {                                                                                  \
+        switch (lq) {                                                                     \
+        EQ_CASE_L4(k, 1, dmc, __VA_ARGS__)                                                \
+        EQ_CASE_L4(k, 2, dmc, __VA_ARGS__)                                                \
+        EQ_CASE_L4(k, 3, dmc, __VA_ARGS__)                                                \
+        EQ_CASE_L3(k, 4, dmc, __VA_ARGS__)                                                \
+        EQ_CASE_L2(k, 5, dmc, __VA_ARGS__)                                                \
+        EQ_CASE_L2(k, 6, dmc, __VA_ARGS__)                                                \
+        default:                                                                          \
+            switch (1) { EQ_CASE_D(k, 7, 1, __VA_ARGS__) }                                \
+            break;                                                                        \
+        }                                                                                 \
+        RUNE_HIP_CHECK(hipGetLastError());                                                \
+    } while (0)
+
 void validate_equivariant(ModelImpl &m) {
     const rune_model_config &c = m.cfg;
     const int lq = c.equivariant_l_max, C = c.equivariant_channels;
@@ -1144,8 +1383,22 @@ void pack_equivariant(ModelImpl &m, Packer &pk, std::map<std::string, size_t> &o
             for (int k = 0; k < kb; ++k) x[size_t(r) * KX + k] = wx[size_t(r) * kb + k];
             for (int k = 0; k < 2 * W; ++k) x[size_t(r) * KX + kb + k] = wp[size_t(r) * 2 * W + k];
         }
-        off[p + "edge_x"] = pk.put(pad_rows(x, D, KX));
         off[p + "edge_xT"] = pk.put(transpose(x, D, KX));
+        // factored edge MLP: [kb, D] radial-basis rows and [lq C, D] probe rows,
+        // the neighbour probes signed (-1)^L
+        off[p + "edge_rbT"] = pk.put(transpose(wx, D, kb));
+        std::vector<float> pc(size_t(W) * D), pn(size_t(W) * D);
+        for (int L = 1; L <= lq; ++L)
+            for (int cc = 0; cc < C; ++cc) {
+                const int row = (L - 1) * C + cc;
+                const float sg = (L & 1) ? -1.0f : 1.0f;
+                for (int r = 0; r < D; ++r) {
+                    pc[size_t(row) * D + r] = wp[size_t(r) * 2 * W + row];
+                    pn[size_t(row) * D + r] = sg * wp[size_t(r) * 2 * W + W + row];
+                }
+            }
+        off[p + "probe_c"] = pk.put(pc);
+        off[p + "probe_n"] = pk.put(pn);
         off[p + "pair_proj"] = pk.put(pair_projection(m.tensor(p + "pair_embedding.weight"), we,
                                                       m.tensor(p + "edge_mlp.0.bias"), T * T, P,
                                                       D, K, kb));
@@ -1192,8 +1445,10 @@ void bind_equivariant(ModelImpl &m, const PackedLookup &P) {
         w.ld_edge_x = (w.KX + 3) & ~3;
         w.node_f = P(p + "node_f");
         w.node_fT = P(p + "node_fT");
-        w.edge_x = P(p + "edge_x");
         w.edge_xT = P(p + "edge_xT");
+        w.edge_rbT = P(p + "edge_rbT");
+        w.probe_c = P(p + "probe_c");
+        w.probe_n = P(p + "probe_n");
         w.pair_proj = P(p + "pair_proj");
         w.gate = P(p + "gate");
         w.gate_T = P(p + "gate_T");
@@ -1233,16 +1488,17 @@ MessagePlan plan_equivariant(ModelImpl &m, Arena &ar, int N, int64_t E) {
     p.i_dd = p.add(ar, 4 * e);
     p.i_rbd = p.add(ar, 4 * e * p.ldrb);
     int dir0 = p.add(ar, 4 * n * CN);
-    int x = p.add(ar, 4 * e * ldx);        // shared by the blocks (forward only)
-    int eh = p.add(ar, 4 * e * D);         // shared
+    const int dmc = edge_dmc(lq, D);
+    p.ld_edge = ceil_div(D, kWave * dmc) * kWave * dmc;
+    const size_t ldd = size_t(p.ld_edge);
+    int eh = p.add(ar, 4 * e * ldd);       // shared by the blocks (forward only)
     for (int b = 0; b < c.message_layers; ++b) {
         BlockBuffers bb;
         bb.h_out = p.add(ar, 4 * n * H);
         bb.rin = p.add(ar, 4 * n);
         bb.vs = p.add(ar, 4 * n * NP);
-        bb.ue = p.add(ar, 4 * e * D);
+        bb.ue = p.add(ar, 4 * e * ldd);
         bb.eh = eh;
-        bb.xe = x;
         bb.gv = p.add(ar, 4 * e * NG);
         bb.msg = p.add(ar, 4 * n * H);
         bb.rm = p.add(ar, 4 * n);
@@ -1259,7 +1515,7 @@ MessagePlan plan_equivariant(ModelImpl &m, Arena &ar, int N, int64_t E) {
     p.t_dmsg = p.add(ar, 4 * n * H);
     p.t_dvsum = p.add(ar, 4 * n * CN);     // dE/d(dir_out) total
     p.t_dgv = p.add(ar, 4 * e * NG);
-    p.t_due = p.add(ar, 4 * e * D);
+    p.t_due = p.add(ar, 4 * e * ldd);
     p.t_dx = p.add(ar, 4 * e * ldx);
     p.t_dvs = p.add(ar, 4 * n * NP);
     p.t_dmix = p.add(ar, 4 * n * CN);
@@ -1308,7 +1564,15 @@ static EqArgs eq_args(ModelImpl &m, MessagePlan &p, const Records &r, int b) {
     a.dir_out = p.at(bb.dir_out);
     a.mixw = m.msg[b].mix;
     a.mixst = p.at(bb.mixstate);
-    a.x = p.at(bb.xe);
+    a.act = c.activation;
+    a.pair = reinterpret_cast<const int32_t *>(p.at(p.i_pair));
+    a.pair_proj = m.msg[b].pair_proj;
+    a.wpc = m.msg[b].probe_c;
+    a.wpn = m.msg[b].probe_n;
+    a.wrb = m.msg[b].edge_rbT;
+    a.ue = p.at(bb.ue);
+    a.ldd = p.ld_edge;
+    a.eh = p.at(bb.eh);
     a.ag = p.at(bb.gv);
     a.msg = p.at(bb.msg);
     a.rm = p.at(bb.rm);
@@ -1371,28 +1635,17 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
         EQ_LAUNCH(k_eq_mix, lq, dim3(mix_grid), dim3(256), mix_lds, s, N, w.mix,
                   p.at(bb.dir_in), C, 0, p.at(bb.mixstate));
         if (E > 0) {
+            const int dmc = edge_dmc(lq, D), cn4 = (C * nq + 3) & ~3;
+            const int ly = nq + (nq % 4 == 0 ? 4 : 1);
+            const dim3 egrid(atom_grid, ceil_div(D, kWave * dmc));
             {
                 Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
-                EQ_LAUNCH_S(k_eq_features, lq, a.S, dim3(atom_grid), dim3(kBlock),
-                            sizeof(float) * kBlock * (nq + (nq % 4 == 0 ? 4 : 1)), s, a);
-            }
-            Epilogue e1;
-            e1.gtab[0] = p.at(bb.vs);
-            e1.gidx[0] = r.ctr;
-            e1.gld[0] = w.NP;
-            e1.gtab[1] = p.at(bb.vs) + D;
-            e1.gidx[1] = r.nbr;
-            e1.gld[1] = w.NP;
-            e1.gtab[2] = w.pair_proj;
-            e1.gidx[2] = reinterpret_cast<const int32_t *>(p.at(p.i_pair));
-            e1.gld[2] = D;
-            e1.pre = p.at(bb.ue);
-            e1.ldp = D;
-            e1.act = act;
-            {
-                Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
-                gemm(int(E), D, w.KX, p.at(bb.xe), a.ldx, w.edge_x, w.ld_edge_x, p.at(bb.eh),
-                     D, e1, s);
+                a.wlds = std::max(cn4, kWave * (ly + p.ldrb));
+                const size_t lds_n = sizeof(float) * kWaves * a.wlds;
+                EQ_LAUNCH_D(k_eq_edge_nbr, lq, dmc, egrid, dim3(kBlock), lds_n, s, a);
+                a.wlds = std::max(cn4, kWave * ly);
+                const size_t lds_c = sizeof(float) * kWaves * a.wlds;
+                EQ_LAUNCH_D(k_eq_edge_centre, lq, dmc, egrid, dim3(kBlock), lds_c, s, a);
             }
             Epilogue e2;
             e2.bias = w.gate_b;
@@ -1401,7 +1654,8 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
             e2.act2 = RUNE_ACT_TANH;
             {
                 Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
-                gemm(int(E), w.NG, D, p.at(bb.eh), D, w.gate, D, p.at(bb.gv), w.NG, e2, s);
+                gemm(int(E), w.NG, D, p.at(bb.eh), p.ld_edge, w.gate, D, p.at(bb.gv), w.NG, e2,
+                     s);
             }
         }
         {
@@ -1473,16 +1727,18 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         if (E > 0) {
             Epilogue e2;
             e2.dact_from = p.at(bb.ue);
-            e2.ldu = D;
+            e2.ldu = p.ld_edge;
             e2.dact = act;
             {
                 Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
-                gemm(int(E), D, w.NG, p.at(p.t_dgv), w.NG, w.gate_T, w.NG, p.at(p.t_due), D, e2, s);
+                gemm(int(E), D, w.NG, p.at(p.t_dgv), w.NG, w.gate_T, w.NG, p.at(p.t_due),
+                     p.ld_edge, e2, s);
             }
             Epilogue e3;
             {
                 Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
-                gemm(int(E), w.KX, D, p.at(p.t_due), D, w.edge_xT, D, p.at(p.t_dx), a.ldx, e3, s);
+                gemm(int(E), w.KX, D, p.at(p.t_due), p.ld_edge, w.edge_xT, D, p.at(p.t_dx), a.ldx,
+                     e3, s);
             }
         }
         {

@@ -39,6 +39,8 @@ struct MessageWeights {
     // edge MLP on per-edge features: MP [radial basis], EQ [radial basis | probes]
     const float *edge_xT, *edge_x;    // [KX, D], [D, ld_edge_x]
     int KX, ld_edge_x;
+    // EQ factored edge MLP: radial-basis rows [kb, D], probe rows [lq*C, D]
+    const float *edge_rbT = nullptr, *probe_c = nullptr, *probe_n = nullptr;
     const float *pair_proj;           // [T*T, D] = pair_embedding W_pair^T + b
     // gates from the edge hidden state: MP [groups | vector], EQ [groups | directions]
     const float *gate_T, *gate, *gate_b;   // [D, NG], [NG, D], [NG]
@@ -63,7 +65,6 @@ struct BlockBuffers {
     int h_out = -1, rin = -1, vs = -1, ue = -1, eh = -1, gv = -1, msg = -1, rm = -1;
     int vsum = -1, mixed = -1, uin = -1, u1 = -1, z1 = -1;
     int dir_in = -1, dir_out = -1, mixstate = -1;   // EQ angular states
-    int xe = -1;                                     // EQ per-edge features
 };
 
 struct MessagePlan {
@@ -76,6 +77,7 @@ struct MessagePlan {
     int64_t E = 0;
     size_t o_gd = 0, o_dmom = 0;
     int ldrb = 0, ldrb_x = 0;
+    int ld_edge = 0;              // EQ: row stride of the per-record [E, D] arrays
     int i_rb = -1, i_fc = -1, i_tfc = -1, i_pair = -1, i_dv = -1, i_harm = -1, i_dharm = -1, i_dharm_n = -1;
     int i_dfc = -1, i_dd = -1, i_rbd = -1;
     std::vector<BlockBuffers> blocks;
