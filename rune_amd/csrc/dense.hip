@@ -181,11 +181,25 @@ __device__ inline void tile_epilogue(floatx4 (&acc)[WM][WN], float *smem, int M,
 // each lane fetches its four steps with one 16-byte LDS read.  Row stride
 // kLdk = 36 floats keeps those reads free of bank conflicts.
 // Block b covers row tile b / nbn and column tile b % nbn.
+// Batched launches (gridDim.y > 1) offset A, C by z times their batch strides
+// and Bt by sb times z, or times L(z) - 1 (L the harmonic order of component z)
+// when the batches share one weight block per order.
 template <int WM, int WN, int WMW, bool kVec>
 __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *__restrict__ A,
                                               int lda, const float *__restrict__ Bt, int ldb,
                                               float *__restrict__ C, int ldc, Epilogue ep,
-                                              int nbn) {
+                                              int nbn, GemmBatch bt) {
+    if (gridDim.y > 1) {
+        const int z = int(blockIdx.y);
+        int w = z;
+        if (bt.b_by_order) {
+            w = 0;
+            while ((w + 2) * (w + 2) - 1 <= z) ++w;
+        }
+        A += size_t(z) * bt.sa;
+        C += size_t(z) * bt.sc;
+        Bt += size_t(w) * bt.sb;
+    }
     constexpr int WNW = 4 / WMW;
     constexpr int kBM = 16 * WM * WMW, BN = 16 * WN * WNW, kLdo = BN + 4;
     static_assert(32 * kLdo <= (kBM + BN) * kLdk, "epilogue staging exceeds the tile LDS");
@@ -343,29 +357,42 @@ static bool narrow_tile(int N) { return ceil_div(N, 32) * 32 < ceil_div(N, 64) *
 
 template <int WM, int WN, int WMW = 2>
 static void launch_gemm(bool vec, int M, int N, int K, const float *A, int lda, const float *Bt,
-                        int ldb, float *C, int ldc, const Epilogue &ep, hipStream_t s) {
+                        int ldb, float *C, int ldc, const Epilogue &ep, const GemmBatch &bt,
+                        hipStream_t s) {
     constexpr int kBM = 16 * WM * WMW, BN = 16 * WN * (4 / WMW);
     int nbn = ceil_div(N, BN);
     int64_t blocks = int64_t(ceil_div(M, kBM)) * nbn;
-    if (blocks > 0x7fffffff) throw Error(RUNE_ERR_ARGUMENT, "gemm: problem too large");
+    if (blocks > 0x7fffffff || bt.count > 65535)
+        throw Error(RUNE_ERR_ARGUMENT, "gemm: problem too large");
+    const dim3 grid(unsigned(blocks), unsigned(bt.count));
     if (vec)
-        hipLaunchKernelGGL((k_gemm<WM, WN, WMW, true>), dim3(unsigned(blocks)), dim3(256), 0, s, M,
-                           N, K, A, lda, Bt, ldb, C, ldc, ep, nbn);
+        hipLaunchKernelGGL((k_gemm<WM, WN, WMW, true>), grid, dim3(256), 0, s, M, N, K, A, lda, Bt,
+                           ldb, C, ldc, ep, nbn, bt);
     else
-        hipLaunchKernelGGL((k_gemm<WM, WN, WMW, false>), dim3(unsigned(blocks)), dim3(256), 0, s,
-                           M, N, K, A, lda, Bt, ldb, C, ldc, ep, nbn);
+        hipLaunchKernelGGL((k_gemm<WM, WN, WMW, false>), grid, dim3(256), 0, s, M, N, K, A, lda,
+                           Bt, ldb, C, ldc, ep, nbn, bt);
+}
+
+static void gemm_any(int M, int N, int K, const float *A, int lda, const float *Bt, int ldb,
+                     float *C, int ldc, const Epilogue &ep, const GemmBatch &bt, hipStream_t s) {
+    if (M == 0 || N == 0 || bt.count == 0) return;
+    bool vec = lda % 4 == 0 && ldb % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
+               (reinterpret_cast<uintptr_t>(Bt) & 15) == 0 && bt.sa % 4 == 0 && bt.sb % 4 == 0;
+    if (narrow_tile(N))
+        launch_gemm<1, 2, 4>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, bt, s);
+    else
+        launch_gemm<2, 2, 2>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, bt, s);
+    RUNE_HIP_CHECK(hipGetLastError());
 }
 
 void gemm(int M, int N, int K, const float *A, int lda, const float *Bt, int ldb, float *C,
           int ldc, const Epilogue &ep, hipStream_t s) {
-    if (M == 0 || N == 0) return;
-    bool vec = lda % 4 == 0 && ldb % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
-               (reinterpret_cast<uintptr_t>(Bt) & 15) == 0;
-    if (narrow_tile(N))
-        launch_gemm<1, 2, 4>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s);
-    else
-        launch_gemm<2, 2, 2>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, s);
-    RUNE_HIP_CHECK(hipGetLastError());
+    gemm_any(M, N, K, A, lda, Bt, ldb, C, ldc, ep, GemmBatch{}, s);
+}
+
+void gemm_batched(const GemmBatch &bt, int M, int N, int K, const float *A, int lda,
+                  const float *Bt, int ldb, float *C, int ldc, hipStream_t s) {
+    gemm_any(M, N, K, A, lda, Bt, ldb, C, ldc, Epilogue{}, bt, s);
 }
 
 void row_inv_rms(int M, int N, const float *x, int ldx, float eps, float *inv_rms, hipStream_t s) {

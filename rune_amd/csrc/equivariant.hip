@@ -73,7 +73,7 @@ __device__ __host__ inline int order_of(int k) {
 
 struct EqArgs {
     Records r;
-    int H, D, G, C, lq, nq, NG, NP, KX, kb, ldx, na, nlm;
+    int H, D, G, C, lq, nq, NG, NP, kb, na, nlm;
     int S;                    // records in flight per wave (lane slots of 64 / S lanes)
     int gmode;                // group-sum method of k_eq_pair_grp
     float eps, cutoff;
@@ -105,14 +105,13 @@ struct EqArgs {
     float *dgg;               // [E, NG]
     float4 *dv;               // [E]
     float *dfc;               // [E] dE/dfc of the message terms, all blocks
-    float *dd;                // [E] dE/dd of the radial-basis inputs, all blocks
-    const float *rbd;         // [E, ldrb] distance derivative of the radial basis
     float *dy;                // [E, nq] dE/dY, centre-side shares
     float *dyn;               // [E, nq] dE/dY, neighbour-side shares
     float *dnode;             // [N, NP]
     float *dmix;              // [N, C*nq]
     const float *due;         // [E, D]
-    const float *dx;          // [E, ldx]
+    float *qbuf;              // [N, nq, 2 ldd] per-atom factors Qc | Qn of the block
+    float *dqbuf;             // [N, nq, 2 ldd] their adjoints
     float *ddir_in;           // [N, C*nq]
 };
 
@@ -218,10 +217,12 @@ __device__ inline void fold_slots(float (&v)[N]) {
 }
 
 // out[n, c, k] = sum_c' W_L[c][c'] in[n, c', k] (trans = 0) or
-// sum_c' W_L[c'][c] in[n, c', k] (trans = 1), L the order of component k.
+// sum_c' W_L[c'][c] in[n, c', k] (trans = 1), L the order of component k,
+// plus add[n, c, k] and add_t[n, k, c] when given.
 template <int LQ>
 __global__ void __launch_bounds__(256) k_eq_mix(int N, const float *mixw, const float *in, int C,
-                                                int trans, float *out) {
+                                                int trans, const float *add, const float *add_t,
+                                                float *out) {
     constexpr int NQ = LQ * (LQ + 2);
     extern __shared__ float lds[];
     const int CN = C * NQ, CC = C * C, LW = C + 1;
@@ -240,6 +241,8 @@ __global__ void __launch_bounds__(256) k_eq_mix(int N, const float *mixw, const 
             const float *w = Wl + size_t((order_of(k) - 1) * C + c) * LW;
             float acc = 0.0f;
             for (int cc = 0; cc < C; ++cc) acc += w[cc] * row[cc * NQ + k];
+            if (add) acc += add[size_t(n) * CN + o];
+            if (add_t) acc += add_t[size_t(n) * CN + k * C + c];
             out[size_t(n) * CN + o] = acc;
         }
     }
@@ -324,6 +327,16 @@ __device__ inline void project_state(const float *Hs, const float *__restrict__ 
     }
 }
 
+// Keeps the factor for the reverse pass: out[k * ld + d].
+template <int LQ, int DMC>
+__device__ inline void store_factor(const float (&Q)[LQ * (LQ + 2)][DMC], float *out, int ld,
+                                    const int (&d)[DMC]) {
+#pragma unroll
+    for (int k = 0; k < LQ * (LQ + 2); ++k)
+#pragma unroll
+        for (int u = 0; u < DMC; ++u) out[size_t(k) * ld + d[u]] = Q[k][u];
+}
+
 __device__ inline void stage_state(float *Hs, const float *__restrict__ row, int CN) {
     const int lane = threadIdx.x & (kWave - 1);
     for (int o = lane; o < CN; o += kWave) Hs[o] = row[o];
@@ -365,6 +378,7 @@ __global__ void __launch_bounds__(kBlock) k_eq_edge_nbr(EqArgs a) {
     float Q[NQ][DMC];
     stage_state(Yc, a.dir_in + size_t(j) * CN, CN);
     project_state<LQ, DMC>(Yc, a.wpn, C, D, col.dl, Q);
+    store_factor<LQ, DMC>(Q, a.qbuf + size_t(j) * NQ * 2 * ldd + ldd, 2 * ldd, col.d);
     float wr[kRbRegs][DMC], Bj[DMC];
 #pragma unroll
     for (int k = 0; k < kRbRegs; ++k)
@@ -443,6 +457,7 @@ __global__ void __launch_bounds__(kBlock) k_eq_edge_centre(EqArgs a) {
     float Q[NQ][DMC], A[DMC];
     stage_state(Yc, a.dir_in + size_t(i) * CN, CN);
     project_state<LQ, DMC>(Yc, a.wpc, C, D, col.dl, Q);
+    store_factor<LQ, DMC>(Q, a.qbuf + size_t(i) * NQ * 2 * ldd, 2 * ldd, col.d);
 #pragma unroll
     for (int u = 0; u < DMC; ++u) A[u] = a.node[size_t(i) * a.NP + col.dl[u]];
     const int b0 = a.r.ptr[i], b1 = a.r.ptr[i + 1];
@@ -631,19 +646,22 @@ __device__ inline float cutoff_slope(float d, float rc) {
 // Reverse pass of the angular messages, walked from the neighbour side: the
 // wave of atom j holds its mixed state M_j, gathers the centre's
 // dE/d(dir_out) once per record and produces the direction-gate adjoints
-// dE/dgate[e, G:], their share of dE/dfc (into dv[e].w) and
-// dE/dM_j = sum_e fc tT[e] dHt_i.  Harmonic rows of a 64-record chunk are
-// staged in LDS with one parallel load.
+// dE/dgate[e, G:], their share of dE/dfc, dE/dM_j = sum_e fc tT[e] dHt_i, and
+// the injected term's share of dE/dY_e = fc sum_c tI[e, (L, c)] dHt_i[c, :]
+// (added to dy; the channel sum goes through a per-wave LDS tile).  Harmonic
+// rows of a 64-record chunk are staged in LDS with one parallel load.
 template <int LQ, int S>
 __global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
-    constexpr int NQ = LQ * (LQ + 2), LY = NQ + (NQ % 4 == 0 ? 4 : 1);
+    constexpr int NQ = LQ * (LQ + 2), LY = NQ + (NQ % 4 == 0 ? 4 : 1), LD = NQ + 1;
     using Ln = Lanes<S>;
     constexpr int W = Ln::W;
+    constexpr int KQ = (NQ + W - 1) / W;   // dE/dY components per lane
     extern __shared__ float lds[];
     const int j = wave_atom(a.r);
     if (j < 0) return;
     const Ln ln(a.C);
-    float *Yc = lds + (threadIdx.x >> 6) * kWave * LY;
+    float *Yc = lds + (threadIdx.x >> 6) * kWave * (LY + LD);
+    float *T = Yc + kWave * LY;
     const int G = a.G, C = a.C, CN = C * NQ, LC = LQ * C, NG = a.NG;
     float MX[NQ], acc[NQ];
     zero(MX);
@@ -669,13 +687,20 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
         }
         wave_sync();
         auto fetch = [&](int q, int &e, float (&dh)[NQ], float (&tt)[LQ], float (&ti)[LQ],
-                         float &f) {
+                         float (&yo)[KQ], float &f) {
             e = bcast(me, min(q, kWave - 1));
             const int i = bcast(mi, min(q, kWave - 1));
             f = bcast(mf, min(q, kWave - 1));
             if (q >= cnt) {
                 e = -1;
                 f = 0.0f;
+            }
+            if (f != 0.0f) {
+#pragma unroll
+                for (int u = 0; u < KQ; ++u) {
+                    const int k = ln.c + W * u;
+                    yo[u] = k < NQ ? a.dy[size_t(e) * NQ + k] : 0.0f;
+                }
             }
             if (f != 0.0f && ln.act) {
                 load_row(dh, a.dht + size_t(i) * CN + ln.c * NQ);
@@ -688,13 +713,13 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
             }
         };
         int e;
-        float DH[NQ], tT[LQ], tI[LQ], fc;
-        fetch(ln.slot, e, DH, tT, tI, fc);
+        float DH[NQ], tT[LQ], tI[LQ], yo[KQ], fc;
+        fetch(ln.slot, e, DH, tT, tI, yo, fc);
         for (int q0 = 0; q0 < cnt; q0 += S) {
             const int q = q0 + ln.slot;
             int en;
-            float DHn[NQ], tTn[LQ], tIn[LQ], fcn;
-            fetch(q + S, en, DHn, tTn, tIn, fcn);
+            float DHn[NQ], tTn[LQ], tIn[LQ], yon[KQ], fcn;
+            fetch(q + S, en, DHn, tTn, tIn, yon, fcn);
             const bool on = fc != 0.0f;
             float contrib = 0.0f;
             if (e >= 0 && ln.act) {
@@ -717,7 +742,10 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
                         dg[LC + (L - 1) * C] = (1.0f - t2 * t2) * fc * sI;
                         contrib += t1 * sT + t2 * sI;
 #pragma unroll
-                        for (int m = 0; m < 2 * L + 1; ++m) acc[st + m] += fc * t1 * DH[st + m];
+                        for (int m = 0; m < 2 * L + 1; ++m) {
+                            acc[st + m] += fc * t1 * DH[st + m];
+                            T[ln.lane * LD + st + m] = fc * t2 * DH[st + m];
+                        }
                     }
                 } else {
 #pragma unroll
@@ -730,10 +758,24 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
             contrib = group_sum(contrib, W);
             const float dold = bcast(md, min(q, kWave - 1));
             if (on && ln.c == 0) a.dfc[e] = dold + contrib;
+            wave_sync();
+            if (on) {
+#pragma unroll
+                for (int u = 0; u < KQ; ++u) {
+                    const int k = ln.c + W * u;
+                    if (k < NQ) {
+                        float sum = 0.0f;
+                        for (int c = 0; c < a.C; ++c) sum += T[(ln.slot * W + c) * LD + k];
+                        a.dy[size_t(e) * NQ + k] = yo[u] + sum;
+                    }
+                }
+            }
+            wave_sync();
             e = en;
             copy(DH, DHn);
             copy(tT, tTn);
             copy(tI, tIn);
+            copy(yo, yon);
             fc = fcn;
         }
     }
@@ -873,205 +915,151 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_grp(EqArgs a) {
     }
 }
 
-// Angular adjoints of the edge features, from both sides of each record:
-// dE/d(dir_in)_n = dHt_n + probe adjoints (+ the channel-mix adjoint that
-// k_eq_mix already wrote to ddir_in), and dE/dY of each record: the centre
-// side adds fc tI dHt_i + dprobe_c H_i, the neighbour side (-1)^L dprobe_n
-// H_j, each into its own buffer.  Harmonic rows of a chunk are staged in LDS;
-// the channel sums of the dE/dY shares go through a per-wave LDS tile.
-template <int LQ, int S>
-__global__ void __launch_bounds__(kBlock) k_eq_atom_dir(EqArgs a) {
-    constexpr int NQ = LQ * (LQ + 2), LD = NQ + 1, LY = NQ + (NQ % 4 == 0 ? 4 : 1);
-    using Ln = Lanes<S>;
-    constexpr int W = Ln::W;
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ inline floatx4 mfma4(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Records per matrix-core batch of the edge-MLP reverse kernels.
+constexpr int kAdjBatch = 16;
+
+// Reverse of the factored edge MLP for the records of atom n on one side
+// (SIDE 0: the records with centre n, SIDE 1: the records with neighbour n),
+// on the matrix cores (v_mfma_f32_16x16x4f32), 16 records at a time.  With
+// due = dE/du [rec, d] and Q_n the side's per-atom factor [NQ, d]:
+//   dY[rec, k]  += sum_d due[rec, d] Q_n[k, d]
+//   dQ_n[k, d]   = sum_rec Y[rec, k] due[rec, d]
+// and, from a constant component Y[rec, NQ] = 1, the context adjoint
+// dE/dA_n (SIDE 0) or dE/dB_n (SIDE 1) = sum_rec due[rec, :].  A batch's
+// due, harmonic and old dE/dY rows are staged in the wave's LDS with one
+// lane-parallel load.  The output columns go in blocks of 16 NTC (one block
+// for the usual widths); each block walks the records again.
+//
+// MFMA operand layout: lane l supplies A[l%16][l/16] and B[l/16][l%16]; the
+// accumulator register v of lane l holds C[4(l/16) + v][l%16].  For dY the
+// k-steps take d = 16 t + 4 (l/16) + s (s = 0..3), so each lane reads its four
+// A values with one 16-byte LDS read.
+template <int LQ, int NTC, int SIDE>
+__global__ void __launch_bounds__(kBlock) k_eq_edge_adj(EqArgs a) {
+    constexpr int NQ = LQ * (LQ + 2), MT = (NQ + 16) / 16, KP = 16 * MT;
+    constexpr int CW = 16 * NTC, LDU = CW + 4, LDY = KP + 4, LDO = NQ + 1;
     extern __shared__ float lds[];
     const int n = wave_atom(a.r);
     if (n < 0) return;
-    const Ln ln(a.C);
-    float *T = lds + (threadIdx.x >> 6) * kWave * (LD + LY);
-    float *Yc = T + kWave * LD;
-    const int C = a.C, CN = C * NQ, LC = LQ * C, kb = a.kb, G = a.G, NG = a.NG;
-    float Hn[NQ], DHn[NQ], g[NQ];
-    zero(Hn);
-    zero(DHn);
-    zero(g);
-    if (ln.act) {
-        load_row(Hn, a.dir_in + size_t(n) * CN + ln.c * NQ);
-        load_row(DHn, a.dht + size_t(n) * CN + ln.c * NQ);
-    }
+    const int lane = threadIdx.x & (kWave - 1), g = lane >> 4, r = lane & 15;
+    float *dueL = lds + (threadIdx.x >> 6) * a.wlds;   // [16][LDU]
+    float *YL = dueL + kAdjBatch * LDU;                 // [16][LDY]
+    float *oldL = YL + kAdjBatch * LDY;                 // [16][LDO]
+    int *eL = reinterpret_cast<int *>(oldL + kAdjBatch * LDO);
+    const int ldd = a.ldd, ldq = 2 * ldd, D = a.D;
+    const int b0 = SIDE ? a.r.tptr[n] : a.r.view[4 * n];
+    const int b1 = SIDE ? a.r.tptr[n + 1] : a.r.view[4 * n + 1];
+    float *dyo = SIDE ? a.dyn : a.dy;
+    const float *Qn = a.qbuf + size_t(n) * NQ * ldq + SIDE * ldd;
+    float *dQo = a.dqbuf + size_t(n) * NQ * ldq + SIDE * ldd;
+    for (int c0 = 0; c0 < ldd; c0 += CW) {
+        const int ntv = min(NTC, (ldd - c0) / 16);   // n-tiles of this column block
+        floatx4 Bq[NTC][MT];
 #pragma unroll
-    for (int side = 0; side < 2; ++side) {
-        const int b0 = side ? a.r.tptr[n] : a.r.view[4 * n];
-        const int b1 = side ? a.r.tptr[n + 1] : a.r.view[4 * n + 1];
-        float *dyo = side ? a.dyn : a.dy;
-        for (int t0 = b0; t0 < b1; t0 += kWave) {
-            const int cnt = min(kWave, b1 - t0);
-            int me = -1;
-            float mf = 0.0f, mdd = 0.0f;
+        for (int t = 0; t < NTC; ++t)
+#pragma unroll
+            for (int nt = 0; nt < MT; ++nt) {
+                const int k = 16 * nt + r;
+                const float4 v = *reinterpret_cast<const float4 *>(
+                    Qn + size_t(min(k, NQ - 1)) * ldq + c0 + 16 * min(t, ntv - 1) + 4 * g);
+                const bool ok = k < NQ && t < ntv;
+                Bq[t][nt] = floatx4{ok ? v.x : 0.0f, ok ? v.y : 0.0f, ok ? v.z : 0.0f,
+                                    ok ? v.w : 0.0f};
+            }
+        floatx4 acc[MT][NTC];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NTC; ++nt) acc[mt][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int t0 = b0; t0 < b1; t0 += kAdjBatch) {
+            const int cnt = min(kAdjBatch, b1 - t0);
             wave_sync();
-            if (ln.lane < cnt) {
-                me = side ? a.r.tidx[t0 + ln.lane] : t0 + ln.lane;
-                mf = side ? a.tfc[t0 + ln.lane] : a.fc[t0 + ln.lane];
-                if (!side) mdd = a.dd[me];
-                if (mf != 0.0f) {
-                    float y[NQ];
-                    load_row(y, a.harm + size_t(me) * NQ);
+            {
+                // row rec = lane / 4 of the batch, quarter qq = lane % 4 of each row
+                const int rec = lane >> 2, qq = lane & 3;
+                const int rv = min(rec, cnt - 1);
+                const int e = SIDE ? a.r.tidx[t0 + rv] : t0 + rv;
+                const bool live = rec < cnt;
+                const float4 *src = reinterpret_cast<const float4 *>(a.due + size_t(e) * ldd + c0);
 #pragma unroll
-                    for (int k = 0; k < NQ; ++k) Yc[ln.lane * LY + k] = y[k];
+                for (int i = 0; i < NTC; ++i) {
+                    const int c4 = qq * NTC + i;
+                    *reinterpret_cast<float4 *>(dueL + rec * LDU + 4 * c4) =
+                        src[min(c4, 4 * ntv - 1)];
                 }
+#pragma unroll
+                for (int i = 0; i < 4 * MT; ++i) {
+                    const int k = 4 * qq * MT + i;
+                    float y = a.harm[size_t(e) * NQ + min(k, NQ - 1)];
+                    y = k < NQ ? y : (k == NQ ? 1.0f : 0.0f);
+                    YL[rec * LDY + k] = live ? y : 0.0f;
+                }
+                for (int k = qq; k < NQ; k += 4) oldL[rec * LDO + k] = dyo[size_t(e) * NQ + k];
+                if (qq == 0) eL[rec] = e;
             }
             wave_sync();
-            constexpr int KQ = (NQ + W - 1) / W;   // dE/dY components per lane
-            // centre side: radial-basis adjoint terms dE/drb_k drb_k/dd (k = c, c + W)
-            auto fetch = [&](int q, int &e, float (&dxv)[LQ], float (&ti)[LQ], float (&yo)[KQ],
-                             float &rbt, float &f) {
-                e = bcast(me, min(q, kWave - 1));
-                f = bcast(mf, min(q, kWave - 1));
-                rbt = 0.0f;
-                if (q >= cnt) {
-                    e = -1;
-                    f = 0.0f;
-                }
-                if (!side && f != 0.0f) {
-                    for (int k = ln.c; k < kb; k += W)
-                        rbt += a.dx[size_t(e) * a.ldx + k] * a.rbd[size_t(e) * a.ldrb + k];
-                }
-                if (f != 0.0f) {
+            floatx4 p[MT];
 #pragma unroll
-                    for (int u = 0; u < KQ; ++u) {
-                        const int k = ln.c + W * u;
-                        yo[u] = k < NQ ? dyo[size_t(e) * NQ + k] : 0.0f;
-                    }
+            for (int nt = 0; nt < MT; ++nt) p[nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < NTC; ++t) {
+                const float4 av = *reinterpret_cast<const float4 *>(dueL + r * LDU + 16 * t + 4 * g);
+#pragma unroll
+                for (int nt = 0; nt < MT; ++nt) {
+                    p[nt] = mfma4(av.x, Bq[t][nt][0], p[nt]);
+                    p[nt] = mfma4(av.y, Bq[t][nt][1], p[nt]);
+                    p[nt] = mfma4(av.z, Bq[t][nt][2], p[nt]);
+                    p[nt] = mfma4(av.w, Bq[t][nt][3], p[nt]);
                 }
-                if (f != 0.0f && ln.act) {
-                    const float *d = a.dx + size_t(e) * a.ldx + kb + side * LC + ln.c;
-                    const float *gr = a.ag + size_t(e) * NG + G + LC + ln.c;
-#pragma unroll
-                    for (int L = 0; L < LQ; ++L) {
-                        dxv[L] = d[L * C];
-                        ti[L] = side ? 0.0f : gr[L * C];
-                    }
-                }
-            };
-            int e;
-            float dxv[LQ], tI[LQ], yo[KQ], rbt, fc;
-            fetch(ln.slot, e, dxv, tI, yo, rbt, fc);
-            for (int q0 = 0; q0 < cnt; q0 += S) {
-                const int q = q0 + ln.slot;
-                int en;
-                float dxn[LQ], tIn[LQ], yon[KQ], rbtn, fcn;
-                fetch(q + S, en, dxn, tIn, yon, rbtn, fcn);
-                if (!side) {
-                    const float sum = group_sum(rbt, W);
-                    const float dold = bcast(mdd, min(q, kWave - 1));
-                    if (fc != 0.0f && ln.c == 0) a.dd[e] = dold + sum;
-                }
-                const bool on = fc != 0.0f && ln.act;
-                float Y[NQ];
-#pragma unroll
-                for (int k = 0; k < NQ; ++k) Y[k] = on ? Yc[q * LY + k] : 0.0f;
-#pragma unroll
-                for (int L = 1; L <= LQ; ++L)
-#pragma unroll
-                    for (int m = 0; m < 2 * L + 1; ++m) {
-                        const int k = L * L - 1 + m;
-                        float yv = 0.0f;
-                        if (on) {
-                            const float v = dxv[L - 1] * Y[k];
-                            g[k] += (side && (L & 1)) ? -v : v;
-                            yv = dxv[L - 1] * Hn[k];
-                            if (side)
-                                yv = (L & 1) ? -yv : yv;
-                            else
-                                yv = fc * tI[L - 1] * DHn[k] + yv;
-                        }
-                        T[ln.lane * LD + k] = yv;
-                    }
-                wave_sync();
-                if (fc != 0.0f) {
-#pragma unroll
-                    for (int u = 0; u < KQ; ++u) {
-                        const int k = ln.c + W * u;
-                        if (k < NQ) {
-                            float s = 0.0f;
-                            for (int c = 0; c < C; ++c) s += T[(ln.slot * W + c) * LD + k];
-                            dyo[size_t(e) * NQ + k] = yo[u] + s;
-                        }
-                    }
-                }
-                wave_sync();
-                e = en;
-                copy(dxv, dxn);
-                copy(tI, tIn);
-                copy(yo, yon);
-                rbt = rbtn;
-                fc = fcn;
             }
-        }
-    }
-    fold_slots<S>(g);
-    if (ln.slot == 0 && ln.act) {
-        float mx[NQ];
-        float *out = a.ddir_in + size_t(n) * CN + ln.c * NQ;
-        load_row(mx, out);
 #pragma unroll
-        for (int k = 0; k < NQ; ++k) DHn[k] = (DHn[k] + g[k]) + mx[k];
-        store_row(DHn, out);
-    }
-}
-
-// Context-projection adjoints: dE/dA_n = sum of dE/du over the records of n
-// as centre, dE/dB_n over the records that see n as neighbour (records with
-// fc = 0 excluded).  Lanes over the message width, two records in flight.
-__global__ void __launch_bounds__(kBlock) k_eq_atom_sums(EqArgs a) {
-    const int n = wave_atom(a.r);
-    if (n < 0) return;
-    const int lane = threadIdx.x & (kWave - 1), D = a.D;
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const int rec = 4 * s4 + g;
+                float ya[MT];
 #pragma unroll
-    for (int side = 0; side < 2; ++side) {
-        const int b0 = side ? a.r.tptr[n] : a.r.view[4 * n];
-        const int b1 = side ? a.r.tptr[n + 1] : a.r.view[4 * n + 1];
-        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int t0 = b0; t0 < b1; t0 += kWave) {
-            const int cnt = min(kWave, b1 - t0);
-            int me = -1;
-            float mf = 0.0f;
-            if (lane < cnt) {
-                me = side ? a.r.tidx[t0 + lane] : t0 + lane;
-                mf = side ? a.tfc[t0 + lane] : a.fc[t0 + lane];
+                for (int mt = 0; mt < MT; ++mt) ya[mt] = YL[rec * LDY + 16 * mt + r];
+#pragma unroll
+                for (int nt = 0; nt < NTC; ++nt) {
+                    const float b = dueL[rec * LDU + 16 * nt + r];
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma4(ya[mt], b, acc[mt][nt]);
+                }
             }
-            auto fetch = [&](int q, float (&du)[4]) {
-                const int e = bcast(me, min(q, kWave - 1));
-                const float f = bcast(mf, min(q, kWave - 1));
-                zero(du);
-                if (q < cnt && f != 0.0f) {
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        const int d = lane + kWave * u;
-                        if (d < D) du[u] = a.due[size_t(e) * a.ldd + d];
+            for (int v = 0; v < 4; ++v) {
+                const int rec = 4 * g + v;
+                if (rec < cnt) {
+                    const size_t row = size_t(eL[rec]) * NQ;
+#pragma unroll
+                    for (int nt = 0; nt < MT; ++nt) {
+                        const int k = 16 * nt + r;
+                        if (k < NQ) dyo[row + k] = oldL[rec * LDO + k] + p[nt][v];
                     }
                 }
-            };
-            float du0[4], du1[4];
-            fetch(0, du0);
-            fetch(1, du1);
-            for (int q = 0; q < cnt; q += 2) {
-                float dn0[4], dn1[4];
-                fetch(q + 2, dn0);
-                fetch(q + 3, dn1);
-#pragma unroll
-                for (int u = 0; u < 4; ++u) s[u] += du0[u];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) s[u] += du1[u];
-                copy(du0, dn0);
-                copy(du1, dn1);
             }
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int d = lane + kWave * u;
-            if (d < D) a.dnode[size_t(n) * a.NP + side * D + d] = s[u];
-        }
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NTC; ++nt) {
+                if (nt < ntv) {
+                    const int d = c0 + 16 * nt + r;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int k = 16 * mt + 4 * g + v;
+                        if (k < NQ)
+                            dQo[size_t(k) * ldq + d] = acc[mt][nt][v];
+                        else if (k == NQ && d < D)
+                            a.dnode[size_t(n) * a.NP + SIDE * D + d] = acc[mt][nt][v];
+                    }
+                }
+            }
     }
 }
 
@@ -1099,11 +1087,12 @@ __global__ void __launch_bounds__(kWave) k_eq_encoder_backward(const float *ddir
     }
 }
 
-// dE/du of the harmonics: sum_k dY_k scale_k db_k/du, added to dv.xyz.
+// dE/du of the harmonics: sum_k dY_k scale_k db_k/du, added to dv.xyz; dv.w
+// gains dE/dfc fc'(d) and the radial-basis term sum_k dE/drb_k drb_k/dd.
 template <int LQ>
 __global__ void k_eq_harmonic_backward(int64_t E, Records r, const float *fcv, const float *dy,
-                                       const float *dyn, const float *dfc, const float *dd,
-                                       float cutoff,
+                                       const float *dyn, const float *dfc, const float *drb,
+                                       const float *rbd, int ldrb, int kb, float cutoff,
                                        const float *ztab, EdgeZ zoff, const float *scale,
                                        float4 *dv) {
     constexpr int NQ = LQ * (LQ + 2);
@@ -1161,7 +1150,11 @@ __global__ void k_eq_harmonic_backward(int64_t E, Records r, const float *fcv, c
     acc.x += dx;
     acc.y += dyy;
     acc.z += dz;
-    if (fcv[e] != 0.0f) acc.w += dfc[e] * cutoff_slope(v.w, cutoff) + dd[e];
+    if (fcv[e] != 0.0f) {
+        float t = 0.0f;
+        for (int k = 0; k < kb; ++k) t += drb[size_t(e) * ldrb + k] * rbd[size_t(e) * ldrb + k];
+        acc.w += dfc[e] * cutoff_slope(v.w, cutoff) + t;
+    }
     dv[e] = acc;
 }
 
@@ -1226,6 +1219,52 @@ static int edge_dmc(int lq, int D) {
     while (c > 1 && (nq + kRbRegs) * c > 140) --c;
     return c;
 }
+
+// Row stride of the per-record [E, D] arrays: whole column blocks of the
+// edge-MLP kernels.
+static int edge_ld(int lq, int D) {
+    const int dmc = edge_dmc(lq, D);
+    return ceil_div(D, kWave * dmc) * kWave * dmc;
+}
+
+// Output column tiles per block of the edge-MLP reverse kernels: 16 x 4, 8
+// or 12 columns, as many as the register budget allows for the order lq.
+static int adj_ntc(int lq, int ldd) {
+    const int nq = lq * (lq + 2), mt = (nq + 16) / 16, nt = ldd / 16;
+    const int cap = mt <= 2 ? 12 : mt == 3 ? 8 : 4;
+    const int want = nt <= 4 ? 4 : nt <= 8 ? 8 : 12;
+    return std::min(cap, want);
+}
+
+#define EQ_CASE_A(k, L, T, S, ...)                                                        \
+    case T: hipLaunchKernelGGL((k<L, T, S>), __VA_ARGS__); break;
+#define EQ_CASE_AL(k, L, ntc, S, ...)                                                     \
+    case L:                                                                               \
+        switch (ntc) {                                                                    \
+        EQ_CASE_A(k, L, 12, S, __VA_ARGS__)                                               \
+        EQ_CASE_A(k, L, 8, S, __VA_ARGS__)                                                \
+        default: hipLaunchKernelGGL((k<L, 4, S>), __VA_ARGS__); break;                    \
+        }                                                                                 \
+        break;
+// Launches kernel template k<LQ, NTC, S> (the pairs adj_ntc can choose).
+#define EQ_LAUNCH_A(k, lq, ntc, S, ...)                                                    \
+    do {                                                                                  \
+        switch (lq) {                                                                     \
+        EQ_CASE_AL(k, 1, ntc, S, __VA_ARGS__)                                             \
+        EQ_CASE_AL(k, 2, ntc, S, __VA_ARGS__)                                             \
+        EQ_CASE_AL(k, 3, ntc, S, __VA_ARGS__)                                             \
+        EQ_CASE_AL(k, 4, ntc, S, __VA_ARGS__)                                             \
+        case 5:                                                                           \
+            if (ntc == 8)                                                                 \
+                hipLaunchKernelGGL((k<5, 8, S>), __VA_ARGS__);                            \
+            else                                                                          \
+                hipLaunchKernelGGL((k<5, 4, S>), __VA_ARGS__);                            \
+            break;                                                                        \
+        case 6: hipLaunchKernelGGL((k<6, 4, S>), __VA_ARGS__); break;                     \
+        default: hipLaunchKernelGGL((k<7, 4, S>), __VA_ARGS__); break;                    \
+        }                                                                                 \
+        RUNE_HIP_CHECK(hipGetLastError());                                                \
+    } while (0)
 
 #define EQ_CASE_D(k, L, D, grid, block, lds, s, ...)                                      \
     case D:                                                                               \
@@ -1343,7 +1382,7 @@ void pack_equivariant(ModelImpl &m, Packer &pk, std::map<std::string, size_t> &o
     const int T = c.n_types, H = c.hidden_dim, D = c.message_dim, P = c.pair_dim;
     const int G = c.message_groups, kb = c.message_basis_size;
     const int lq = c.equivariant_l_max, C = c.equivariant_channels, W = lq * C;
-    const int K = kb + P + 2 * D + 2 * W, NP = 2 * D + H, NG = G + 2 * W, KX = kb + 2 * W;
+    const int K = kb + P + 2 * D + 2 * W, NP = 2 * D + H, NG = G + 2 * W;
     std::vector<float> enc;
     for (int L = 0; L < lq; ++L) {
         const auto &t = m.tensor("direction_encoder.projections." + std::to_string(L) + ".weight");
@@ -1376,14 +1415,8 @@ void pack_equivariant(ModelImpl &m, Packer &pk, std::map<std::string, size_t> &o
         node = fold_cols(node, NP, H, win.data());
         off[p + "node_f"] = pk.put(node);
         off[p + "node_fT"] = pk.put(transpose(node, NP, H));
-        std::vector<float> wx = columns(we, D, K, 0, kb);                    // [D, KX]
-        std::vector<float> wp = columns(we, D, K, kb + P + 2 * D, K);
-        std::vector<float> x(size_t(D) * KX);
-        for (int r = 0; r < D; ++r) {
-            for (int k = 0; k < kb; ++k) x[size_t(r) * KX + k] = wx[size_t(r) * kb + k];
-            for (int k = 0; k < 2 * W; ++k) x[size_t(r) * KX + kb + k] = wp[size_t(r) * 2 * W + k];
-        }
-        off[p + "edge_xT"] = pk.put(transpose(x, D, KX));
+        std::vector<float> wx = columns(we, D, K, 0, kb);                    // [D, kb]
+        std::vector<float> wp = columns(we, D, K, kb + P + 2 * D, K);        // [D, 2W]
         // factored edge MLP: [kb, D] radial-basis rows and [lq C, D] probe rows,
         // the neighbour probes signed (-1)^L
         off[p + "edge_rbT"] = pk.put(transpose(wx, D, kb));
@@ -1399,6 +1432,14 @@ void pack_equivariant(ModelImpl &m, Packer &pk, std::map<std::string, size_t> &o
             }
         off[p + "probe_c"] = pk.put(pc);
         off[p + "probe_n"] = pk.put(pn);
+        const int ldd = edge_ld(lq, D);
+        std::vector<float> cat(size_t(W) * 2 * ldd, 0.0f);
+        for (int row = 0; row < W; ++row)
+            for (int r = 0; r < D; ++r) {
+                cat[size_t(row) * 2 * ldd + r] = pc[size_t(row) * D + r];
+                cat[size_t(row) * 2 * ldd + ldd + r] = pn[size_t(row) * D + r];
+            }
+        off[p + "probe_cat"] = pk.put(cat);
         off[p + "pair_proj"] = pk.put(pair_projection(m.tensor(p + "pair_embedding.weight"), we,
                                                       m.tensor(p + "edge_mlp.0.bias"), T * T, P,
                                                       D, K, kb));
@@ -1410,6 +1451,11 @@ void pack_equivariant(ModelImpl &m, Packer &pk, std::map<std::string, size_t> &o
         gb.insert(gb.end(), db.begin(), db.end());
         off[p + "gate"] = pk.put(gate);
         off[p + "gate_T"] = pk.put(transpose(gate, NG, D));
+        {
+            std::vector<float> gtp = transpose(gate, NG, D);
+            gtp.resize(size_t(edge_ld(lq, D)) * NG, 0.0f);
+            off[p + "gate_Tp"] = pk.put(gtp);
+        }
         off[p + "gate_b"] = pk.put(gb);
         std::vector<float> mix;
         for (int L = 0; L < lq; ++L) {
@@ -1445,10 +1491,11 @@ void bind_equivariant(ModelImpl &m, const PackedLookup &P) {
         w.ld_edge_x = (w.KX + 3) & ~3;
         w.node_f = P(p + "node_f");
         w.node_fT = P(p + "node_fT");
-        w.edge_xT = P(p + "edge_xT");
         w.edge_rbT = P(p + "edge_rbT");
         w.probe_c = P(p + "probe_c");
         w.probe_n = P(p + "probe_n");
+        w.probe_cat = P(p + "probe_cat");
+        w.gate_Tp = P(p + "gate_Tp");
         w.pair_proj = P(p + "pair_proj");
         w.gate = P(p + "gate");
         w.gate_T = P(p + "gate_T");
@@ -1469,8 +1516,7 @@ MessagePlan plan_equivariant(ModelImpl &m, Arena &ar, int N, int64_t E) {
     const size_t n = size_t(N), e = size_t(std::max<int64_t>(E, 1));
     const int H = c.hidden_dim, D = c.message_dim, lq = c.equivariant_l_max;
     const int C = c.equivariant_channels, W = lq * C, nq = lq * (lq + 2), CN = C * nq;
-    const int NP = 2 * D + H, NG = c.message_groups + 2 * W, KX = c.message_basis_size + 2 * W;
-    const int ldx = (KX + 3) & ~3;
+    const int NP = 2 * D + H, NG = c.message_groups + 2 * W;
     p.N = N;
     p.E = E;
     p.ldrb = (c.message_basis_size + 3) & ~3;
@@ -1485,11 +1531,10 @@ MessagePlan plan_equivariant(ModelImpl &m, Arena &ar, int N, int64_t E) {
     p.i_dharm = p.add(ar, 4 * e * nq);
     p.i_dharm_n = p.add(ar, 4 * e * nq);
     p.i_dfc = p.add(ar, 4 * e);
-    p.i_dd = p.add(ar, 4 * e);
+    p.i_drb = p.add(ar, 4 * e * p.ldrb);
     p.i_rbd = p.add(ar, 4 * e * p.ldrb);
     int dir0 = p.add(ar, 4 * n * CN);
-    const int dmc = edge_dmc(lq, D);
-    p.ld_edge = ceil_div(D, kWave * dmc) * kWave * dmc;
+    p.ld_edge = edge_ld(lq, D);
     const size_t ldd = size_t(p.ld_edge);
     int eh = p.add(ar, 4 * e * ldd);       // shared by the blocks (forward only)
     for (int b = 0; b < c.message_layers; ++b) {
@@ -1508,6 +1553,7 @@ MessagePlan plan_equivariant(ModelImpl &m, Arena &ar, int N, int64_t E) {
         bb.dir_in = b == 0 ? dir0 : p.blocks[b - 1].dir_out;
         bb.dir_out = p.add(ar, 4 * n * CN);
         bb.mixstate = p.add(ar, 4 * n * CN);
+        bb.q = p.add(ar, 4 * n * nq * 2 * ldd);
         p.blocks.push_back(bb);
     }
     p.t_dz1 = p.add(ar, 4 * n * D);
@@ -1516,7 +1562,8 @@ MessagePlan plan_equivariant(ModelImpl &m, Arena &ar, int N, int64_t E) {
     p.t_dvsum = p.add(ar, 4 * n * CN);     // dE/d(dir_out) total
     p.t_dgv = p.add(ar, 4 * e * NG);
     p.t_due = p.add(ar, 4 * e * ldd);
-    p.t_dx = p.add(ar, 4 * e * ldx);
+    p.t_dq = p.add(ar, 4 * n * nq * 2 * ldd);
+    p.t_dhk = p.add(ar, 4 * n * CN);
     p.t_dvs = p.add(ar, 4 * n * NP);
     p.t_dmix = p.add(ar, 4 * n * CN);
     p.t_ddir0 = p.add(ar, 4 * n * CN);
@@ -1524,7 +1571,6 @@ MessagePlan plan_equivariant(ModelImpl &m, Arena &ar, int N, int64_t E) {
     p.t_dz = p.add(ar, 4 * n * H);
     p.t_dh0 = p.add(ar, 4 * n * H);
     p.t_dh1 = p.add(ar, 4 * n * H);
-    p.ldrb_x = ldx;
     return p;
 }
 
@@ -1542,8 +1588,6 @@ static EqArgs eq_args(ModelImpl &m, MessagePlan &p, const Records &r, int b) {
     a.NG = a.G + 2 * a.lq * a.C;
     a.NP = 2 * a.D + a.H;
     a.kb = c.message_basis_size;
-    a.KX = a.kb + 2 * a.lq * a.C;
-    a.ldx = p.ldrb_x;
     a.na = m.desc.na;
     a.nlm = m.desc.nlm;
     a.S = eq_slots(a.C);
@@ -1583,14 +1627,13 @@ static EqArgs eq_args(ModelImpl &m, MessagePlan &p, const Records &r, int b) {
     a.dgg = p.at(p.t_dgv);
     a.dv = reinterpret_cast<float4 *>(p.at(p.i_dv));
     a.dfc = p.at(p.i_dfc);
-    a.dd = p.at(p.i_dd);
-    a.rbd = p.at(p.i_rbd);
     a.dy = p.at(p.i_dharm);
     a.dyn = p.at(p.i_dharm_n);
     a.dnode = p.at(p.t_dvs);
     a.dmix = p.at(p.t_dmix);
     a.due = p.at(p.t_due);
-    a.dx = p.at(p.t_dx);
+    a.qbuf = p.at(bb.q);
+    a.dqbuf = p.at(p.t_dq);
     return a;
 }
 
@@ -1618,7 +1661,6 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dharm), 0, 4 * size_t(E) * nq, s));
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dharm_n), 0, 4 * size_t(E) * nq, s));
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dfc), 0, 4 * size_t(E), s));
-        RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dd), 0, 4 * size_t(E), s));
     }
     hipLaunchKernelGGL(k_eq_encode, dim3(N), dim3(kWave), 0, s, N, moments, m.desc.na,
                        m.desc.nlm, m.enc_w, m.harm_scale, C, nq, p.at(p.blocks[0].dir_in));
@@ -1633,7 +1675,7 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
         e0.row_scale = p.at(bb.rin);
         gemm(N, w.NP, H, cur, H, w.node_f, H, p.at(bb.vs), w.NP, e0, s);
         EQ_LAUNCH(k_eq_mix, lq, dim3(mix_grid), dim3(256), mix_lds, s, N, w.mix,
-                  p.at(bb.dir_in), C, 0, p.at(bb.mixstate));
+                  p.at(bb.dir_in), C, 0, nullptr, nullptr, p.at(bb.mixstate));
         if (E > 0) {
             const int dmc = edge_dmc(lq, D), cn4 = (C * nq + 3) & ~3;
             const int ly = nq + (nq % 4 == 0 ? 4 : 1);
@@ -1689,10 +1731,15 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
     const rune_model_config &c = m.cfg;
     const int N = p.N, H = c.hidden_dim, D = c.message_dim, act = c.activation;
     const int lq = c.equivariant_l_max, C = c.equivariant_channels, nq = lq * (lq + 2);
-    const int NU = H + lq * C;
+    const int NU = H + lq * C, kb = c.message_basis_size, ldd = p.ld_edge;
     const int64_t E = p.E;
     const int atom_grid = ceil_div(N, kWaves), mix_grid = std::max(1, std::min(N, 2048));
     const size_t mix_lds = sizeof(float) * (size_t(lq) * C * (C + 1) + size_t(C) * nq);
+    const int ly = nq + (nq % 4 == 0 ? 4 : 1);
+    const int ntc = adj_ntc(lq, ldd), mt = (nq + 16) / 16;
+    // per-wave LDS of the reverse edge-MLP kernels: due, harmonic and old dE/dY
+    // rows of one batch, and its record ids
+    const int adj_wlds = kAdjBatch * ((16 * ntc + 4) + (16 * mt + 4) + (nq + 1) + 1);
     float *cur = dh;
     const float *ddir_out = nullptr;   // the last block's states feed only its invariants
     float *ddir_in = p.at(p.t_ddir0);
@@ -1713,7 +1760,7 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         {
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
             EQ_LAUNCH_S(k_eq_pair_dir, lq, a.S, dim3(atom_grid), dim3(kBlock),
-                        sizeof(float) * kBlock * (nq + (nq % 4 == 0 ? 4 : 1)), s, a);
+                        sizeof(float) * kBlock * (ly + nq + 1), s, a);
         }
         {
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
@@ -1721,36 +1768,50 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
                                a.gmode == 2 ? sizeof(float) * kWaves * H : 0, s, a);
         }
         RUNE_HIP_CHECK(hipGetLastError());
-        // channel-mix adjoint M^T dmix, completed by k_eq_atom_backward
-        EQ_LAUNCH(k_eq_mix, lq, dim3(mix_grid), dim3(256), mix_lds, s, N, w.mix, a.dmix, C, 1,
-                  a.ddir_in);
         if (E > 0) {
+            // due = (dE/dgates) gate^T * act'(u), zero in the padding columns
             Epilogue e2;
             e2.dact_from = p.at(bb.ue);
-            e2.ldu = p.ld_edge;
+            e2.ldu = ldd;
             e2.dact = act;
             {
                 Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
-                gemm(int(E), D, w.NG, p.at(p.t_dgv), w.NG, w.gate_T, w.NG, p.at(p.t_due),
-                     p.ld_edge, e2, s);
+                gemm(int(E), ldd, w.NG, p.at(p.t_dgv), w.NG, w.gate_Tp, w.NG, p.at(p.t_due), ldd,
+                     e2, s);
             }
+            // dE/drb = due W_rb^T, summed over the blocks
             Epilogue e3;
+            if (b != c.message_layers - 1) {
+                e3.residual = p.at(p.i_drb);
+                e3.ldr = p.ldrb;
+            }
             {
                 Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
-                gemm(int(E), w.KX, D, p.at(p.t_due), p.ld_edge, w.edge_xT, D, p.at(p.t_dx), a.ldx,
-                     e3, s);
+                gemm(int(E), kb, D, p.at(p.t_due), ldd, w.edge_rbT, D, p.at(p.i_drb), p.ldrb, e3,
+                     s);
             }
         }
         {
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
-            EQ_LAUNCH_S(k_eq_atom_dir, lq, a.S, dim3(atom_grid), dim3(kBlock),
-                        sizeof(float) * kBlock * (2 * nq + 1 + (nq % 4 == 0 ? 4 : 1)), s, a);
+            a.wlds = adj_wlds;
+            const size_t lds = sizeof(float) * kWaves * adj_wlds;
+            EQ_LAUNCH_A(k_eq_edge_adj, lq, ntc, 0, dim3(atom_grid), dim3(kBlock), lds, s, a);
+            EQ_LAUNCH_A(k_eq_edge_adj, lq, ntc, 1, dim3(atom_grid), dim3(kBlock), lds, s, a);
         }
+        // channel projection of the factor adjoints: dHk[n, k, :] = dQ[n, k, :] [Wc | Wn]_L(k)^T
         {
-            Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
-            hipLaunchKernelGGL(k_eq_atom_sums, dim3(atom_grid), dim3(kBlock), 0, s, a);
+            GemmBatch bt;
+            bt.count = nq;
+            bt.sa = 2 * int64_t(ldd);
+            bt.sb = int64_t(C) * 2 * ldd;
+            bt.sc = C;
+            bt.b_by_order = 1;
+            gemm_batched(bt, N, C, 2 * ldd, p.at(p.t_dq), nq * 2 * ldd, w.probe_cat, 2 * ldd,
+                         p.at(p.t_dhk), nq * C, s);
         }
-        RUNE_HIP_CHECK(hipGetLastError());
+        // dE/d(dir_in) = M^T dmix + dE/d(dir_out) + the factor adjoints
+        EQ_LAUNCH(k_eq_mix, lq, dim3(mix_grid), dim3(256), mix_lds, s, N, w.mix, a.dmix, C, 1,
+                  p.at(p.t_dvsum), p.at(p.t_dhk), a.ddir_in);
         Epilogue e4;
         gemm(N, H, w.NP, p.at(p.t_dvs), w.NP, w.node_fT, w.NP, p.at(p.t_dz), H, e4, s);
         float *next = (cur == p.at(p.t_dh0)) ? p.at(p.t_dh1) : p.at(p.t_dh0);
@@ -1769,8 +1830,8 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
             EQ_LAUNCH(k_eq_harmonic_backward, lq, dim3(ceil_div(E, 256)), dim3(256), 0, s, E, r,
                       p.at(p.i_fc), p.at(p.i_dharm), p.at(p.i_dharm_n), p.at(p.i_dfc),
-                      p.at(p.i_dd), float(c.message_cutoff), m.desc.z, zo, m.harm_scale,
-                      reinterpret_cast<float4 *>(p.at(p.i_dv)));
+                      p.at(p.i_drb), p.at(p.i_rbd), p.ldrb, kb, float(c.message_cutoff),
+                      m.desc.z, zo, m.harm_scale, reinterpret_cast<float4 *>(p.at(p.i_dv)));
         }
     }
     RUNE_HIP_CHECK(hipGetLastError());

@@ -98,6 +98,16 @@ struct Epilogue {
 // C[M,N] = A[M,K] Bt[N,K]^T (+ epilogue); row-major with leading dimensions.
 void gemm(int M, int N, int K, const float *A, int lda, const float *Bt, int ldb, float *C,
           int ldc, const Epilogue &ep, hipStream_t s);
+// count independent products: batch z uses A + z sa, C + z sc and Bt + w sb,
+// w = z, or w = L(z) - 1 with L(z) the harmonic order of component z
+// (z = L^2 - 1 + m) when b_by_order is set.
+struct GemmBatch {
+    int count = 1;
+    int64_t sa = 0, sb = 0, sc = 0;
+    int b_by_order = 0;
+};
+void gemm_batched(const GemmBatch &bt, int M, int N, int K, const float *A, int lda,
+                  const float *Bt, int ldb, float *C, int ldc, hipStream_t s);
 // inv_rms[m] = rsqrt(mean_n x[m,n]^2 + eps)
 void row_inv_rms(int M, int N, const float *x, int ldx, float eps, float *inv_rms, hipStream_t s);
 // dh[m] = base[m] + r*dz[m] - r^3/N (dz[m].h[m]) h[m]   (RMSNorm backward + residual)

@@ -39,8 +39,11 @@ struct MessageWeights {
     // edge MLP on per-edge features: MP [radial basis], EQ [radial basis | probes]
     const float *edge_xT, *edge_x;    // [KX, D], [D, ld_edge_x]
     int KX, ld_edge_x;
-    // EQ factored edge MLP: radial-basis rows [kb, D], probe rows [lq*C, D]
+    // EQ factored edge MLP: radial-basis rows [kb, D], probe rows [lq*C, D],
+    // both probe blocks per order [lq][C][2 ldd] (zero past D), and the gate
+    // transpose with zero rows up to ldd [ldd, NG]
     const float *edge_rbT = nullptr, *probe_c = nullptr, *probe_n = nullptr;
+    const float *probe_cat = nullptr, *gate_Tp = nullptr;
     const float *pair_proj;           // [T*T, D] = pair_embedding W_pair^T + b
     // gates from the edge hidden state: MP [groups | vector], EQ [groups | directions]
     const float *gate_T, *gate, *gate_b;   // [D, NG], [NG, D], [NG]
@@ -65,6 +68,7 @@ struct BlockBuffers {
     int h_out = -1, rin = -1, vs = -1, ue = -1, eh = -1, gv = -1, msg = -1, rm = -1;
     int vsum = -1, mixed = -1, uin = -1, u1 = -1, z1 = -1;
     int dir_in = -1, dir_out = -1, mixstate = -1;   // EQ angular states
+    int q = -1;                                      // EQ per-atom edge-MLP factors
 };
 
 struct MessagePlan {
@@ -76,15 +80,16 @@ struct MessagePlan {
     int N = 0;
     int64_t E = 0;
     size_t o_gd = 0, o_dmom = 0;
-    int ldrb = 0, ldrb_x = 0;
+    int ldrb = 0;
     int ld_edge = 0;              // EQ: row stride of the per-record [E, D] arrays
     int i_rb = -1, i_fc = -1, i_tfc = -1, i_pair = -1, i_dv = -1, i_harm = -1, i_dharm = -1, i_dharm_n = -1;
-    int i_dfc = -1, i_dd = -1, i_rbd = -1;
+    int i_dfc = -1, i_drb = -1, i_rbd = -1;
     std::vector<BlockBuffers> blocks;
     // reverse-pass temporaries shared by the blocks
     int t_dz1 = -1, t_duin = -1, t_dmsg = -1, t_dvsum = -1, t_dgv = -1, t_due = -1;
     int t_drb = -1, t_dvs = -1, t_dz = -1, t_dh0 = -1, t_dh1 = -1;
-    int t_ddir0 = -1, t_ddir1 = -1, t_dmix = -1, t_dx = -1, t_dab = -1;
+    int t_ddir0 = -1, t_ddir1 = -1, t_dmix = -1, t_dab = -1;
+    int t_dq = -1, t_dhk = -1;    // EQ: per-atom factor adjoints, their channel projection
     std::vector<const float *> block_input;
     int add(Arena &ar, size_t bytes);
     void bind(char *base);
