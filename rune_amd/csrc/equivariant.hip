@@ -530,31 +530,29 @@ __global__ void __launch_bounds__(kBlock) k_eq_aggregate(EqArgs a) {
             mj = a.r.nbr[t0 + ln.lane];
             mf = a.fc[t0 + ln.lane];
         }
+        // every lane loads (clamped indices), so the compiler's waits stay exact
         auto fetch = [&](int q, float (&y)[NQ], float (&mx)[NQ], float (&tt)[LQ],
                          float (&ti)[LQ], float (&v)[HM], float (&g)[HM], float &f) {
-            const int j = bcast(mj, min(q, kWave - 1));
-            f = bcast(mf, min(q, kWave - 1));
-            if (q >= cnt) f = 0.0f;
-            if (f != 0.0f) {
-                const int e = t0 + q;
-                if (ln.act) {
-                    load_row(y, a.harm + size_t(e) * NQ);
-                    load_row(mx, a.mixst + size_t(j) * CN + ln.c * NQ);
-                    const float *gr = a.ag + size_t(e) * NG + G + ln.c;
+            const int qq = min(q, cnt - 1);
+            const int j = bcast(mj, qq);
+            const float fq = bcast(mf, qq);   // every lane joins the shuffle
+            f = q < cnt ? fq : 0.0f;
+            const int e = t0 + qq, cl = min(ln.c, C - 1);
+            load_row(y, a.harm + size_t(e) * NQ);
+            load_row(mx, a.mixst + size_t(j) * CN + cl * NQ);
+            const float *gd = a.ag + size_t(e) * NG + G + cl;
 #pragma unroll
-                    for (int L = 0; L < LQ; ++L) {
-                        tt[L] = gr[L * C];
-                        ti[L] = gr[LC + L * C];
-                    }
-                }
-                const float *Vr = a.node + size_t(j) * a.NP + 2 * a.D;
-                const float *gr = a.ag + size_t(e) * NG;
+            for (int L = 0; L < LQ; ++L) {
+                tt[L] = gd[L * C];
+                ti[L] = gd[LC + L * C];
+            }
+            const float *Vr = a.node + size_t(j) * a.NP + 2 * a.D;
+            const float *gr = a.ag + size_t(e) * NG;
 #pragma unroll
-                for (int u = 0; u < HM; ++u) {
-                    const int h = ln.c + Ln::W * u;
-                    v[u] = h < H ? Vr[h] : 0.0f;
-                    g[u] = h < H ? gr[h / gw] : 0.0f;
-                }
+            for (int u = 0; u < HM; ++u) {
+                const int h = min(ln.c + Ln::W * u, H - 1);
+                v[u] = Vr[h];
+                g[u] = gr[h / gw];
             }
         };
         float Y[NQ], M[NQ], tT[LQ], tI[LQ], V[HM], g[HM], fc;
@@ -686,30 +684,22 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
             }
         }
         wave_sync();
+        // every lane loads (clamped indices), so the compiler's waits stay exact
         auto fetch = [&](int q, int &e, float (&dh)[NQ], float (&tt)[LQ], float (&ti)[LQ],
                          float (&yo)[KQ], float &f) {
-            e = bcast(me, min(q, kWave - 1));
-            const int i = bcast(mi, min(q, kWave - 1));
-            f = bcast(mf, min(q, kWave - 1));
-            if (q >= cnt) {
-                e = -1;
-                f = 0.0f;
-            }
-            if (f != 0.0f) {
+            const int qq = min(q, cnt - 1);
+            const int ec = bcast(me, qq), i = bcast(mi, qq), cl = min(ln.c, C - 1);
+            const float fq = bcast(mf, qq);   // every lane joins the shuffle
+            f = q < cnt ? fq : 0.0f;
+            e = q < cnt ? ec : -1;
 #pragma unroll
-                for (int u = 0; u < KQ; ++u) {
-                    const int k = ln.c + W * u;
-                    yo[u] = k < NQ ? a.dy[size_t(e) * NQ + k] : 0.0f;
-                }
-            }
-            if (f != 0.0f && ln.act) {
-                load_row(dh, a.dht + size_t(i) * CN + ln.c * NQ);
-                const float *gr = a.ag + size_t(e) * NG + G + ln.c;
+            for (int u = 0; u < KQ; ++u) yo[u] = a.dy[size_t(ec) * NQ + min(ln.c + W * u, NQ - 1)];
+            load_row(dh, a.dht + size_t(i) * CN + cl * NQ);
+            const float *gr = a.ag + size_t(ec) * NG + G + cl;
 #pragma unroll
-                for (int L = 0; L < LQ; ++L) {
-                    tt[L] = gr[L * C];
-                    ti[L] = gr[LC + L * C];
-                }
+            for (int L = 0; L < LQ; ++L) {
+                tt[L] = gr[L * C];
+                ti[L] = gr[LC + L * C];
             }
         };
         int e;
@@ -814,27 +804,20 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_grp(EqArgs a) {
             mf = a.tfc[t0 + lane];
             md = a.dfc[me];
         }
+        // every lane loads (clamped indices), so the compiler's waits stay exact
         auto fetch = [&](int q, int &e, float (&dm)[4], float (&sg)[4], float &f) {
-            e = bcast(me, min(q, kWave - 1));
-            const int i = bcast(mi, min(q, kWave - 1));
-            f = bcast(mf, min(q, kWave - 1));
-            if (q >= cnt) {
-                e = -1;
-                f = 0.0f;
-            }
-            zero(dm);
-            zero(sg);
-            if (f != 0.0f) {
-                const float *dr = a.dmsg + size_t(i) * H;
-                const float *gr = a.ag + size_t(e) * NG;
+            const int qq = min(q, cnt - 1);
+            e = lane_get(me, qq);
+            const int i = lane_get(mi, qq);
+            const float fq = lane_get(mf, qq);
+            f = q < cnt ? fq : 0.0f;
+            const float *dr = a.dmsg + size_t(i) * H;
+            const float *gr = a.ag + size_t(e) * NG;
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int h = lane + kWave * u;
-                    if (h < H) {
-                        dm[u] = dr[h];
-                        sg[u] = gr[h / gw];
-                    }
-                }
+            for (int u = 0; u < 4; ++u) {
+                const int h = min(lane + kWave * u, H - 1);
+                dm[u] = dr[h];
+                sg[u] = gr[h / gw];
             }
         };
         int e, e1;
@@ -1004,20 +987,26 @@ __global__ void __launch_bounds__(kBlock) k_eq_edge_adj(EqArgs a) {
                 if (qq == 0) eL[rec] = e;
             }
             wave_sync();
-            floatx4 p[MT];
+            // four independent accumulation chains per tile keep the matrix pipe busy
+            floatx4 pc[4][MT];
 #pragma unroll
-            for (int nt = 0; nt < MT; ++nt) p[nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int h = 0; h < 4; ++h)
+#pragma unroll
+                for (int nt = 0; nt < MT; ++nt) pc[h][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int t = 0; t < NTC; ++t) {
                 const float4 av = *reinterpret_cast<const float4 *>(dueL + r * LDU + 16 * t + 4 * g);
 #pragma unroll
                 for (int nt = 0; nt < MT; ++nt) {
-                    p[nt] = mfma4(av.x, Bq[t][nt][0], p[nt]);
-                    p[nt] = mfma4(av.y, Bq[t][nt][1], p[nt]);
-                    p[nt] = mfma4(av.z, Bq[t][nt][2], p[nt]);
-                    p[nt] = mfma4(av.w, Bq[t][nt][3], p[nt]);
+                    pc[0][nt] = mfma4(av.x, Bq[t][nt][0], pc[0][nt]);
+                    pc[1][nt] = mfma4(av.y, Bq[t][nt][1], pc[1][nt]);
+                    pc[2][nt] = mfma4(av.z, Bq[t][nt][2], pc[2][nt]);
+                    pc[3][nt] = mfma4(av.w, Bq[t][nt][3], pc[3][nt]);
                 }
             }
+            floatx4 p[MT];
+#pragma unroll
+            for (int nt = 0; nt < MT; ++nt) p[nt] = (pc[0][nt] + pc[1][nt]) + (pc[2][nt] + pc[3][nt]);
 #pragma unroll
             for (int s4 = 0; s4 < 4; ++s4) {
                 const int rec = 4 * s4 + g;
