@@ -1220,8 +1220,8 @@ static int edge_ld(int lq, int D) {
 // or 12 columns, as many as the register budget allows for the order lq.
 static int adj_ntc(int lq, int ldd) {
     const int nq = lq * (lq + 2), mt = (nq + 16) / 16, nt = ldd / 16;
-    const int cap = mt <= 2 ? 12 : mt == 3 ? 8 : 4;
-    const int want = nt <= 4 ? 4 : nt <= 8 ? 8 : 12;
+    const int cap = mt <= 2 ? 6 : mt == 3 ? 6 : 4;
+    const int want = nt <= 4 ? 4 : 6;
     return std::min(cap, want);
 }
 
@@ -1230,8 +1230,7 @@ static int adj_ntc(int lq, int ldd) {
 #define EQ_CASE_AL(k, L, ntc, S, ...)                                                     \
     case L:                                                                               \
         switch (ntc) {                                                                    \
-        EQ_CASE_A(k, L, 12, S, __VA_ARGS__)                                               \
-        EQ_CASE_A(k, L, 8, S, __VA_ARGS__)                                                \
+        EQ_CASE_A(k, L, 6, S, __VA_ARGS__)                                                \
         default: hipLaunchKernelGGL((k<L, 4, S>), __VA_ARGS__); break;                    \
         }                                                                                 \
         break;
@@ -1244,8 +1243,8 @@ static int adj_ntc(int lq, int ldd) {
         EQ_CASE_AL(k, 3, ntc, S, __VA_ARGS__)                                             \
         EQ_CASE_AL(k, 4, ntc, S, __VA_ARGS__)                                             \
         case 5:                                                                           \
-            if (ntc == 8)                                                                 \
-                hipLaunchKernelGGL((k<5, 8, S>), __VA_ARGS__);                            \
+            if (ntc == 6)                                                                 \
+                hipLaunchKernelGGL((k<5, 6, S>), __VA_ARGS__);                            \
             else                                                                          \
                 hipLaunchKernelGGL((k<5, 4, S>), __VA_ARGS__);                            \
             break;                                                                        \
