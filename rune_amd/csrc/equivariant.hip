@@ -443,7 +443,7 @@ __global__ void __launch_bounds__(kBlock) k_eq_edge_nbr(EqArgs a) {
 
 // Centre side: u = A_i + (the neighbour pass's row) + (fc != 0: Qc_i Y_e),
 // stored as ue (pre-activation) and eh = act(u).  The records of a centre are
-// contiguous, so the rows of the next two are loaded while one is computed.
+// contiguous, so the rows of the next six are loaded while one is computed.
 template <int LQ, int DMC>
 __global__ void __launch_bounds__(kBlock) k_eq_edge_centre(EqArgs a) {
     constexpr int NQ = LQ * (LQ + 2), LY = NQ + (NQ % 4 == 0 ? 4 : 1);
@@ -467,9 +467,12 @@ __global__ void __launch_bounds__(kBlock) k_eq_edge_centre(EqArgs a) {
 #pragma unroll
         for (int u = 0; u < DMC; ++u) X[u] = a.ue[row + col.d[u]];
     };
-    float X0[DMC], X1[DMC];
-    fetch(b0, X0);
-    fetch(b0 + 1, X1);
+    // ring of the next kPf rows: loads stay in flight across the stores of
+    // several records (vector loads and stores share one in-order counter)
+    constexpr int kPf = 6;
+    float X[kPf][DMC];
+#pragma unroll
+    for (int f = 0; f < kPf; ++f) fetch(b0 + f, X[f]);
     for (int t0 = b0; t0 < b1; t0 += kWave) {
         const int cnt = min(kWave, b1 - t0);
         float mf = 0.0f;
@@ -481,8 +484,8 @@ __global__ void __launch_bounds__(kBlock) k_eq_edge_centre(EqArgs a) {
         wave_sync();
         for (int q = 0; q < cnt; ++q) {
             const int e = t0 + q;
-            float X2[DMC];
-            fetch(e + 2, X2);
+            float Xn[DMC];
+            fetch(e + kPf, Xn);
             float acc[DMC];
 #pragma unroll
             for (int u = 0; u < DMC; ++u) acc[u] = 0.0f;
@@ -495,12 +498,13 @@ __global__ void __launch_bounds__(kBlock) k_eq_edge_centre(EqArgs a) {
             const bool on = lane_get(mf, q) != 0.0f;
 #pragma unroll
             for (int u = 0; u < DMC; ++u) {
-                const float v = (A[u] + X0[u]) + (on ? acc[u] : 0.0f);
+                const float v = (A[u] + X[0][u]) + (on ? acc[u] : 0.0f);
                 a.ue[size_t(e) * ldd + col.d[u]] = v;
                 a.eh[size_t(e) * ldd + col.d[u]] = act_f(act, v);
             }
-            copy(X0, X1);
-            copy(X1, X2);
+#pragma unroll
+            for (int f = 0; f + 1 < kPf; ++f) copy(X[f], X[f + 1]);
+            copy(X[kPf - 1], Xn);
         }
     }
 }
@@ -907,6 +911,34 @@ __device__ inline floatx4 mfma4(float a, float b, floatx4 c) {
 // Records per matrix-core batch of the edge-MLP reverse kernels.
 constexpr int kAdjBatch = 16;
 
+// One lane's share of a batch row: quarter qq of the due row (NTC float4 of
+// the column block), 4 MT harmonic values and the old dE/dY values
+// qq + 4 i.  Indices are clamped, so every lane loads.
+template <int NTC, int NY, int KO>
+struct AdjRows {
+    float dv[4 * NTC];
+    float yv[NY], ov[KO];
+};
+template <int NTC, int NY, int KO, int NQ>
+__device__ __forceinline__ AdjRows<NTC, NY, KO> adj_rows(const float *due, int n4, int qq,
+                                                        const float *harm, const float *dy) {
+    AdjRows<NTC, NY, KO> st;
+    const float4 *src = reinterpret_cast<const float4 *>(due);
+#pragma unroll
+    for (int i = 0; i < NTC; ++i) {
+        const float4 v = src[min(qq * NTC + i, n4 - 1)];
+        st.dv[4 * i] = v.x;
+        st.dv[4 * i + 1] = v.y;
+        st.dv[4 * i + 2] = v.z;
+        st.dv[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < NY; ++i) st.yv[i] = harm[min(qq * NY + i, NQ - 1)];
+#pragma unroll
+    for (int i = 0; i < KO; ++i) st.ov[i] = dy[min(qq + 4 * i, NQ - 1)];
+    return st;
+}
+
 // Reverse of the factored edge MLP for the records of atom n on one side
 // (SIDE 0: the records with centre n, SIDE 1: the records with neighbour n),
 // on the matrix cores (v_mfma_f32_16x16x4f32), 16 records at a time.  With
@@ -924,7 +956,7 @@ constexpr int kAdjBatch = 16;
 // k-steps take d = 16 t + 4 (l/16) + s (s = 0..3), so each lane reads its four
 // A values with one 16-byte LDS read.
 template <int LQ, int NTC, int SIDE>
-__global__ void __launch_bounds__(kBlock) k_eq_edge_adj(EqArgs a) {
+__global__ void __launch_bounds__(kBlock, 2) k_eq_edge_adj(EqArgs a) {
     constexpr int NQ = LQ * (LQ + 2), MT = (NQ + 16) / 16, KP = 16 * MT;
     constexpr int CW = 16 * NTC, LDU = CW + 4, LDY = KP + 4, LDO = NQ + 1;
     extern __shared__ float lds[];
@@ -960,37 +992,58 @@ __global__ void __launch_bounds__(kBlock) k_eq_edge_adj(EqArgs a) {
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int nt = 0; nt < NTC; ++nt) acc[mt][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        // The rows of batch b + 1 are loaded into registers while batch b is
+        // on the matrix cores, and written to LDS once its reads are done;
+        // the record ids run one batch further ahead.  Lane l stages row
+        // l / 4 of a batch, quarter l % 4 of each row.
+        const int rec = lane >> 2, qq = lane & 3;
+        constexpr int KO = (NQ + 3) / 4;
+        auto record_of = [&](int t0) {
+            const int rv = min(rec, max(min(kAdjBatch, b1 - t0), 1) - 1);
+            return SIDE ? a.r.tidx[min(t0 + rv, b1 - 1)] : min(t0 + rv, b1 - 1);
+        };
+        AdjRows<NTC, 4 * MT, KO> st;
+        int e_cur = 0, e_nxt = 0;
+        if (b1 > b0) {
+            e_cur = record_of(b0);
+            e_nxt = record_of(b0 + kAdjBatch);
+            st = adj_rows<NTC, 4 * MT, KO, NQ>(a.due + size_t(e_cur) * ldd + c0, 4 * ntv, qq,
+                                               a.harm + size_t(e_cur) * NQ,
+                                               dyo + size_t(e_cur) * NQ);
+        }
         for (int t0 = b0; t0 < b1; t0 += kAdjBatch) {
             const int cnt = min(kAdjBatch, b1 - t0);
             wave_sync();
             {
-                // row rec = lane / 4 of the batch, quarter qq = lane % 4 of each row
-                const int rec = lane >> 2, qq = lane & 3;
-                const int rv = min(rec, cnt - 1);
-                const int e = SIDE ? a.r.tidx[t0 + rv] : t0 + rv;
                 const bool live = rec < cnt;
-                const float4 *src = reinterpret_cast<const float4 *>(a.due + size_t(e) * ldd + c0);
 #pragma unroll
-                for (int i = 0; i < NTC; ++i) {
-                    const int c4 = qq * NTC + i;
-                    *reinterpret_cast<float4 *>(dueL + rec * LDU + 4 * c4) =
-                        src[min(c4, 4 * ntv - 1)];
-                }
+                for (int i = 0; i < NTC; ++i)
+                    *reinterpret_cast<float4 *>(dueL + rec * LDU + 4 * (qq * NTC + i)) =
+                        make_float4(st.dv[4 * i], st.dv[4 * i + 1], st.dv[4 * i + 2],
+                                    st.dv[4 * i + 3]);
 #pragma unroll
                 for (int i = 0; i < 4 * MT; ++i) {
                     const int k = 4 * qq * MT + i;
-                    float y = a.harm[size_t(e) * NQ + min(k, NQ - 1)];
-                    y = k < NQ ? y : (k == NQ ? 1.0f : 0.0f);
+                    const float y = k < NQ ? st.yv[i] : (k == NQ ? 1.0f : 0.0f);
                     YL[rec * LDY + k] = live ? y : 0.0f;
                 }
-                for (int k = qq; k < NQ; k += 4) oldL[rec * LDO + k] = dyo[size_t(e) * NQ + k];
-                if (qq == 0) eL[rec] = e;
+#pragma unroll
+                for (int i = 0; i < KO; ++i)
+                    if (qq + 4 * i < NQ) oldL[rec * LDO + qq + 4 * i] = st.ov[i];
+                if (qq == 0) eL[rec] = e_cur;
             }
             wave_sync();
-            // four independent accumulation chains per tile keep the matrix pipe busy
-            floatx4 pc[4][MT];
+            if (t0 + kAdjBatch < b1) {
+                e_cur = e_nxt;
+                e_nxt = record_of(t0 + 2 * kAdjBatch);
+                st = adj_rows<NTC, 4 * MT, KO, NQ>(a.due + size_t(e_cur) * ldd + c0, 4 * ntv, qq,
+                                                   a.harm + size_t(e_cur) * NQ,
+                                                   dyo + size_t(e_cur) * NQ);
+            }
+            // two independent accumulation chains per tile
+            floatx4 pc[2][MT];
 #pragma unroll
-            for (int h = 0; h < 4; ++h)
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int nt = 0; nt < MT; ++nt) pc[h][nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -1000,35 +1053,32 @@ __global__ void __launch_bounds__(kBlock) k_eq_edge_adj(EqArgs a) {
                 for (int nt = 0; nt < MT; ++nt) {
                     pc[0][nt] = mfma4(av.x, Bq[t][nt][0], pc[0][nt]);
                     pc[1][nt] = mfma4(av.y, Bq[t][nt][1], pc[1][nt]);
-                    pc[2][nt] = mfma4(av.z, Bq[t][nt][2], pc[2][nt]);
-                    pc[3][nt] = mfma4(av.w, Bq[t][nt][3], pc[3][nt]);
+                    pc[0][nt] = mfma4(av.z, Bq[t][nt][2], pc[0][nt]);
+                    pc[1][nt] = mfma4(av.w, Bq[t][nt][3], pc[1][nt]);
                 }
             }
-            floatx4 p[MT];
-#pragma unroll
-            for (int nt = 0; nt < MT; ++nt) p[nt] = (pc[0][nt] + pc[1][nt]) + (pc[2][nt] + pc[3][nt]);
 #pragma unroll
             for (int s4 = 0; s4 < 4; ++s4) {
-                const int rec = 4 * s4 + g;
+                const int rr = 4 * s4 + g;
                 float ya[MT];
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) ya[mt] = YL[rec * LDY + 16 * mt + r];
+                for (int mt = 0; mt < MT; ++mt) ya[mt] = YL[rr * LDY + 16 * mt + r];
 #pragma unroll
                 for (int nt = 0; nt < NTC; ++nt) {
-                    const float b = dueL[rec * LDU + 16 * nt + r];
+                    const float b = dueL[rr * LDU + 16 * nt + r];
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma4(ya[mt], b, acc[mt][nt]);
                 }
             }
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int rec = 4 * g + v;
-                if (rec < cnt) {
-                    const size_t row = size_t(eL[rec]) * NQ;
+                const int rr = 4 * g + v;
+                if (rr < cnt) {
+                    const size_t row = size_t(eL[rr]) * NQ;
 #pragma unroll
                     for (int nt = 0; nt < MT; ++nt) {
                         const int k = 16 * nt + r;
-                        if (k < NQ) dyo[row + k] = oldL[rec * LDO + k] + p[nt][v];
+                        if (k < NQ) dyo[row + k] = oldL[rr * LDO + k] + (pc[0][nt][v] + pc[1][nt][v]);
                     }
                 }
             }
