@@ -115,29 +115,30 @@ def group_model(ev, prep, n_records, params):
     prep_bytes = E * (16 + 4 + 4 + 4 * ldrb + 4 + 4 + 16) + N * (16 + 4)
     direct = E * (16 + 16 + 16)
     rb_bwd = E * (4 + 16 + 4 * kb + 8)
-    if p["message_mode"] == "equivariant":
+    if p.get("message_mode", "scalar") == "equivariant":
         C, lq = p["equivariant_channels"], p["equivariant_l_max"]
         nq, LC = lq * (lq + 2), lq * p["equivariant_channels"]
-        CN, KX, NG = C * nq, kb + 2 * LC, G + 2 * LC
-        flops = B * 4 * E * D * (KX + NG)
-        prep_bytes += E * 4 * nq + E * 12            # harmonics out; transposed fc
+        CN, NG = C * nq, G + 2 * LC
+        # gate GEMM, its transpose (dE/du) and the radial-basis adjoint GEMM
+        flops = B * 2 * E * D * (2 * NG + kb)
+        prep_bytes += E * 4 * nq + E * 4 * ldrb + E * 12   # harmonics, rb derivative; fc gather
+        qbytes = N * 4 * nq * D                              # one side's per-atom factors
         per_block = (
-            # features: harm, rb, fc/tfc/tidx, ptr/tptr, dir_in in; x out
-            E * (4 * nq + 4 * kb + 12 + 4 * KX) + N * (8 + 4 * CN)
+            # neighbour pass: harm, rb, tidx/tfc/pair, tptr, B rows, dir_in in; ue, Qn out
+            E * (4 * nq + 4 * kb + 12) + N * (4 + 4 * D + 4 * CN) + E * 4 * D + qbytes
+            # centre pass: ue, harm, fc, ptr, A rows, dir_in in; ue, eh, Qc out
+            + E * (4 * D + 4 * nq + 4) + N * (4 + 4 * D + 4 * CN) + E * 8 * D + qbytes
             # aggregate: harm, mixed states, gates, values, dir_in, fc, nbr in; states, msg out
             + E * (4 * nq + 4 * NG + 8) + N * (4 * CN * 3 + 4 * H * 2 + 4 + 4 * (H + LC) + 16)
-            # pair_dir: dHt, mixed states, harm, direction gates, metadata, dE/dfc r/w; dg, dmix
-            + E * (4 * nq + 8 * 2 * LC + 12 + 8) + N * 4 * CN * 3
+            # pair_dir: dHt, mixed states, harm, direction gates, metadata, dE/dfc and
+            # dE/dY r/w; dg, dmix
+            + E * (4 * nq + 8 * 2 * LC + 12 + 8 + 8 * nq) + N * 4 * CN * 3
             # pair_grp: dmsg, values, group gates, metadata, dE/dfc r/w; dg, dV
             + E * (8 * G + 12 + 8) + N * 4 * H * 3
-            # rb reverse
-            + rb_bwd
-            # atom_dir: dir_in, dHt, ddir_in r/w; harm, probe adjoints, injection gates,
-            # metadata, dE/dY (two buffers) r/w
-            + N * 4 * CN * 4 + E * (4 * nq + 4 * 3 * LC + 12 + 16 * nq)
-            # atom_sums: dE/du rows, metadata; dA, dB out
-            + E * (4 * D + 12) + N * 8 * D)
-        once = prep_bytes + direct + E * (8 * nq + 16 + 8 + 12 + 32) + N * 16
+            # edge adjoints, both sides: dE/du, harm, dE/dY r/w, ids; Q in; dQ, dA | dB out
+            + 2 * (E * (4 * D + 4 * nq + 8 * nq + 4) + 2 * qbytes + N * 4 * D))
+        # harmonic reverse: vec, fc, dE/dY (two), dE/dfc, dE/drb, rb derivative, dv r/w
+        once = (prep_bytes + direct + E * (16 + 4 + 8 * nq + 4 + 8 * ldrb + 32) + N * 16)
     else:
         vc = p["vector_channels"]
         NP, NG = H + vc, G + vc

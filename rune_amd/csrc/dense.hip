@@ -180,7 +180,7 @@ __device__ inline void tile_epilogue(floatx4 (&acc)[WM][WN], float *smem, int M,
 // The k index l/16 of MFMA step s in half h is LDS column 16h + 4(l/16) + s, so
 // each lane fetches its four steps with one 16-byte LDS read.  Row stride
 // kLdk = 36 floats keeps those reads free of bank conflicts.
-// Block b covers row tile b / nbn and column tile b % nbn.
+// Tile t (the XCD-renumbered block) covers row tile t / nbn and column tile t % nbn.
 // Batched launches (gridDim.y > 1) offset A, C by z times their batch strides
 // and Bt by sb times z, or times L(z) - 1 (L the harmonic order of component z)
 // when the batches share one weight block per order.
@@ -207,7 +207,12 @@ __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *
     float *As = smem, *Bs = smem + kBM * kLdk;
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
-    const int m0 = (blockIdx.x / nbn) * kBM, n0 = (blockIdx.x % nbn) * BN;
+    // Blocks are dealt to the 8 XCDs round-robin; renumbering them so that each
+    // XCD runs one contiguous range of tiles keeps all column tiles of a row
+    // tile on one XCD, which then reads that A tile from HBM once.
+    const int nb = int(gridDim.x), hx = int(blockIdx.x) & 7, hk = int(blockIdx.x) >> 3;
+    const int tile = hx * (nb >> 3) + min(hx, nb & 7) + hk;
+    const int m0 = (tile / nbn) * kBM, n0 = (tile % nbn) * BN;
     const int wm = (wave / WNW) * 16 * WM, wn = (wave % WNW) * 16 * WN;
     const int g = lane >> 4, rr = lane & 15;
     floatx4 acc[WM][WN];
