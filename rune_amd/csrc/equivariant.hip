@@ -513,13 +513,15 @@ __global__ void __launch_bounds__(kBlock) k_eq_edge_centre(EqArgs a) {
 // update input [RMSNorm(msg) | per-(L, c) squared norms of dir_out].  The
 // neighbour rows (mixed state, values) are gathered for S records at a time.
 template <int LQ, int S>
-__global__ void __launch_bounds__(kBlock) k_eq_aggregate(EqArgs a) {
-    constexpr int NQ = LQ * (LQ + 2);
+__global__ void __launch_bounds__(kBlock, 2) k_eq_aggregate(EqArgs a) {
+    constexpr int NQ = LQ * (LQ + 2), LY = NQ + (NQ % 4 == 0 ? 4 : 1);
     using Ln = Lanes<S>;
     constexpr int HM = Ln::HM;
+    extern __shared__ float lds[];
     const int i = wave_atom(a.r);
     if (i < 0) return;
     const Ln ln(a.C);
+    float *Yc = lds + (threadIdx.x >> 6) * kWave * LY;
     const int H = a.H, G = a.G, C = a.C, CN = C * NQ, LC = LQ * C, NG = a.NG;
     const int gw = H / G;
     const int e_begin = a.r.view[4 * i], e_end = a.r.view[4 * i + 1];
@@ -530,19 +532,24 @@ __global__ void __launch_bounds__(kBlock) k_eq_aggregate(EqArgs a) {
         const int cnt = min(kWave, e_end - t0);
         int mj = 0;
         float mf = 0.0f;
+        wave_sync();
         if (ln.lane < cnt) {
             mj = a.r.nbr[t0 + ln.lane];
             mf = a.fc[t0 + ln.lane];
+            float y[NQ];
+            load_row(y, a.harm + size_t(t0 + ln.lane) * NQ);
+#pragma unroll
+            for (int k = 0; k < NQ; ++k) Yc[ln.lane * LY + k] = y[k];
         }
+        wave_sync();
         // every lane loads (clamped indices), so the compiler's waits stay exact
-        auto fetch = [&](int q, float (&y)[NQ], float (&mx)[NQ], float (&tt)[LQ],
-                         float (&ti)[LQ], float (&v)[HM], float (&g)[HM], float &f) {
+        auto fetch = [&](int q, float (&mx)[NQ], float (&tt)[LQ], float (&ti)[LQ],
+                         float (&v)[HM], float (&g)[HM], float &f) {
             const int qq = min(q, cnt - 1);
             const int j = bcast(mj, qq);
             const float fq = bcast(mf, qq);   // every lane joins the shuffle
             f = q < cnt ? fq : 0.0f;
             const int e = t0 + qq, cl = min(ln.c, C - 1);
-            load_row(y, a.harm + size_t(e) * NQ);
             load_row(mx, a.mixst + size_t(j) * CN + cl * NQ);
             const float *gd = a.ag + size_t(e) * NG + G + cl;
 #pragma unroll
@@ -559,13 +566,19 @@ __global__ void __launch_bounds__(kBlock) k_eq_aggregate(EqArgs a) {
                 g[u] = gr[h / gw];
             }
         };
-        float Y[NQ], M[NQ], tT[LQ], tI[LQ], V[HM], g[HM], fc;
-        fetch(ln.slot, Y, M, tT, tI, V, g, fc);
+        // two rounds of gathers in flight
+        float M[NQ], tT[LQ], tI[LQ], V[HM], g[HM], fc;
+        float M1[NQ], tT1[LQ], tI1[LQ], V1[HM], g1[HM], fc1;
+        fetch(ln.slot, M, tT, tI, V, g, fc);
+        fetch(ln.slot + S, M1, tT1, tI1, V1, g1, fc1);
         for (int q0 = 0; q0 < cnt; q0 += S) {
-            float Yn[NQ], Mn[NQ], tTn[LQ], tIn[LQ], Vn[HM], gn[HM], fcn;
-            fetch(q0 + S + ln.slot, Yn, Mn, tTn, tIn, Vn, gn, fcn);
+            float Mn[NQ], tTn[LQ], tIn[LQ], Vn[HM], gn[HM], fcn;
+            fetch(q0 + 2 * S + ln.slot, Mn, tTn, tIn, Vn, gn, fcn);
             if (fc != 0.0f) {
                 if (ln.act) {
+                    float Y[NQ];
+#pragma unroll
+                    for (int k = 0; k < NQ; ++k) Y[k] = Yc[(q0 + ln.slot) * LY + k];
 #pragma unroll
                     for (int L = 1; L <= LQ; ++L)
 #pragma unroll
@@ -577,13 +590,18 @@ __global__ void __launch_bounds__(kBlock) k_eq_aggregate(EqArgs a) {
 #pragma unroll
                 for (int u = 0; u < HM; ++u) macc[u] += g[u] * fc * V[u];
             }
-            copy(Y, Yn);
-            copy(M, Mn);
-            copy(tT, tTn);
-            copy(tI, tIn);
-            copy(V, Vn);
-            copy(g, gn);
-            fc = fcn;
+            copy(M, M1);
+            copy(tT, tT1);
+            copy(tI, tI1);
+            copy(V, V1);
+            copy(g, g1);
+            fc = fc1;
+            copy(M1, Mn);
+            copy(tT1, tTn);
+            copy(tI1, tIn);
+            copy(V1, Vn);
+            copy(g1, gn);
+            fc1 = fcn;
         }
     }
     fold_slots<S>(acc);
@@ -706,14 +724,17 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
                 ti[L] = gr[LC + L * C];
             }
         };
-        int e;
+        // two rounds of gathers in flight
+        int e, e1;
         float DH[NQ], tT[LQ], tI[LQ], yo[KQ], fc;
+        float DH1[NQ], tT1[LQ], tI1[LQ], yo1[KQ], fc1;
         fetch(ln.slot, e, DH, tT, tI, yo, fc);
+        fetch(ln.slot + S, e1, DH1, tT1, tI1, yo1, fc1);
         for (int q0 = 0; q0 < cnt; q0 += S) {
             const int q = q0 + ln.slot;
             int en;
             float DHn[NQ], tTn[LQ], tIn[LQ], yon[KQ], fcn;
-            fetch(q + S, en, DHn, tTn, tIn, yon, fcn);
+            fetch(q + 2 * S, en, DHn, tTn, tIn, yon, fcn);
             const bool on = fc != 0.0f;
             float contrib = 0.0f;
             if (e >= 0 && ln.act) {
@@ -765,12 +786,18 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
                 }
             }
             wave_sync();
-            e = en;
-            copy(DH, DHn);
-            copy(tT, tTn);
-            copy(tI, tIn);
-            copy(yo, yon);
-            fc = fcn;
+            e = e1;
+            copy(DH, DH1);
+            copy(tT, tT1);
+            copy(tI, tI1);
+            copy(yo, yo1);
+            fc = fc1;
+            e1 = en;
+            copy(DH1, DHn);
+            copy(tT1, tTn);
+            copy(tI1, tIn);
+            copy(yo1, yon);
+            fc1 = fcn;
         }
     }
     fold_slots<S>(acc);
@@ -1740,7 +1767,8 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
         }
         {
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
-            EQ_LAUNCH_S(k_eq_aggregate, lq, a.S, dim3(atom_grid), dim3(kBlock), 0, s, a);
+            EQ_LAUNCH_S(k_eq_aggregate, lq, a.S, dim3(atom_grid), dim3(kBlock),
+                        sizeof(float) * kBlock * (nq + (nq % 4 == 0 ? 4 : 1)), s, a);
         }
         const int NU = H + lq * C;
         Epilogue e3;
