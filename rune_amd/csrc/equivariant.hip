@@ -115,16 +115,31 @@ struct EqArgs {
     float *ddir_in;           // [N, C*nq]
 };
 
-__global__ void __launch_bounds__(kWave) k_eq_encode(int N, const float *s, int na, int nlm,
-                                                     const float *enc, const float *scale,
-                                                     int C, int nq, float *out) {
-    const int i = blockIdx.x, lane = threadIdx.x;
-    for (int o = lane; o < C * nq; o += kWave) {
-        int c = o / nq, k = o - c * nq, L = order_of(k);
-        const float *w = enc + size_t((L - 1) * C + c) * na;
-        float acc = 0.0f;
-        for (int n = 0; n < na; ++n) acc += w[n] * (s[size_t(i) * na * nlm + n * nlm + k] * scale[k]);
-        out[size_t(i) * C * nq + o] = acc;
+// Direction encoder: out[i, c, k] = sum_n enc[(L(k)-1) C + c][n] s[i, n, k] scale[k].
+// One atom per wave, four per block (blocks loop over atom groups); the
+// block stages the projection weights, each wave its atom's moment row.
+__global__ void __launch_bounds__(256) k_eq_encode(int N, const float *s, int na, int nlm,
+                                                   const float *enc, const float *scale, int lq,
+                                                   int C, int nq, int wrow, float *out) {
+    extern __shared__ float lds[];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kWave - 1);
+    float *W = lds;                                  // [lq C][na]
+    float *row = lds + lq * C * na + wave * wrow;    // [na][nlm]
+    for (int o = threadIdx.x; o < lq * C * na; o += blockDim.x) W[o] = enc[o];
+    __syncthreads();
+    for (int i0 = blockIdx.x * 4; i0 < N; i0 += gridDim.x * 4) {
+        const int i = i0 + wave;
+        if (i >= N) continue;
+        wave_sync();
+        for (int o = lane; o < na * nlm; o += kWave) row[o] = s[size_t(i) * na * nlm + o];
+        wave_sync();
+        for (int o = lane; o < C * nq; o += kWave) {
+            const int c = o / nq, k = o - c * nq, L = order_of(k);
+            const float *w = W + ((L - 1) * C + c) * na;
+            float acc = 0.0f;
+            for (int n = 0; n < na; ++n) acc += w[n] * (row[n * nlm + k] * scale[k]);
+            out[size_t(i) * C * nq + o] = acc;
+        }
     }
 }
 
@@ -218,32 +233,85 @@ __device__ inline void fold_slots(float (&v)[N]) {
 
 // out[n, c, k] = sum_c' W_L[c][c'] in[n, c', k] (trans = 0) or
 // sum_c' W_L[c'][c] in[n, c', k] (trans = 1), L the order of component k,
-// plus add[n, c, k] and add_t[n, k, c] when given.
-template <int LQ>
+// plus add[n, c, k] and add_t[n, k, c] when given.  One atom per wave (four
+// per block, blocks loop over atom groups).  Lane p owns channel
+// c = p % CM (CM = C rounded up to a power of two) and the orders
+// L = 1 + part + j * (64 / CM), part = p / CM; up to 32 channels it keeps the
+// rows W_L[c][:] of its orders in registers for the whole launch (beyond,
+// the block stages them in LDS) and reads the atom's input row, staged in
+// the wave's LDS, as broadcasts.
+template <int LQ, int CM>
 __global__ void __launch_bounds__(256) k_eq_mix(int N, const float *mixw, const float *in, int C,
                                                 int trans, const float *add, const float *add_t,
                                                 float *out) {
-    constexpr int NQ = LQ * (LQ + 2);
+    constexpr int NQ = LQ * (LQ + 2), PARTS = kWave / CM, NL = (LQ + PARTS - 1) / PARTS;
+    constexpr bool kRegW = CM <= 32;
     extern __shared__ float lds[];
-    const int CN = C * NQ, CC = C * C, LW = C + 1;
-    float *Wl = lds;                  // [LQ][c][c'] as applied, rows padded to C + 1
-    float *row = lds + LQ * C * LW;   // [C][NQ] input row of the current atom
-    for (int o = threadIdx.x; o < LQ * CC; o += blockDim.x) {
-        const int L = o / CC, r = o - L * CC, c = r / C, cc = r - c * C;
-        Wl[(L * C + c) * LW + cc] = trans ? mixw[size_t(L) * CC + cc * C + c] : mixw[o];
+    const int CN = C * NQ, CNP = (CN + 3) & ~3;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c = lane % CM, part = lane / CM;
+    float *Wl = lds + 4 * CNP;       // [LQ][c][c'] as applied (C > 32 only)
+    float *row = lds + wave * CNP;   // this wave's input row [C][NQ]
+    const bool act = c < C;
+    float W[kRegW ? NL : 1][kRegW ? CM : 1];
+    if constexpr (kRegW) {
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+            const int L = 1 + part + j * PARTS;
+#pragma unroll
+            for (int cc = 0; cc < CM; ++cc) {
+                float w = 0.0f;
+                if (act && L <= LQ && cc < C)
+                    w = trans ? mixw[size_t(L - 1) * C * C + size_t(cc) * C + c]
+                              : mixw[size_t(L - 1) * C * C + size_t(c) * C + cc];
+                W[j][cc] = w;
+            }
+        }
+    } else {
+        for (int o = threadIdx.x; o < LQ * C * C; o += blockDim.x) {
+            const int L = o / (C * C), r = o - L * C * C, ci = r / C, cc = r - ci * C;
+            Wl[o] = trans ? mixw[size_t(L) * C * C + size_t(cc) * C + ci] : mixw[o];
+        }
+        __syncthreads();
     }
-    for (int n = blockIdx.x; n < N; n += gridDim.x) {
-        __syncthreads();
-        for (int o = threadIdx.x; o < CN; o += blockDim.x) row[o] = in[size_t(n) * CN + o];
-        __syncthreads();
-        for (int o = threadIdx.x; o < CN; o += blockDim.x) {
-            const int c = o / NQ, k = o - c * NQ;
-            const float *w = Wl + size_t((order_of(k) - 1) * C + c) * LW;
-            float acc = 0.0f;
-            for (int cc = 0; cc < C; ++cc) acc += w[cc] * row[cc * NQ + k];
-            if (add) acc += add[size_t(n) * CN + o];
-            if (add_t) acc += add_t[size_t(n) * CN + k * C + c];
-            out[size_t(n) * CN + o] = acc;
+    for (int n0 = blockIdx.x * 4; n0 < N; n0 += gridDim.x * 4) {
+        const int n = n0 + wave;
+        if (n >= N) continue;
+        wave_sync();
+        for (int o = lane; o < CN; o += kWave) row[o] = in[size_t(n) * CN + o];
+        wave_sync();
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+            const int L = 1 + part + j * PARTS;
+            if (!act || L > LQ) continue;
+            const int st = L * L - 1;
+            float acc[2 * LQ + 1];
+#pragma unroll
+            for (int m = 0; m < 2 * LQ + 1; ++m) acc[m] = 0.0f;
+#pragma unroll
+            for (int cc = 0; cc < CM; ++cc) {
+                if (cc < C) {
+                    const float *x = row + cc * NQ + st;
+                    float wv;
+                    if constexpr (kRegW)
+                        wv = W[j][cc];
+                    else
+                        wv = Wl[(size_t(L - 1) * C + c) * C + cc];
+#pragma unroll
+                    for (int m = 0; m < 2 * LQ + 1; ++m)
+                        if (m < 2 * L + 1) acc[m] += wv * x[m];
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < 2 * LQ + 1; ++m) {
+                if (m < 2 * L + 1) {
+                    const int k = st + m;
+                    float v = acc[m];
+                    if (add) v += add[size_t(n) * CN + c * NQ + k];
+                    if (add_t) v += add_t[size_t(n) * CN + k * C + c];
+                    out[size_t(n) * CN + c * NQ + k] = v;
+                }
+            }
         }
     }
 }
@@ -1134,22 +1202,36 @@ __global__ void k_gather_f(int64_t E, const int32_t *idx, const float *src, floa
     if (t < E) dst[t] = src[idx[t]];
 }
 
-__global__ void __launch_bounds__(kWave) k_eq_encoder_backward(const float *ddir0,
-                                                               const float *enc,
-                                                               const float *scale, int C,
-                                                               int nq, int na, int nlm,
-                                                               float *dmom) {
-    const int i = blockIdx.x, lane = threadIdx.x;
-    for (int o = lane; o < na * nlm; o += kWave) {
-        int n = o / nlm, k = o - n * nlm;
-        float g = 0.0f;
-        if (k < nq) {
-            int L = order_of(k);
-            for (int c = 0; c < C; ++c)
-                g += enc[size_t((L - 1) * C + c) * na + n] * ddir0[size_t(i) * C * nq + c * nq + k];
-            g *= scale[k];
+// Reverse of the direction encoder: dE/ds[i, n, k] = scale[k] sum_c
+// enc[(L(k)-1) C + c][n] dE/dout[i, c, k] (zero for k >= nq).  Same layout as
+// k_eq_encode.
+__global__ void __launch_bounds__(256) k_eq_encoder_backward(int N, const float *ddir0,
+                                                            const float *enc,
+                                                            const float *scale, int lq, int C,
+                                                            int nq, int na, int nlm, int wrow,
+                                                            float *dmom) {
+    extern __shared__ float lds[];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kWave - 1);
+    float *W = lds;                                  // [lq C][na]
+    float *row = lds + lq * C * na + wave * wrow;    // [C][nq]
+    for (int o = threadIdx.x; o < lq * C * na; o += blockDim.x) W[o] = enc[o];
+    __syncthreads();
+    for (int i0 = blockIdx.x * 4; i0 < N; i0 += gridDim.x * 4) {
+        const int i = i0 + wave;
+        if (i >= N) continue;
+        wave_sync();
+        for (int o = lane; o < C * nq; o += kWave) row[o] = ddir0[size_t(i) * C * nq + o];
+        wave_sync();
+        for (int o = lane; o < na * nlm; o += kWave) {
+            const int n = o / nlm, k = o - n * nlm;
+            float g = 0.0f;
+            if (k < nq) {
+                const int L = order_of(k);
+                for (int c = 0; c < C; ++c) g += W[((L - 1) * C + c) * na + n] * row[c * nq + k];
+                g *= scale[k];
+            }
+            dmom[size_t(i) * na * nlm + o] = g;
         }
-        dmom[size_t(i) * na * nlm + o] = g;
     }
 }
 
@@ -1379,6 +1461,46 @@ static int adj_ntc(int lq, int ldd) {
         }                                                                                 \
         RUNE_HIP_CHECK(hipGetLastError());                                                \
     } while (0)
+
+// Channel mixing per order (k_eq_mix).
+template <int LQ>
+static void launch_mix_lq(int C, int N, const float *w, const float *in, int trans,
+                          const float *add, const float *add_t, float *out, hipStream_t s) {
+    constexpr int NQ = LQ * (LQ + 2);
+    const int grid = std::max(1, std::min(ceil_div(N, 4), 4096));
+    const size_t lds = sizeof(float) * (4 * ((size_t(C) * NQ + 3) & ~size_t(3)) +
+                                        (C > 32 ? size_t(LQ) * C * C : 0));
+    if (C <= 4)
+        hipLaunchKernelGGL((k_eq_mix<LQ, 4>), dim3(grid), dim3(256), lds, s, N, w, in, C, trans, add, add_t, out);
+    else if (C <= 8)
+        hipLaunchKernelGGL((k_eq_mix<LQ, 8>), dim3(grid), dim3(256), lds, s, N, w, in, C, trans, add, add_t, out);
+    else if (C <= 16)
+        hipLaunchKernelGGL((k_eq_mix<LQ, 16>), dim3(grid), dim3(256), lds, s, N, w, in, C, trans, add, add_t, out);
+    else if (C <= 32)
+        hipLaunchKernelGGL((k_eq_mix<LQ, 32>), dim3(grid), dim3(256), lds, s, N, w, in, C, trans, add, add_t, out);
+    else {
+        if (lds > 65536)
+            RUNE_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_eq_mix<LQ, 64>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               int(lds)));
+        hipLaunchKernelGGL((k_eq_mix<LQ, 64>), dim3(grid), dim3(256), lds, s, N, w, in, C, trans, add, add_t, out);
+    }
+    RUNE_HIP_CHECK(hipGetLastError());
+}
+
+static void launch_mix(int lq, int C, int N, const float *w, const float *in, int trans,
+                       const float *add, const float *add_t, float *out, hipStream_t s) {
+    if (N == 0) return;
+    switch (lq) {
+    case 1: launch_mix_lq<1>(C, N, w, in, trans, add, add_t, out, s); break;
+    case 2: launch_mix_lq<2>(C, N, w, in, trans, add, add_t, out, s); break;
+    case 3: launch_mix_lq<3>(C, N, w, in, trans, add, add_t, out, s); break;
+    case 4: launch_mix_lq<4>(C, N, w, in, trans, add, add_t, out, s); break;
+    case 5: launch_mix_lq<5>(C, N, w, in, trans, add, add_t, out, s); break;
+    case 6: launch_mix_lq<6>(C, N, w, in, trans, add, add_t, out, s); break;
+    default: launch_mix_lq<7>(C, N, w, in, trans, add, add_t, out, s); break;
+    }
+}
 
 void validate_equivariant(ModelImpl &m) {
     const rune_model_config &c = m.cfg;
@@ -1711,8 +1833,7 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
     const int N = p.N, H = c.hidden_dim, D = c.message_dim, act = c.activation;
     const int lq = c.equivariant_l_max, C = c.equivariant_channels, nq = lq * (lq + 2);
     const int64_t E = p.E;
-    const int atom_grid = ceil_div(N, kWaves), mix_grid = std::max(1, std::min(N, 2048));
-    const size_t mix_lds = sizeof(float) * (size_t(lq) * C * (C + 1) + size_t(C) * nq);
+    const int atom_grid = ceil_div(N, kWaves), mix_grid = std::max(1, std::min(ceil_div(N, 4), 4096));
     {
         Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
         edge_prep(m, p, r, types, s, p.at(p.i_harm), m.harm_scale, lq, nq);
@@ -1727,8 +1848,13 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dharm_n), 0, 4 * size_t(E) * nq, s));
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dfc), 0, 4 * size_t(E), s));
     }
-    hipLaunchKernelGGL(k_eq_encode, dim3(N), dim3(kWave), 0, s, N, moments, m.desc.na,
-                       m.desc.nlm, m.enc_w, m.harm_scale, C, nq, p.at(p.blocks[0].dir_in));
+    {
+        const int wrow = (std::max(m.desc.na * m.desc.nlm, C * nq) + 3) & ~3;
+        const size_t lds = sizeof(float) * (size_t(lq) * C * m.desc.na + 4 * size_t(wrow));
+        hipLaunchKernelGGL(k_eq_encode, dim3(mix_grid), dim3(256), lds, s, N, moments, m.desc.na,
+                           m.desc.nlm, m.enc_w, m.harm_scale, lq, C, nq, wrow,
+                           p.at(p.blocks[0].dir_in));
+    }
     RUNE_HIP_CHECK(hipGetLastError());
     const float *cur = h;
     for (int b = 0; b < c.message_layers; ++b) {
@@ -1739,8 +1865,7 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
         Epilogue e0;
         e0.row_scale = p.at(bb.rin);
         gemm(N, w.NP, H, cur, H, w.node_f, H, p.at(bb.vs), w.NP, e0, s);
-        EQ_LAUNCH(k_eq_mix, lq, dim3(mix_grid), dim3(256), mix_lds, s, N, w.mix,
-                  p.at(bb.dir_in), C, 0, nullptr, nullptr, p.at(bb.mixstate));
+        launch_mix(lq, C, N, w.mix, p.at(bb.dir_in), 0, nullptr, nullptr, p.at(bb.mixstate), s);
         if (E > 0) {
             const int dmc = edge_dmc(lq, D), cn4 = (C * nq + 3) & ~3;
             const int ly = nq + (nq % 4 == 0 ? 4 : 1);
@@ -1799,8 +1924,7 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
     const int lq = c.equivariant_l_max, C = c.equivariant_channels, nq = lq * (lq + 2);
     const int NU = H + lq * C, kb = c.message_basis_size, ldd = p.ld_edge;
     const int64_t E = p.E;
-    const int atom_grid = ceil_div(N, kWaves), mix_grid = std::max(1, std::min(N, 2048));
-    const size_t mix_lds = sizeof(float) * (size_t(lq) * C * (C + 1) + size_t(C) * nq);
+    const int atom_grid = ceil_div(N, kWaves), mix_grid = std::max(1, std::min(ceil_div(N, 4), 4096));
     const int ly = nq + (nq % 4 == 0 ? 4 : 1);
     const int ntc = adj_ntc(lq, ldd), mt = (nq + 16) / 16;
     // per-wave LDS of the reverse edge-MLP kernels: due, harmonic and old dE/dY
@@ -1876,8 +2000,7 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
                          p.at(p.t_dhk), nq * C, s);
         }
         // dE/d(dir_in) = M^T dmix + dE/d(dir_out) + the factor adjoints
-        EQ_LAUNCH(k_eq_mix, lq, dim3(mix_grid), dim3(256), mix_lds, s, N, w.mix, a.dmix, C, 1,
-                  p.at(p.t_dvsum), p.at(p.t_dhk), a.ddir_in);
+        launch_mix(lq, C, N, w.mix, a.dmix, 1, p.at(p.t_dvsum), p.at(p.t_dhk), a.ddir_in, s);
         Epilogue e4;
         gemm(N, H, w.NP, p.at(p.t_dvs), w.NP, w.node_fT, w.NP, p.at(p.t_dz), H, e4, s);
         float *next = (cur == p.at(p.t_dh0)) ? p.at(p.t_dh1) : p.at(p.t_dh0);
@@ -1887,8 +2010,12 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         ddir_in = (ddir_in == p.at(p.t_ddir0)) ? p.at(p.t_ddir1) : p.at(p.t_ddir0);
     }
     // ddir_out now holds dE/d(encoder output)
-    hipLaunchKernelGGL(k_eq_encoder_backward, dim3(N), dim3(kWave), 0, s, ddir_out, m.enc_w,
-                       m.harm_scale, C, nq, m.desc.na, m.desc.nlm, p.dmom);
+    {
+        const int wrow = (std::max(m.desc.na * m.desc.nlm, C * nq) + 3) & ~3;
+        const size_t lds = sizeof(float) * (size_t(lq) * C * m.desc.na + 4 * size_t(wrow));
+        hipLaunchKernelGGL(k_eq_encoder_backward, dim3(mix_grid), dim3(256), lds, s, N, ddir_out,
+                           m.enc_w, m.harm_scale, lq, C, nq, m.desc.na, m.desc.nlm, wrow, p.dmom);
+    }
     if (E > 0) {
         EdgeZ zo;
         for (int k = 0; k < kMaxL + 2; ++k) zo.off[k] = m.desc.z_off[k];
