@@ -65,6 +65,27 @@ __device__ inline void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ inline floatx4 mfma4(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Copies n floats from global memory into this wave's LDS with up to eight
+// loads per lane in flight (a plain strided loop would wait for each load
+// before its LDS store and issue the next).
+__device__ inline void stage_row(float *dst, const float *__restrict__ src, int n) {
+    const int lane = threadIdx.x & (kWave - 1);
+    for (int o = lane; o < n; o += 8 * kWave) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = src[min(o + u * kWave, n - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (o + u * kWave < n) dst[o + u * kWave] = v[u];
+    }
+}
+
 __device__ __host__ inline int order_of(int k) {
     int L = 1;
     while ((L + 1) * (L + 1) - 1 <= k) ++L;
@@ -131,7 +152,7 @@ __global__ void __launch_bounds__(256) k_eq_encode(int N, const float *s, int na
         const int i = i0 + wave;
         if (i >= N) continue;
         wave_sync();
-        for (int o = lane; o < na * nlm; o += kWave) row[o] = s[size_t(i) * na * nlm + o];
+        stage_row(row, s + size_t(i) * na * nlm, na * nlm);
         wave_sync();
         for (int o = lane; o < C * nq; o += kWave) {
             const int c = o / nq, k = o - c * nq, L = order_of(k);
@@ -234,43 +255,42 @@ __device__ inline void fold_slots(float (&v)[N]) {
 // out[n, c, k] = sum_c' W_L[c][c'] in[n, c', k] (trans = 0) or
 // sum_c' W_L[c'][c] in[n, c', k] (trans = 1), L the order of component k,
 // plus add[n, c, k] and add_t[n, k, c] when given.  One atom per wave (four
-// per block, blocks loop over atom groups).  Lane p owns channel
-// c = p % CM (CM = C rounded up to a power of two) and the orders
-// L = 1 + part + j * (64 / CM), part = p / CM; up to 32 channels it keeps the
-// rows W_L[c][:] of its orders in registers for the whole launch (beyond,
-// the block stages them in LDS) and reads the atom's input row, staged in
-// the wave's LDS, as broadcasts.
-template <int LQ, int CM>
+// per block, blocks loop over atom groups), on the matrix cores: for each
+// order, out_L [C, 2L+1] = W_L [C, C] x in_L [C, 2L+1] as 16 x 16 tiles
+// (channels padded to 16 MT, components to 16).  The W_L fragments stay in
+// registers for the whole launch when they fit (MT <= 2), else the block
+// stages them in LDS; the atom's input row is staged in the wave's LDS.
+// MFMA operand layout as in k_eq_edge_adj: lane l supplies A[l%16][l/16] and
+// B[l/16][l%16]; accumulator v of lane l is C[4(l/16) + v][l%16].
+template <int LQ, int MT>
 __global__ void __launch_bounds__(256) k_eq_mix(int N, const float *mixw, const float *in, int C,
                                                 int trans, const float *add, const float *add_t,
                                                 float *out) {
-    constexpr int NQ = LQ * (LQ + 2), PARTS = kWave / CM, NL = (LQ + PARTS - 1) / PARTS;
-    constexpr bool kRegW = CM <= 32;
+    constexpr int NQ = LQ * (LQ + 2), KS = 4 * MT;   // k-steps over the padded channels
+    constexpr bool kRegW = MT <= 2;
     extern __shared__ float lds[];
-    const int CN = C * NQ, CNP = (CN + 3) & ~3;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int c = lane % CM, part = lane / CM;
-    float *Wl = lds + 4 * CNP;       // [LQ][c][c'] as applied (C > 32 only)
-    float *row = lds + wave * CNP;   // this wave's input row [C][NQ]
-    const bool act = c < C;
-    float W[kRegW ? NL : 1][kRegW ? CM : 1];
+    const int CN = C * NQ, CNP = (CN + 3) & ~3, CP = 16 * MT;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, r = lane & 15;
+    float *row = lds + wave * 2 * CNP;               // this wave's input row [C][NQ]
+    float *res = row + CNP;                          // and its result row [C][NQ]
+    float *Wl = lds + 8 * CNP;                       // [LQ][CP][CP] as applied (MT > 2)
+    auto wval = [&](int L, int c, int cc) {          // W_L[c][cc] as applied, 0 in the padding
+        if (c >= C || cc >= C) return 0.0f;
+        return trans ? mixw[size_t(L - 1) * C * C + size_t(cc) * C + c]
+                     : mixw[size_t(L - 1) * C * C + size_t(c) * C + cc];
+    };
+    float Wr[kRegW ? LQ : 1][kRegW ? MT : 1][kRegW ? KS : 1];
     if constexpr (kRegW) {
 #pragma unroll
-        for (int j = 0; j < NL; ++j) {
-            const int L = 1 + part + j * PARTS;
+        for (int L = 1; L <= LQ; ++L)
 #pragma unroll
-            for (int cc = 0; cc < CM; ++cc) {
-                float w = 0.0f;
-                if (act && L <= LQ && cc < C)
-                    w = trans ? mixw[size_t(L - 1) * C * C + size_t(cc) * C + c]
-                              : mixw[size_t(L - 1) * C * C + size_t(c) * C + cc];
-                W[j][cc] = w;
-            }
-        }
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int s4 = 0; s4 < KS; ++s4) Wr[L - 1][mt][s4] = wval(L, 16 * mt + r, 4 * s4 + g);
     } else {
-        for (int o = threadIdx.x; o < LQ * C * C; o += blockDim.x) {
-            const int L = o / (C * C), r = o - L * C * C, ci = r / C, cc = r - ci * C;
-            Wl[o] = trans ? mixw[size_t(L) * C * C + size_t(cc) * C + ci] : mixw[o];
+        for (int o = threadIdx.x; o < LQ * CP * CP; o += blockDim.x) {
+            const int L = o / (CP * CP), q = o - L * CP * CP, c = q / CP, cc = q - c * CP;
+            Wl[o] = wval(L + 1, c, cc);
         }
         __syncthreads();
     }
@@ -278,41 +298,63 @@ __global__ void __launch_bounds__(256) k_eq_mix(int N, const float *mixw, const 
         const int n = n0 + wave;
         if (n >= N) continue;
         wave_sync();
-        for (int o = lane; o < CN; o += kWave) row[o] = in[size_t(n) * CN + o];
+        // rows move between HBM and LDS contiguously; add_t is transposed in LDS
+        stage_row(row, in + size_t(n) * CN, CN);
+        if (add) {
+            stage_row(res, add + size_t(n) * CN, CN);
+        } else {
+            for (int o = lane; o < CN; o += kWave) res[o] = 0.0f;
+        }
         wave_sync();
+        if (add_t) {
+            for (int o = lane; o < CN; o += 4 * kWave) {
+                float v[4];
 #pragma unroll
-        for (int j = 0; j < NL; ++j) {
-            const int L = 1 + part + j * PARTS;
-            if (!act || L > LQ) continue;
-            const int st = L * L - 1;
-            float acc[2 * LQ + 1];
+                for (int u = 0; u < 4; ++u) v[u] = add_t[size_t(n) * CN + min(o + u * kWave, CN - 1)];
 #pragma unroll
-            for (int m = 0; m < 2 * LQ + 1; ++m) acc[m] = 0.0f;
-#pragma unroll
-            for (int cc = 0; cc < CM; ++cc) {
-                if (cc < C) {
-                    const float *x = row + cc * NQ + st;
-                    float wv;
-                    if constexpr (kRegW)
-                        wv = W[j][cc];
-                    else
-                        wv = Wl[(size_t(L - 1) * C + c) * C + cc];
-#pragma unroll
-                    for (int m = 0; m < 2 * LQ + 1; ++m)
-                        if (m < 2 * L + 1) acc[m] += wv * x[m];
+                for (int u = 0; u < 4; ++u) {
+                    const int q = o + u * kWave;
+                    if (q < CN) {
+                        const int k = q / C, c = q - k * C;
+                        res[c * NQ + k] += v[u];
+                    }
                 }
             }
+            wave_sync();
+        }
 #pragma unroll
-            for (int m = 0; m < 2 * LQ + 1; ++m) {
-                if (m < 2 * L + 1) {
-                    const int k = st + m;
-                    float v = acc[m];
-                    if (add) v += add[size_t(n) * CN + c * NQ + k];
-                    if (add_t) v += add_t[size_t(n) * CN + k * C + c];
-                    out[size_t(n) * CN + c * NQ + k] = v;
+        for (int L = 1; L <= LQ; ++L) {
+            const int st = L * L - 1, w = 2 * L + 1;
+            floatx4 acc[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s4 = 0; s4 < KS; ++s4) {
+                const int cc = 4 * s4 + g;
+                const float b = (cc < C && r < w) ? row[cc * NQ + st + min(r, w - 1)] : 0.0f;
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    float av;
+                    if constexpr (kRegW)
+                        av = Wr[L - 1][mt][s4];
+                    else
+                        av = Wl[(size_t(L - 1) * CP + 16 * mt + r) * CP + 4 * s4 + g];
+                    acc[mt] = mfma4(av, b, acc[mt]);
                 }
+            }
+            if (r < w) {
+                const int k = st + r;
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int c = 16 * mt + 4 * g + v;
+                        if (c < C) res[c * NQ + k] = acc[mt][v] + res[c * NQ + k];
+                    }
             }
         }
+        wave_sync();
+        for (int o = lane; o < CN; o += kWave) out[size_t(n) * CN + o] = res[o];
     }
 }
 
@@ -406,8 +448,7 @@ __device__ inline void store_factor(const float (&Q)[LQ * (LQ + 2)][DMC], float 
 }
 
 __device__ inline void stage_state(float *Hs, const float *__restrict__ row, int CN) {
-    const int lane = threadIdx.x & (kWave - 1);
-    for (int o = lane; o < CN; o += kWave) Hs[o] = row[o];
+    stage_row(Hs, row, CN);
     wave_sync();
 }
 
@@ -714,11 +755,14 @@ __global__ void __launch_bounds__(kWave) k_eq_node_backward(EqArgs a) {
     const float *d = a.duin + size_t(i) * ldu;
     const float *m = a.msg + size_t(i) * H;
     float dot = 0.0f;
+#pragma unroll 4
     for (int c = lane; c < H; c += kWave) dot += d[c] * m[c];
     dot = wave_sum(dot);
     float r = a.rm[i];
     float coef = r * r * r * dot / float(H);
+#pragma unroll 4
     for (int c = lane; c < H; c += kWave) a.dmsg[size_t(i) * H + c] = r * d[c] - coef * m[c];
+#pragma unroll 4
     for (int o = lane; o < CN; o += kWave) {
         int c = o / nq, k = o - c * nq, L = order_of(k);
         float g = a.ddir_out ? a.ddir_out[size_t(i) * CN + o] : 0.0f;
@@ -997,12 +1041,6 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_grp(EqArgs a) {
     }
 }
 
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-
-__device__ inline floatx4 mfma4(float a, float b, floatx4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
 // Records per matrix-core batch of the edge-MLP reverse kernels.
 constexpr int kAdjBatch = 16;
 
@@ -1220,7 +1258,7 @@ __global__ void __launch_bounds__(256) k_eq_encoder_backward(int N, const float 
         const int i = i0 + wave;
         if (i >= N) continue;
         wave_sync();
-        for (int o = lane; o < C * nq; o += kWave) row[o] = ddir0[size_t(i) * C * nq + o];
+        stage_row(row, ddir0 + size_t(i) * C * nq, C * nq);
         wave_sync();
         for (int o = lane; o < na * nlm; o += kWave) {
             const int n = o / nlm, k = o - n * nlm;
@@ -1468,22 +1506,20 @@ static void launch_mix_lq(int C, int N, const float *w, const float *in, int tra
                           const float *add, const float *add_t, float *out, hipStream_t s) {
     constexpr int NQ = LQ * (LQ + 2);
     const int grid = std::max(1, std::min(ceil_div(N, 4), 4096));
-    const size_t lds = sizeof(float) * (4 * ((size_t(C) * NQ + 3) & ~size_t(3)) +
-                                        (C > 32 ? size_t(LQ) * C * C : 0));
-    if (C <= 4)
-        hipLaunchKernelGGL((k_eq_mix<LQ, 4>), dim3(grid), dim3(256), lds, s, N, w, in, C, trans, add, add_t, out);
-    else if (C <= 8)
-        hipLaunchKernelGGL((k_eq_mix<LQ, 8>), dim3(grid), dim3(256), lds, s, N, w, in, C, trans, add, add_t, out);
-    else if (C <= 16)
-        hipLaunchKernelGGL((k_eq_mix<LQ, 16>), dim3(grid), dim3(256), lds, s, N, w, in, C, trans, add, add_t, out);
-    else if (C <= 32)
-        hipLaunchKernelGGL((k_eq_mix<LQ, 32>), dim3(grid), dim3(256), lds, s, N, w, in, C, trans, add, add_t, out);
-    else {
+    const int mt = ceil_div(C, 16), cp = 16 * mt;
+    const size_t lds = sizeof(float) * (8 * ((size_t(C) * NQ + 3) & ~size_t(3)) +
+                                        (mt > 2 ? size_t(LQ) * cp * cp : 0));
+    switch (mt) {
+    case 1: hipLaunchKernelGGL((k_eq_mix<LQ, 1>), dim3(grid), dim3(256), lds, s, N, w, in, C, trans, add, add_t, out); break;
+    case 2: hipLaunchKernelGGL((k_eq_mix<LQ, 2>), dim3(grid), dim3(256), lds, s, N, w, in, C, trans, add, add_t, out); break;
+    case 3: hipLaunchKernelGGL((k_eq_mix<LQ, 3>), dim3(grid), dim3(256), lds, s, N, w, in, C, trans, add, add_t, out); break;
+    default:
         if (lds > 65536)
-            RUNE_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_eq_mix<LQ, 64>),
+            RUNE_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_eq_mix<LQ, 4>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                                int(lds)));
-        hipLaunchKernelGGL((k_eq_mix<LQ, 64>), dim3(grid), dim3(256), lds, s, N, w, in, C, trans, add, add_t, out);
+        hipLaunchKernelGGL((k_eq_mix<LQ, 4>), dim3(grid), dim3(256), lds, s, N, w, in, C, trans, add, add_t, out);
+        break;
     }
     RUNE_HIP_CHECK(hipGetLastError());
 }
