@@ -20,6 +20,7 @@ namespace rune {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kWave = 64;
 
 struct Geo {
     double cell[9];     // rows = lattice vectors
@@ -127,32 +128,45 @@ __device__ inline uint64_t make_key(int cls, int j, const int *S) {
     return k;
 }
 
+// Candidate enumeration, one atom per wave: the 64 lanes test the candidates
+// of a stencil cell (bins within the stencil reach, periodic images by
+// wrapping) in parallel with the exact fp64 test, and ballots count the
+// members (pass 1: union, radial and angular counts) and give each passing
+// candidate its slot (pass 2), so the fill pass writes the keys of a centre in
+// candidate order; the centre's keys (at most kWaveKeys) are then sorted in
+// LDS by rank (each key's rank is the number of smaller keys; keys of one
+// centre are distinct).  Centres with more keys fall back to lane 0's
+// insertion sort in global memory.
+constexpr int kWaveKeys = 1024;
+
 template <bool kFill>
-__global__ void enumerate_edges(int n, const double *pos, const int32_t *sptr, int nstruct,
-                                const Geo *geo, const int32_t *atom_wrap,
-                                const int32_t *atom_cell, const int32_t *bin_start,
-                                const int32_t *bin_atoms, double rc2_r, double rc2_a,
-                                double rc2_max, int cls1_radial, int max_r, int max_a,
-                                int32_t *cnt_union, int32_t *cnt_r, int32_t *cnt_a,
-                                int32_t *error_flag, const int32_t *ptr, uint64_t *keys) {
-    int i = blockIdx.x * blockDim.x + threadIdx.x;
+__global__ void __launch_bounds__(256) enumerate_wave(
+    int n, const double *pos, const int32_t *sptr, int nstruct, const Geo *geo,
+    const int32_t *atom_wrap, const int32_t *atom_cell, const int32_t *bin_start,
+    const int32_t *bin_atoms, double rc2_r, double rc2_a, double rc2_max, int max_r, int max_a,
+    int32_t *cnt_union, int32_t *cnt_r, int32_t *cnt_a, int32_t *error_flag, const int32_t *ptr,
+    uint64_t *keys) {
+    __shared__ uint64_t kl[4][kFill ? kWaveKeys : 1];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int i = blockIdx.x * 4 + wave;
     if (i >= n) return;
-    int s = find_structure(sptr, nstruct, i);
+    const int s = find_structure(sptr, nstruct, i);
     const Geo &g = geo[s];
-    int wi[3] = {atom_wrap[3 * i], atom_wrap[3 * i + 1], atom_wrap[3 * i + 2]};
-    int ci[3] = {atom_cell[3 * i], atom_cell[3 * i + 1], atom_cell[3 * i + 2]};
+    const int wi[3] = {atom_wrap[3 * i], atom_wrap[3 * i + 1], atom_wrap[3 * i + 2]};
+    const int ci[3] = {atom_cell[3 * i], atom_cell[3 * i + 1], atom_cell[3 * i + 2]};
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     int cu = 0, cr = 0, ca = 0;
-    int base = kFill ? ptr[i] : 0;
+    const int base = kFill ? ptr[i] : 0;
     for (int dx = -g.m[0]; dx <= g.m[0]; ++dx) {
         for (int dy = -g.m[1]; dy <= g.m[1]; ++dy) {
             for (int dz = -g.m[2]; dz <= g.m[2]; ++dz) {
-                int dd[3] = {dx, dy, dz};
+                const int dd[3] = {dx, dy, dz};
                 int T[3], bb[3];
                 bool ok = true;
                 for (int d = 0; d < 3; ++d) {
-                    int b = ci[d] + dd[d];
+                    const int b = ci[d] + dd[d];
                     if (g.pbc[d]) {
-                        int t = (b >= 0) ? b / g.nb[d] : -((-b + g.nb[d] - 1) / g.nb[d]);
+                        const int t = (b >= 0) ? b / g.nb[d] : -((-b + g.nb[d] - 1) / g.nb[d]);
                         T[d] = t;
                         bb[d] = b - t * g.nb[d];
                     } else {
@@ -162,41 +176,64 @@ __global__ void enumerate_edges(int n, const double *pos, const int32_t *sptr, i
                     }
                 }
                 if (!ok) continue;
-                int flat = g.bin_offset + (bb[0] * g.nb[1] + bb[1]) * g.nb[2] + bb[2];
-                int beg = bin_start[flat], end = bin_start[flat + 1];
-                for (int q = beg; q < end; ++q) {
-                    int j = bin_atoms[q];
-                    int S[3];
-                    for (int d = 0; d < 3; ++d)
-                        S[d] = g.pbc[d] ? (T[d] - atom_wrap[3 * j + d] + wi[d]) : 0;
-                    if (j == i && S[0] == 0 && S[1] == 0 && S[2] == 0) continue;
-                    double v[3];
-                    double r2 = pair_d2(pos, g, i, j, S, v);
-                    if (!(r2 < rc2_max)) continue;
-                    bool in_r = r2 < rc2_r, in_a = r2 < rc2_a;
-                    if (kFill) {
-                        // class 0: inside the smaller cutoff (both lists)
-                        int cls = (in_r && in_a) ? 0 : 1;
-                        keys[base + cu] = make_key(cls, j, S);
+                const int flat = g.bin_offset + (bb[0] * g.nb[1] + bb[1]) * g.nb[2] + bb[2];
+                const int beg = bin_start[flat], end = bin_start[flat + 1];
+                for (int q0 = beg; q0 < end; q0 += kWave) {
+                    const int q = q0 + lane;
+                    bool pass = false, in_r = false, in_a = false;
+                    int j = 0, S[3] = {0, 0, 0};
+                    if (q < end) {
+                        j = bin_atoms[q];
+                        for (int d = 0; d < 3; ++d)
+                            S[d] = g.pbc[d] ? (T[d] - atom_wrap[3 * j + d] + wi[d]) : 0;
+                        if (!(j == i && S[0] == 0 && S[1] == 0 && S[2] == 0)) {
+                            double v[3];
+                            const double r2 = pair_d2(pos, g, i, j, S, v);
+                            pass = r2 < rc2_max;
+                            in_r = r2 < rc2_r;
+                            in_a = r2 < rc2_a;
+                        }
                     }
-                    ++cu;
-                    cr += in_r;
-                    ca += in_a;
+                    const uint64_t bp = __ballot(pass);
+                    if (kFill && pass) {
+                        const int slot = cu + __popcll(bp & below);
+                        const uint64_t key = make_key((in_r && in_a) ? 0 : 1, j, S);
+                        keys[base + slot] = key;
+                        if (slot < kWaveKeys) kl[wave][slot] = key;
+                    }
+                    cu += __popcll(bp);
+                    cr += __popcll(__ballot(pass && in_r));
+                    ca += __popcll(__ballot(pass && in_a));
                 }
             }
         }
     }
     if (!kFill) {
-        cnt_union[i] = cu;
-        cnt_r[i] = cr;
-        cnt_a[i] = ca;
-        if (cr > max_r || ca > max_a) atomicOr(error_flag, 1);
+        if (lane == 0) {
+            cnt_union[i] = cu;
+            cnt_r[i] = cr;
+            cnt_a[i] = ca;
+            if (cr > max_r || ca > max_a) atomicOr(error_flag, 1);
+        }
+        return;
+    }
+    if (cu <= kWaveKeys) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        for (int a = lane; a < cu; a += kWave) {
+            const uint64_t x = kl[wave][a];
+            int rank = 0;
+            for (int b = 0; b < cu; ++b) rank += kl[wave][b] < x ? 1 : 0;
+            keys[base + rank] = x;
+        }
         return;
     }
     // insertion sort of this centre's keys: (class, j, S) ascending
+    if (lane != 0) return;
     uint64_t *k = keys + base;
     for (int a = 1; a < cu; ++a) {
-        uint64_t x = k[a];
+        const uint64_t x = k[a];
         int b = a - 1;
         while (b >= 0 && k[b] > x) {
             k[b + 1] = k[b];
@@ -611,10 +648,10 @@ extern "C" int rune_nlist_build(rune_nlist *nl, int64_t n_atoms, const double *d
         if (n > 0) {
             hipLaunchKernelGGL(fill_bins, dim3(gb), dim3(kThreads), 0, s, n, w.atom_bin,
                                w.bin_start, w.bin_cursor, w.bin_atoms);
-            hipLaunchKernelGGL((enumerate_edges<false>), dim3(gb), dim3(kThreads), 0, s, n,
+            hipLaunchKernelGGL((enumerate_wave<false>), dim3(ceil_div(n, 4)), dim3(256), 0, s, n,
                                d_positions, sptr, n_structures, w.geo, w.atom_wrap, w.atom_cell,
                                w.bin_start, w.bin_atoms, rc_radial * rc_radial,
-                               rc_angular * rc_angular, rc * rc, 0, max_radial, max_angular,
+                               rc_angular * rc_angular, rc * rc, max_radial, max_angular,
                                w.cnt_union, w.cnt_r, w.cnt_a, w.flag, nullptr, nullptr);
         }
         exclusive_scan(w.cnt_union, nl->ptr.as<int32_t>(), n, w.scan_tmp, s);
@@ -640,10 +677,10 @@ extern "C" int rune_nlist_build(rune_nlist *nl, int64_t n_atoms, const double *d
         nl->vec.reserve(16 * ecap);
         nl->ctr.reserve(4 * ecap);
         if (n > 0) {
-            hipLaunchKernelGGL((enumerate_edges<true>), dim3(gb), dim3(kThreads), 0, s, n,
+            hipLaunchKernelGGL((enumerate_wave<true>), dim3(ceil_div(n, 4)), dim3(256), 0, s, n,
                                d_positions, sptr, n_structures, w.geo, w.atom_wrap, w.atom_cell,
                                w.bin_start, w.bin_atoms, rc_radial * rc_radial,
-                               rc_angular * rc_angular, rc * rc, 0, max_radial, max_angular,
+                               rc_angular * rc_angular, rc * rc, max_radial, max_angular,
                                w.cnt_union, w.cnt_r, w.cnt_a, w.flag, nl->ptr.as<int32_t>(),
                                nl->keys.as<uint64_t>());
             hipLaunchKernelGGL(decode_records, dim3(gb), dim3(kThreads), 0, s, n, d_positions,
