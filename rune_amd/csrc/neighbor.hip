@@ -128,25 +128,33 @@ __device__ inline uint64_t make_key(int cls, int j, const int *S) {
     return k;
 }
 
-// Candidate enumeration, one atom per wave: the 64 lanes test the candidates
-// of a stencil cell (bins within the stencil reach, periodic images by
-// wrapping) in parallel with the exact fp64 test, and ballots count the
-// members (pass 1: union, radial and angular counts) and give each passing
-// candidate its slot (pass 2), so the fill pass writes the keys of a centre in
-// candidate order; the centre's keys (at most kWaveKeys) are then sorted in
-// LDS by rank (each key's rank is the number of smaller keys; keys of one
-// centre are distinct).  Centres with more keys fall back to lane 0's
-// insertion sort in global memory.
+// Candidate enumeration, one atom per wave, in one pass: the stencil cells
+// (bins within the stencil reach, periodic images by wrapping) are taken 64
+// at a time, a wave scan of their sizes flattens their candidates into one
+// index range, and the 64 lanes test 64 candidates at a time with the exact
+// fp64 test.  Ballots count the members (union, radial, angular) and give
+// each its slot in the atom's row of `keys` ([n, cap], cap = the larger
+// neighbour limit, so a centre within the limits always fits).  The centre's
+// keys are then sorted by rank in LDS (each key's rank is the number of
+// smaller keys; keys of one centre are distinct, since each (j, S) image is
+// proposed once); centres with more than kWaveKeys keys fall back to lane
+// 0's insertion sort in global memory.
 constexpr int kWaveKeys = 1024;
 
-template <bool kFill>
-__global__ void __launch_bounds__(256) enumerate_wave(
+__device__ inline void wave_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ void __launch_bounds__(256) enumerate_flat(
     int n, const double *pos, const int32_t *sptr, int nstruct, const Geo *geo,
     const int32_t *atom_wrap, const int32_t *atom_cell, const int32_t *bin_start,
     const int32_t *bin_atoms, double rc2_r, double rc2_a, double rc2_max, int max_r, int max_a,
-    int32_t *cnt_union, int32_t *cnt_r, int32_t *cnt_a, int32_t *error_flag, const int32_t *ptr,
+    int cap, int32_t *cnt_union, int32_t *cnt_r, int32_t *cnt_a, int32_t *error_flag,
     uint64_t *keys) {
-    __shared__ uint64_t kl[4][kFill ? kWaveKeys : 1];
+    __shared__ uint64_t kl[4][kWaveKeys];
+    __shared__ int cst[4][kWave], cbg[4][kWave], cT[4][kWave][3];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int i = blockIdx.x * 4 + wave;
     if (i >= n) return;
@@ -154,119 +162,146 @@ __global__ void __launch_bounds__(256) enumerate_wave(
     const Geo &g = geo[s];
     const int wi[3] = {atom_wrap[3 * i], atom_wrap[3 * i + 1], atom_wrap[3 * i + 2]};
     const int ci[3] = {atom_cell[3 * i], atom_cell[3 * i + 1], atom_cell[3 * i + 2]};
+    const int sx = 2 * g.m[0] + 1, sy = 2 * g.m[1] + 1, sz = 2 * g.m[2] + 1;
+    const int ncell = sx * sy * sz;
     const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    uint64_t *out = keys + size_t(i) * cap;
     int cu = 0, cr = 0, ca = 0;
-    const int base = kFill ? ptr[i] : 0;
-    for (int dx = -g.m[0]; dx <= g.m[0]; ++dx) {
-        for (int dy = -g.m[1]; dy <= g.m[1]; ++dy) {
-            for (int dz = -g.m[2]; dz <= g.m[2]; ++dz) {
-                const int dd[3] = {dx, dy, dz};
-                int T[3], bb[3];
-                bool ok = true;
-                for (int d = 0; d < 3; ++d) {
-                    const int b = ci[d] + dd[d];
-                    if (g.pbc[d]) {
-                        const int t = (b >= 0) ? b / g.nb[d] : -((-b + g.nb[d] - 1) / g.nb[d]);
-                        T[d] = t;
-                        bb[d] = b - t * g.nb[d];
-                    } else {
-                        T[d] = 0;
-                        bb[d] = b;
-                        ok = ok && (b >= 0 && b < g.nb[d]);
-                    }
-                }
-                if (!ok) continue;
-                const int flat = g.bin_offset + (bb[0] * g.nb[1] + bb[1]) * g.nb[2] + bb[2];
-                const int beg = bin_start[flat], end = bin_start[flat + 1];
-                for (int q0 = beg; q0 < end; q0 += kWave) {
-                    const int q = q0 + lane;
-                    bool pass = false, in_r = false, in_a = false;
-                    int j = 0, S[3] = {0, 0, 0};
-                    if (q < end) {
-                        j = bin_atoms[q];
-                        for (int d = 0; d < 3; ++d)
-                            S[d] = g.pbc[d] ? (T[d] - atom_wrap[3 * j + d] + wi[d]) : 0;
-                        if (!(j == i && S[0] == 0 && S[1] == 0 && S[2] == 0)) {
-                            double v[3];
-                            const double r2 = pair_d2(pos, g, i, j, S, v);
-                            pass = r2 < rc2_max;
-                            in_r = r2 < rc2_r;
-                            in_a = r2 < rc2_a;
-                        }
-                    }
-                    const uint64_t bp = __ballot(pass);
-                    if (kFill && pass) {
-                        const int slot = cu + __popcll(bp & below);
-                        const uint64_t key = make_key((in_r && in_a) ? 0 : 1, j, S);
-                        keys[base + slot] = key;
-                        if (slot < kWaveKeys) kl[wave][slot] = key;
-                    }
-                    cu += __popcll(bp);
-                    cr += __popcll(__ballot(pass && in_r));
-                    ca += __popcll(__ballot(pass && in_a));
+    for (int c0 = 0; c0 < ncell; c0 += kWave) {
+        const int c = c0 + lane;
+        int cnt = 0, beg = 0, T[3] = {0, 0, 0};
+        if (c < ncell) {
+            const int dd[3] = {c / (sz * sy) - g.m[0], (c / sz) % sy - g.m[1], c % sz - g.m[2]};
+            int bb[3];
+            bool ok = true;
+            for (int d = 0; d < 3; ++d) {
+                const int b = ci[d] + dd[d];
+                if (g.pbc[d]) {
+                    const int t = (b >= 0) ? b / g.nb[d] : -((-b + g.nb[d] - 1) / g.nb[d]);
+                    T[d] = t;
+                    bb[d] = b - t * g.nb[d];
+                } else {
+                    bb[d] = b;
+                    ok = ok && (b >= 0 && b < g.nb[d]);
                 }
             }
+            if (ok) {
+                const int flat = g.bin_offset + (bb[0] * g.nb[1] + bb[1]) * g.nb[2] + bb[2];
+                beg = bin_start[flat];
+                cnt = bin_start[flat + 1] - beg;
+            }
         }
-    }
-    if (!kFill) {
-        if (lane == 0) {
-            cnt_union[i] = cu;
-            cnt_r[i] = cr;
-            cnt_a[i] = ca;
-            if (cr > max_r || ca > max_a) atomicOr(error_flag, 1);
+        int incl = cnt;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int v = __shfl_up(incl, off, kWave);
+            if (lane >= off) incl += v;
         }
-        return;
+        const int total = __shfl(incl, kWave - 1, kWave);
+        wave_fence();
+        cst[wave][lane] = incl - cnt;
+        cbg[wave][lane] = beg;
+        cT[wave][lane][0] = T[0];
+        cT[wave][lane][1] = T[1];
+        cT[wave][lane][2] = T[2];
+        wave_fence();
+        for (int t0 = 0; t0 < total; t0 += kWave) {
+            const int t = t0 + lane;
+            bool pass = false, in_r = false, in_a = false;
+            int j = 0, S[3] = {0, 0, 0};
+            if (t < total) {
+                // the cell holding candidate t: the last one starting at or before t
+                int lo = 0, hi = kWave - 1;
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (cst[wave][mid] <= t) lo = mid; else hi = mid - 1;
+                }
+                j = bin_atoms[cbg[wave][lo] + (t - cst[wave][lo])];
+                for (int d = 0; d < 3; ++d)
+                    S[d] = g.pbc[d] ? (cT[wave][lo][d] - atom_wrap[3 * j + d] + wi[d]) : 0;
+                if (!(j == i && S[0] == 0 && S[1] == 0 && S[2] == 0)) {
+                    double v[3];
+                    const double r2 = pair_d2(pos, g, i, j, S, v);
+                    pass = r2 < rc2_max;
+                    in_r = r2 < rc2_r;
+                    in_a = r2 < rc2_a;
+                }
+            }
+            const uint64_t bp = __ballot(pass);
+            if (pass) {
+                const int slot = cu + __popcll(bp & below);
+                const uint64_t key = make_key((in_r && in_a) ? 0 : 1, j, S);
+                if (slot < cap) out[slot] = key;
+                if (slot < kWaveKeys) kl[wave][slot] = key;
+            }
+            cu += __popcll(bp);
+            cr += __popcll(__ballot(pass && in_r));
+            ca += __popcll(__ballot(pass && in_a));
+        }
+        wave_fence();
     }
+    if (lane == 0) {
+        cnt_union[i] = cu;
+        cnt_r[i] = cr;
+        cnt_a[i] = ca;
+        if (cr > max_r || ca > max_a || cu > cap) atomicOr(error_flag, 1);
+    }
+    if (cu > cap) return;
     if (cu <= kWaveKeys) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         for (int a = lane; a < cu; a += kWave) {
             const uint64_t x = kl[wave][a];
             int rank = 0;
             for (int b = 0; b < cu; ++b) rank += kl[wave][b] < x ? 1 : 0;
-            keys[base + rank] = x;
+            out[rank] = x;
         }
         return;
     }
     // insertion sort of this centre's keys: (class, j, S) ascending
     if (lane != 0) return;
-    uint64_t *k = keys + base;
     for (int a = 1; a < cu; ++a) {
-        const uint64_t x = k[a];
+        const uint64_t x = out[a];
         int b = a - 1;
-        while (b >= 0 && k[b] > x) {
-            k[b + 1] = k[b];
+        while (b >= 0 && out[b] > x) {
+            out[b + 1] = out[b];
             --b;
         }
-        k[b + 1] = x;
+        out[b + 1] = x;
     }
 }
 
-__global__ void decode_records(int n, const double *pos, const int32_t *sptr, int nstruct,
-                               const Geo *geo, const int32_t *ptr, const int32_t *cnt_r,
-                               const int32_t *cnt_a, const uint64_t *keys, int32_t *view,
-                               int32_t *nbr, int32_t *shift, float4 *vec, int32_t *ctr) {
-    int i = blockIdx.x * blockDim.x + threadIdx.x;
+// Records of centre i from its sorted keys (row i of keys, stride cap), one
+// atom per wave, lanes over its records.
+__global__ void __launch_bounds__(256) decode_wave(int n, const double *pos, const int32_t *sptr,
+                                                   int nstruct, const Geo *geo, int cap,
+                                                   const int32_t *ptr, const int32_t *cnt_r,
+                                                   const int32_t *cnt_a, const uint64_t *keys,
+                                                   int32_t *view, int32_t *nbr, int32_t *shift,
+                                                   float4 *vec, int32_t *ctr) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int i = blockIdx.x * 4 + wave;
     if (i >= n) return;
-    int s = find_structure(sptr, nstruct, i);
+    const int s = find_structure(sptr, nstruct, i);
     const Geo &g = geo[s];
-    int b = ptr[i], e = ptr[i + 1];
-    view[4 * i + 0] = b;
-    view[4 * i + 1] = b + cnt_r[i];
-    view[4 * i + 2] = b;
-    view[4 * i + 3] = b + cnt_a[i];
-    float pi[3] = {float(pos[3 * i]), float(pos[3 * i + 1]), float(pos[3 * i + 2])};
-    for (int r = b; r < e; ++r) {
-        uint64_t key = keys[r];
-        int j = int((key >> 24) & 0x3fffffffffull);
-        int S[3] = {int((key >> 16) & 0xff) - 128, int((key >> 8) & 0xff) - 128,
-                    int(key & 0xff) - 128};
+    const int b = ptr[i], e = ptr[i + 1];
+    if (lane == 0) {
+        view[4 * i + 0] = b;
+        view[4 * i + 1] = b + cnt_r[i];
+        view[4 * i + 2] = b;
+        view[4 * i + 3] = b + cnt_a[i];
+    }
+    const float pi[3] = {float(pos[3 * i]), float(pos[3 * i + 1]), float(pos[3 * i + 2])};
+    const uint64_t *row = keys + size_t(i) * cap;
+    for (int k = lane; k < e - b; k += kWave) {
+        const int r = b + k;
+        const uint64_t key = row[k];
+        const int j = int((key >> 24) & 0x3fffffffffull);
+        const int S[3] = {int((key >> 16) & 0xff) - 128, int((key >> 8) & 0xff) - 128,
+                          int(key & 0xff) - 128};
         float v[3];
         for (int d = 0; d < 3; ++d) {
-            double o = (double(S[0]) * g.cell[0 * 3 + d] + double(S[1]) * g.cell[1 * 3 + d]) +
-                       double(S[2]) * g.cell[2 * 3 + d];
-            float pj = float(pos[3 * j + d]);
+            const double o = (double(S[0]) * g.cell[0 * 3 + d] + double(S[1]) * g.cell[1 * 3 + d]) +
+                             double(S[2]) * g.cell[2 * 3 + d];
+            const float pj = float(pos[3 * j + d]);
             v[d] = (pj + float(o)) - pi[d];
         }
         nbr[r] = j;
@@ -274,10 +309,11 @@ __global__ void decode_records(int n, const double *pos, const int32_t *sptr, in
         shift[3 * r + 0] = S[0];
         shift[3 * r + 1] = S[1];
         shift[3 * r + 2] = S[2];
-        float d2 = v[0] * v[0] + v[1] * v[1] + v[2] * v[2];
+        const float d2 = v[0] * v[0] + v[1] * v[1] + v[2] * v[2];
         vec[r] = make_float4(v[0], v[1], v[2], sqrtf(d2));
     }
 }
+
 
 // ---- records from padded reference batches ----
 
@@ -639,6 +675,9 @@ extern "C" int rune_nlist_build(rune_nlist *nl, int64_t n_atoms, const double *d
         nl->view.reserve(16 * size_t(n + 1));
         int gb = ceil_div(std::max(n, 1), kThreads);
         const int32_t *sptr = nl->sptr.as<int32_t>();
+        // one row of sorted keys per centre, as wide as the larger neighbour limit
+        const int cap = std::max(max_radial, max_angular);
+        nl->keys.reserve(8 * size_t(std::max(n, 1)) * size_t(cap));
         if (n > 0) {
             hipLaunchKernelGGL(bin_atoms, dim3(gb), dim3(kThreads), 0, s, n, d_positions, sptr,
                                n_structures, w.geo, w.atom_bin, w.atom_wrap, w.atom_cell,
@@ -648,11 +687,11 @@ extern "C" int rune_nlist_build(rune_nlist *nl, int64_t n_atoms, const double *d
         if (n > 0) {
             hipLaunchKernelGGL(fill_bins, dim3(gb), dim3(kThreads), 0, s, n, w.atom_bin,
                                w.bin_start, w.bin_cursor, w.bin_atoms);
-            hipLaunchKernelGGL((enumerate_wave<false>), dim3(ceil_div(n, 4)), dim3(256), 0, s, n,
+            hipLaunchKernelGGL(enumerate_flat, dim3(ceil_div(n, 4)), dim3(256), 0, s, n,
                                d_positions, sptr, n_structures, w.geo, w.atom_wrap, w.atom_cell,
                                w.bin_start, w.bin_atoms, rc_radial * rc_radial,
-                               rc_angular * rc_angular, rc * rc, max_radial, max_angular,
-                               w.cnt_union, w.cnt_r, w.cnt_a, w.flag, nullptr, nullptr);
+                               rc_angular * rc_angular, rc * rc, max_radial, max_angular, cap,
+                               w.cnt_union, w.cnt_r, w.cnt_a, w.flag, nl->keys.as<uint64_t>());
         }
         exclusive_scan(w.cnt_union, nl->ptr.as<int32_t>(), n, w.scan_tmp, s);
         RUNE_HIP_CHECK(hipGetLastError());
@@ -671,20 +710,13 @@ extern "C" int rune_nlist_build(rune_nlist *nl, int64_t n_atoms, const double *d
         int64_t e = host[0];
         nl->n_records = e;
         size_t ecap = size_t(std::max<int64_t>(e, 1));
-        nl->keys.reserve(8 * ecap);
         nl->nbr.reserve(4 * ecap);
         nl->shift.reserve(12 * ecap);
         nl->vec.reserve(16 * ecap);
         nl->ctr.reserve(4 * ecap);
         if (n > 0) {
-            hipLaunchKernelGGL((enumerate_wave<true>), dim3(ceil_div(n, 4)), dim3(256), 0, s, n,
-                               d_positions, sptr, n_structures, w.geo, w.atom_wrap, w.atom_cell,
-                               w.bin_start, w.bin_atoms, rc_radial * rc_radial,
-                               rc_angular * rc_angular, rc * rc, max_radial, max_angular,
-                               w.cnt_union, w.cnt_r, w.cnt_a, w.flag, nl->ptr.as<int32_t>(),
-                               nl->keys.as<uint64_t>());
-            hipLaunchKernelGGL(decode_records, dim3(gb), dim3(kThreads), 0, s, n, d_positions,
-                               sptr, n_structures, w.geo, nl->ptr.as<int32_t>(), w.cnt_r,
+            hipLaunchKernelGGL(decode_wave, dim3(ceil_div(n, 4)), dim3(256), 0, s, n, d_positions,
+                               sptr, n_structures, w.geo, cap, nl->ptr.as<int32_t>(), w.cnt_r,
                                w.cnt_a, nl->keys.as<uint64_t>(), nl->view.as<int32_t>(),
                                nl->nbr.as<int32_t>(), nl->shift.as<int32_t>(),
                                nl->vec.as<float4>(), nl->ctr.as<int32_t>());

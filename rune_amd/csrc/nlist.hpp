@@ -30,7 +30,7 @@ struct rune_nlist {
     std::vector<int32_t> h_perm; // host bin ranks behind the last order upload
     // working memory of the builder
     rune::DeviceBuffer work;
-    rune::DeviceBuffer keys;     // uint64 [E]
+    rune::DeviceBuffer keys;     // uint64 [N, max(max_radial, max_angular)] sorted per centre
     rune::DeviceBuffer pinned_dummy;
 };
 
