@@ -784,15 +784,16 @@ __device__ inline float cutoff_slope(float d, float rc) {
 // rows of a 64-record chunk are staged in LDS with one parallel load.
 template <int LQ, int S>
 __global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
-    constexpr int NQ = LQ * (LQ + 2), LY = NQ + (NQ % 4 == 0 ? 4 : 1), LD = NQ + 1;
+    constexpr int NQ = LQ * (LQ + 2), LY = NQ + (NQ % 4 == 0 ? 4 : 1);
     using Ln = Lanes<S>;
     constexpr int W = Ln::W;
+    constexpr int WT = W + 4;              // T row: channels of one (slot, k), padded
     constexpr int KQ = (NQ + W - 1) / W;   // dE/dY components per lane
     extern __shared__ float lds[];
     const int j = wave_atom(a.r);
     if (j < 0) return;
     const Ln ln(a.C);
-    float *Yc = lds + (threadIdx.x >> 6) * kWave * (LY + LD);
+    float *Yc = lds + (threadIdx.x >> 6) * (kWave * LY + S * NQ * WT);
     float *T = Yc + kWave * LY;
     const int G = a.G, C = a.C, CN = C * NQ, LC = LQ * C, NG = a.NG;
     float MX[NQ], acc[NQ];
@@ -871,7 +872,7 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
 #pragma unroll
                         for (int m = 0; m < 2 * L + 1; ++m) {
                             acc[st + m] += fc * t1 * DH[st + m];
-                            T[ln.lane * LD + st + m] = fc * t2 * DH[st + m];
+                            T[(ln.slot * NQ + st + m) * WT + ln.c] = fc * t2 * DH[st + m];
                         }
                     }
                 } else {
@@ -891,8 +892,18 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
                 for (int u = 0; u < KQ; ++u) {
                     const int k = ln.c + W * u;
                     if (k < NQ) {
-                        float sum = 0.0f;
-                        for (int c = 0; c < a.C; ++c) sum += T[(ln.slot * W + c) * LD + k];
+                        const float *row = T + (ln.slot * NQ + k) * WT;
+                        float4 s4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                        int c = 0;
+                        for (; c + 4 <= C; c += 4) {
+                            const float4 t = *reinterpret_cast<const float4 *>(row + c);
+                            s4.x += t.x;
+                            s4.y += t.y;
+                            s4.z += t.z;
+                            s4.w += t.w;
+                        }
+                        float sum = (s4.x + s4.y) + (s4.z + s4.w);
+                        for (; c < C; ++c) sum += row[c];
                         a.dy[size_t(e) * NQ + k] = yo[u] + sum;
                     }
                 }
@@ -1911,6 +1922,9 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
                 a.wlds = std::max(cn4, kWave * (ly + p.ldrb));
                 const size_t lds_n = sizeof(float) * kWaves * a.wlds;
                 EQ_LAUNCH_D(k_eq_edge_nbr, lq, dmc, egrid, dim3(kBlock), lds_n, s, a);
+            }
+            {
+                Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
                 a.wlds = std::max(cn4, kWave * ly);
                 const size_t lds_c = sizeof(float) * kWaves * a.wlds;
                 EQ_LAUNCH_D(k_eq_edge_centre, lq, dmc, egrid, dim3(kBlock), lds_c, s, a);
@@ -1986,7 +2000,8 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         {
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
             EQ_LAUNCH_S(k_eq_pair_dir, lq, a.S, dim3(atom_grid), dim3(kBlock),
-                        sizeof(float) * kBlock * (ly + nq + 1), s, a);
+                        sizeof(float) * kWaves * (kWave * ly + a.S * nq * (kWave / a.S + 4)),
+                        s, a);
         }
         {
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
@@ -2017,12 +2032,14 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
                      s);
             }
         }
-        {
+        a.wlds = adj_wlds;
+        for (int side = 0; side < 2; ++side) {
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
-            a.wlds = adj_wlds;
             const size_t lds = sizeof(float) * kWaves * adj_wlds;
-            EQ_LAUNCH_A(k_eq_edge_adj, lq, ntc, 0, dim3(atom_grid), dim3(kBlock), lds, s, a);
-            EQ_LAUNCH_A(k_eq_edge_adj, lq, ntc, 1, dim3(atom_grid), dim3(kBlock), lds, s, a);
+            if (side == 0)
+                EQ_LAUNCH_A(k_eq_edge_adj, lq, ntc, 0, dim3(atom_grid), dim3(kBlock), lds, s, a);
+            else
+                EQ_LAUNCH_A(k_eq_edge_adj, lq, ntc, 1, dim3(atom_grid), dim3(kBlock), lds, s, a);
         }
         // channel projection of the factor adjoints: dHk[n, k, :] = dQ[n, k, :] [Wc | Wn]_L(k)^T
         {
