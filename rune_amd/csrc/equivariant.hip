@@ -10,6 +10,7 @@
 //
 // Angular states are stored [atom][channel][component] (components of order L
 // at L*L-1 .. L*L+2L-1), matching direction[..., start:stop] of the reference.
+#include <algorithm>
 #include <cmath>
 
 #include "activation.hpp"
@@ -386,7 +387,7 @@ __device__ inline float lane_get(float v, int q) {
 // compiler's memory-counter waits exact, so prefetched loads stay in flight.
 
 // Radial-basis weights held in registers; a longer basis reads the rest from L2.
-constexpr int kRbRegs = 20;
+constexpr int kRbRegs = 17;
 
 template <int DMC>
 struct EdgeCols {
@@ -403,12 +404,18 @@ struct EdgeCols {
 };
 
 // Q[k][u] = sum_c Hs[c, k] Wp[(L(k) - 1) C + c, dl[u]], Hs the atom's state
-// row [C, NQ] staged in the wave's LDS.  The weights of channel c + 1 are
-// loaded while channel c is applied.
+// row [C, NQ] staged in LDS.  The block's four waves stage the weights of one
+// order at a time (this block's column chunk, [C][kWave * DMC]) into the
+// shared Ws with one lane-parallel load, so the per-channel weight reads are
+// LDS reads instead of a chain of dependent L2 loads.  Every wave of the
+// block calls this (it holds block barriers); `active` is false for waves
+// without an atom.
 template <int LQ, int DMC>
 __device__ inline void project_state(const float *Hs, const float *__restrict__ Wp, int C, int D,
-                                     const int (&dl)[DMC], float (&Q)[LQ * (LQ + 2)][DMC]) {
-    constexpr int NQ = LQ * (LQ + 2);
+                                     const int (&dl)[DMC], float (&Q)[LQ * (LQ + 2)][DMC],
+                                     float *Ws, bool active) {
+    constexpr int NQ = LQ * (LQ + 2), WC = kWave * DMC;
+    const int c0 = int(blockIdx.y) * WC, cw = min(WC, D - c0);
 #pragma unroll
     for (int k = 0; k < NQ; ++k)
 #pragma unroll
@@ -416,25 +423,35 @@ __device__ inline void project_state(const float *Hs, const float *__restrict__ 
 #pragma unroll
     for (int L = 1; L <= LQ; ++L) {
         const int st = L * L - 1;
-        const float *wl = Wp + size_t(L - 1) * C * D;
-        float w[DMC];
+        const float *wl = Wp + size_t(L - 1) * C * D + c0;
+        __syncthreads();
+        for (int o = threadIdx.x; o < C * WC; o += 8 * kBlock) {
+            float v[8];
 #pragma unroll
-        for (int u = 0; u < DMC; ++u) w[u] = wl[dl[u]];
-        for (int c = 0; c < C; ++c) {
-            float wn[DMC];
-            const int cn = min(c + 1, C - 1);
-#pragma unroll
-            for (int u = 0; u < DMC; ++u) wn[u] = wl[size_t(cn) * D + dl[u]];
-#pragma unroll
-            for (int m = 0; m < 2 * L + 1; ++m) {
-                const float h = Hs[c * NQ + st + m];
-#pragma unroll
-                for (int u = 0; u < DMC; ++u) Q[st + m][u] += h * w[u];
+            for (int u = 0; u < 8; ++u) {
+                const int q = min(o + u * kBlock, C * WC - 1), c = q / WC, x = min(q - c * WC, cw - 1);
+                v[u] = wl[size_t(c) * D + x];
             }
 #pragma unroll
-            for (int u = 0; u < DMC; ++u) w[u] = wn[u];
+            for (int u = 0; u < 8; ++u)
+                if (o + u * kBlock < C * WC) Ws[o + u * kBlock] = v[u];
+        }
+        __syncthreads();
+        if (active) {
+            for (int c = 0; c < C; ++c) {
+                float w[DMC];
+#pragma unroll
+                for (int u = 0; u < DMC; ++u) w[u] = Ws[c * WC + dl[u] - c0];
+#pragma unroll
+                for (int m = 0; m < 2 * L + 1; ++m) {
+                    const float h = Hs[c * NQ + st + m];
+#pragma unroll
+                    for (int u = 0; u < DMC; ++u) Q[st + m][u] += h * w[u];
+                }
+            }
         }
     }
+    __syncthreads();
 }
 
 // Keeps the factor for the reverse pass: out[k * ld + d].
@@ -445,11 +462,6 @@ __device__ inline void store_factor(const float (&Q)[LQ * (LQ + 2)][DMC], float 
     for (int k = 0; k < LQ * (LQ + 2); ++k)
 #pragma unroll
         for (int u = 0; u < DMC; ++u) out[size_t(k) * ld + d[u]] = Q[k][u];
-}
-
-__device__ inline void stage_state(float *Hs, const float *__restrict__ row, int CN) {
-    stage_row(Hs, row, CN);
-    wave_sync();
 }
 
 // Harmonic row (and radial-basis row when R) of record e into the wave's LDS
@@ -478,15 +490,19 @@ __global__ void __launch_bounds__(kBlock) k_eq_edge_nbr(EqArgs a) {
     constexpr int NQ = LQ * (LQ + 2), LY = NQ + (NQ % 4 == 0 ? 4 : 1);
     extern __shared__ float lds[];
     const int j = wave_atom(a.r);
-    if (j < 0) return;
     const int lane = threadIdx.x & (kWave - 1), C = a.C, D = a.D, CN = C * NQ, kb = a.kb;
-    const int LR = a.ldrb, ldd = a.ldd;
-    float *Yc = lds + (threadIdx.x >> 6) * a.wlds;
-    float *Rc = Yc + kWave * LY;
+    const int LR = a.ldrb, ldd = a.ldd, cn4 = (CN + 3) & ~3;
     const EdgeCols<DMC> col(D);
     float Q[NQ][DMC];
-    stage_state(Yc, a.dir_in + size_t(j) * CN, CN);
-    project_state<LQ, DMC>(Yc, a.wpn, C, D, col.dl, Q);
+    {
+        // prologue layout: the four state rows, then the shared weight chunk
+        float *Hs = lds + (threadIdx.x >> 6) * cn4;
+        if (j >= 0) stage_row(Hs, a.dir_in + size_t(j) * CN, CN);
+        project_state<LQ, DMC>(Hs, a.wpn, C, D, col.dl, Q, lds + kWaves * cn4, j >= 0);
+    }
+    if (j < 0) return;
+    float *Yc = lds + (threadIdx.x >> 6) * a.wlds;
+    float *Rc = Yc + kWave * LY;
     store_factor<LQ, DMC>(Q, a.qbuf + size_t(j) * NQ * 2 * ldd + ldd, 2 * ldd, col.d);
     float wr[kRbRegs][DMC], Bj[DMC];
 #pragma unroll
@@ -558,14 +574,17 @@ __global__ void __launch_bounds__(kBlock) k_eq_edge_centre(EqArgs a) {
     constexpr int NQ = LQ * (LQ + 2), LY = NQ + (NQ % 4 == 0 ? 4 : 1);
     extern __shared__ float lds[];
     const int i = wave_atom(a.r);
-    if (i < 0) return;
     const int lane = threadIdx.x & (kWave - 1), C = a.C, D = a.D, CN = C * NQ, act = a.act;
-    const int ldd = a.ldd;
-    float *Yc = lds + (threadIdx.x >> 6) * a.wlds;
+    const int ldd = a.ldd, cn4 = (CN + 3) & ~3;
     const EdgeCols<DMC> col(D);
     float Q[NQ][DMC], A[DMC];
-    stage_state(Yc, a.dir_in + size_t(i) * CN, CN);
-    project_state<LQ, DMC>(Yc, a.wpc, C, D, col.dl, Q);
+    {
+        float *Hs = lds + (threadIdx.x >> 6) * cn4;
+        if (i >= 0) stage_row(Hs, a.dir_in + size_t(i) * CN, CN);
+        project_state<LQ, DMC>(Hs, a.wpc, C, D, col.dl, Q, lds + kWaves * cn4, i >= 0);
+    }
+    if (i < 0) return;
+    float *Yc = lds + (threadIdx.x >> 6) * a.wlds;
     store_factor<LQ, DMC>(Q, a.qbuf + size_t(i) * NQ * 2 * ldd, 2 * ldd, col.d);
 #pragma unroll
     for (int u = 0; u < DMC; ++u) A[u] = a.node[size_t(i) * a.NP + col.dl[u]];
@@ -1919,13 +1938,17 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
             const dim3 egrid(atom_grid, ceil_div(D, kWave * dmc));
             {
                 Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
-                a.wlds = std::max(cn4, kWave * (ly + p.ldrb));
+                // per-wave record rows, or (prologue) the state rows plus one
+                // order's weight chunk
+                const int pro = ceil_div(kWaves * cn4 + C * kWave * dmc, kWaves);
+                a.wlds = std::max({cn4, kWave * (ly + p.ldrb), pro});
                 const size_t lds_n = sizeof(float) * kWaves * a.wlds;
                 EQ_LAUNCH_D(k_eq_edge_nbr, lq, dmc, egrid, dim3(kBlock), lds_n, s, a);
             }
             {
                 Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
-                a.wlds = std::max(cn4, kWave * ly);
+                const int pro = ceil_div(kWaves * cn4 + C * kWave * dmc, kWaves);
+                a.wlds = std::max({cn4, kWave * ly, pro});
                 const size_t lds_c = sizeof(float) * kWaves * a.wlds;
                 EQ_LAUNCH_D(k_eq_edge_centre, lq, dmc, egrid, dim3(kBlock), lds_c, s, a);
             }
