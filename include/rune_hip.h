@@ -76,6 +76,27 @@ int rune_nlist_build(rune_nlist *nl, int64_t n_atoms, const double *d_positions,
                      int32_t max_radial, int32_t max_angular,
                      void *stream, int64_t *n_records);
 
+/* Verlet-skin reuse of the lists for a moving system (MD loop): same
+ * arguments and records as rune_nlist_build, plus `skin` (Angstrom, > 0).
+ * The handle keeps the candidates within max(rc) + skin found by its last
+ * search and the positions that search saw; a call searches again only when
+ * it is the first, when the atom count, structure ranges, cells, pbc,
+ * cutoffs, limits or skin changed, or when some atom moved by skin / 2 or
+ * more (positions compared as given: an atom wrapped into the cell also
+ * triggers a search).  Otherwise the candidates are re-tested at the current
+ * positions with the same exact fp64 test, so the records are bitwise those
+ * of rune_nlist_build on the same positions either way.  *searched (may be
+ * NULL) receives 1 when this call searched.  Replaces the candidate cache of
+ * the reference's GPUMD evaluator (rune/mobius/src/mobius.cu:241-271,
+ * :334-402: 1 A skin, reuse while every atom moved less than skin / 2, new
+ * search on a box or pbc change). */
+int rune_nlist_update(rune_nlist *nl, int64_t n_atoms, const double *d_positions,
+                      int32_t n_structures, const int64_t *h_struct_ptr,
+                      const double *h_cells, const int32_t *h_pbc,
+                      double rc_radial, double rc_angular,
+                      int32_t max_radial, int32_t max_angular, double skin,
+                      void *stream, int64_t *n_records, int32_t *searched);
+
 /* Records from the reference's padded batch tensors (-1 padded int64
  * [N,K] neighbour rows and fp32 [N,K,3] offsets, batch.py:9-39), with fp32
  * positions [N,3]; vec = (p[j] + offset) - p[i] as descriptor.py:813-817.

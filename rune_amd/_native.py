@@ -68,6 +68,8 @@ def library():
         "rune_nlist_destroy": (None, [vp]),
         "rune_nlist_build": (C.c_int, [vp, i64, vp, i32, vp, vp, vp, f64, f64, i32, i32, vp,
                                        C.POINTER(i64)]),
+        "rune_nlist_update": (C.c_int, [vp, i64, vp, i32, vp, vp, vp, f64, f64, i32, i32, f64,
+                                        vp, C.POINTER(i64), C.POINTER(i32)]),
         "rune_nlist_from_padded": (C.c_int, [vp, i64, vp, vp, vp, i32, vp, vp, i32, i32, vp, vp,
                                              C.POINTER(i64)]),
         "rune_nlist_export": (C.c_int, [vp, vp, vp, vp, vp, vp, vp]),
@@ -157,6 +159,31 @@ class NeighborList:
         self.device = pos.device
         self._keep = pos
         return self
+
+    def update(self, positions, struct_ptr, cells, pbc, rc_radial, rc_angular, max_radial,
+               max_angular, skin=1.0):
+        """As build(), reusing the candidates of the last search while every atom
+        stays within skin / 2 of where that search saw it.  Returns True when
+        this call searched again."""
+        import numpy as np
+        pos = positions.contiguous()
+        assert pos.dtype == torch.float64 and pos.is_cuda
+        sp = np.ascontiguousarray(struct_ptr, dtype=np.int64)
+        cl = np.ascontiguousarray(cells, dtype=np.float64).reshape(-1, 9)
+        pb = np.ascontiguousarray(pbc, dtype=np.int32).reshape(-1, 3)
+        n_rec = C.c_int64()
+        searched = C.c_int32()
+        check(library().rune_nlist_update(
+            self._h, pos.shape[0], _ptr(pos), len(sp) - 1,
+            sp.ctypes.data_as(C.c_void_p), cl.ctypes.data_as(C.c_void_p),
+            pb.ctypes.data_as(C.c_void_p), float(rc_radial), float(rc_angular),
+            int(max_radial), int(max_angular), float(skin), _stream(pos.device),
+            C.byref(n_rec), C.byref(searched)))
+        self.n_atoms = pos.shape[0]
+        self.n_records = n_rec.value
+        self.device = pos.device
+        self._keep = pos
+        return bool(searched.value)
 
     def from_padded(self, positions, radial_neighbors, radial_offsets, angular_neighbors,
                     angular_offsets, struct_ptr):

@@ -147,6 +147,42 @@ __device__ inline void wave_fence() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Counts of centre i (and the overflow flag), then its keys sorted ascending:
+// by rank in LDS when they all fit there (kl holds the first kWaveKeys keys),
+// else by lane 0's insertion sort in global memory.
+__device__ inline void finish_centre(int i, int lane, int cu, int cr, int ca, int max_r, int max_a,
+                                     int cap, const uint64_t *kl, uint64_t *out,
+                                     int32_t *cnt_union, int32_t *cnt_r, int32_t *cnt_a,
+                                     int32_t *error_flag) {
+    if (lane == 0) {
+        cnt_union[i] = cu;
+        cnt_r[i] = cr;
+        cnt_a[i] = ca;
+        if (cr > max_r || ca > max_a || cu > cap) atomicOr(error_flag, 1);
+    }
+    if (cu > cap) return;
+    if (cu <= kWaveKeys) {
+        for (int a = lane; a < cu; a += kWave) {
+            const uint64_t x = kl[a];
+            int rank = 0;
+            for (int b = 0; b < cu; ++b) rank += kl[b] < x ? 1 : 0;
+            out[rank] = x;
+        }
+        return;
+    }
+    // insertion sort of this centre's keys: (class, j, S) ascending
+    if (lane != 0) return;
+    for (int a = 1; a < cu; ++a) {
+        const uint64_t x = out[a];
+        int b = a - 1;
+        while (b >= 0 && out[b] > x) {
+            out[b + 1] = out[b];
+            --b;
+        }
+        out[b + 1] = x;
+    }
+}
+
 __global__ void __launch_bounds__(256) enumerate_flat(
     int n, const double *pos, const int32_t *sptr, int nstruct, const Geo *geo,
     const int32_t *atom_wrap, const int32_t *atom_cell, const int32_t *bin_start,
@@ -240,33 +276,71 @@ __global__ void __launch_bounds__(256) enumerate_flat(
         }
         wave_fence();
     }
-    if (lane == 0) {
-        cnt_union[i] = cu;
-        cnt_r[i] = cr;
-        cnt_a[i] = ca;
-        if (cr > max_r || ca > max_a || cu > cap) atomicOr(error_flag, 1);
-    }
-    if (cu > cap) return;
-    if (cu <= kWaveKeys) {
-        for (int a = lane; a < cu; a += kWave) {
-            const uint64_t x = kl[wave][a];
-            int rank = 0;
-            for (int b = 0; b < cu; ++b) rank += kl[wave][b] < x ? 1 : 0;
-            out[rank] = x;
+    finish_centre(i, lane, cu, cr, ca, max_r, max_a, cap, kl[wave], out, cnt_union, cnt_r, cnt_a,
+                  error_flag);
+}
+
+// Re-test of cached candidates at the current positions (the skin reuse of
+// rune_nlist_update): one centre per wave, its candidate keys (any class)
+// taken 64 at a time with the same exact fp64 test and key packing as
+// enumerate_flat, so the centre's row of `keys` comes out identical to a
+// fresh enumeration whenever the candidates include every member.
+__global__ void __launch_bounds__(256) refilter_wave(
+    int n, const double *pos, const int32_t *sptr, int nstruct, const Geo *geo,
+    const uint64_t *cand, int capc, const int32_t *cand_cnt, double rc2_r, double rc2_a,
+    double rc2_max, int max_r, int max_a, int cap, int32_t *cnt_union, int32_t *cnt_r,
+    int32_t *cnt_a, int32_t *error_flag, uint64_t *keys) {
+    __shared__ uint64_t kl[4][kWaveKeys];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int i = blockIdx.x * 4 + wave;
+    if (i >= n) return;
+    const Geo &g = geo[find_structure(sptr, nstruct, i)];
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const uint64_t *row = cand + size_t(i) * capc;
+    uint64_t *out = keys + size_t(i) * cap;
+    const int m = cand_cnt[i];
+    int cu = 0, cr = 0, ca = 0;
+    for (int t0 = 0; t0 < m; t0 += kWave) {
+        const int t = t0 + lane;
+        bool pass = false, in_r = false, in_a = false;
+        int j = 0, S[3] = {0, 0, 0};
+        if (t < m) {
+            const uint64_t key = row[t];
+            j = int((key >> 24) & 0x3fffffffffull);
+            S[0] = int((key >> 16) & 0xff) - 128;
+            S[1] = int((key >> 8) & 0xff) - 128;
+            S[2] = int(key & 0xff) - 128;
+            double v[3];
+            const double r2 = pair_d2(pos, g, i, j, S, v);
+            pass = r2 < rc2_max;
+            in_r = r2 < rc2_r;
+            in_a = r2 < rc2_a;
         }
-        return;
-    }
-    // insertion sort of this centre's keys: (class, j, S) ascending
-    if (lane != 0) return;
-    for (int a = 1; a < cu; ++a) {
-        const uint64_t x = out[a];
-        int b = a - 1;
-        while (b >= 0 && out[b] > x) {
-            out[b + 1] = out[b];
-            --b;
+        const uint64_t bp = __ballot(pass);
+        if (pass) {
+            const int slot = cu + __popcll(bp & below);
+            const uint64_t key = make_key((in_r && in_a) ? 0 : 1, j, S);
+            if (slot < cap) out[slot] = key;
+            if (slot < kWaveKeys) kl[wave][slot] = key;
         }
-        out[b + 1] = x;
+        cu += __popcll(bp);
+        cr += __popcll(__ballot(pass && in_r));
+        ca += __popcll(__ballot(pass && in_a));
     }
+    wave_fence();
+    finish_centre(i, lane, cu, cr, ca, max_r, max_a, cap, kl[wave], out, cnt_union, cnt_r, cnt_a,
+                  error_flag);
+}
+
+// Sets *flag when some atom moved by skin / 2 or more since the candidate
+// search (positions compared as given, so a wrapped atom also triggers it).
+__global__ void check_displacement(int n, const double *pos, const double *ref, double limit2,
+                                   int32_t *flag) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const double x = pos[3 * i] - ref[3 * i], y = pos[3 * i + 1] - ref[3 * i + 1],
+                 z = pos[3 * i + 2] - ref[3 * i + 2];
+    if ((x * x + y * y) + z * z >= limit2) atomicOr(flag, 1);
 }
 
 // Records of centre i from its sorted keys (row i of keys, stride cap), one
@@ -603,127 +677,172 @@ static void set_structures(rune_nlist *nl, int64_t n_atoms, int32_t nstruct,
     nl->n_atoms = n_atoms;
 }
 
-extern "C" int rune_nlist_build(rune_nlist *nl, int64_t n_atoms, const double *d_positions,
-                                int32_t n_structures, const int64_t *h_struct_ptr,
-                                const double *h_cells, const int32_t *h_pbc, double rc_radial,
-                                double rc_angular, int32_t max_radial, int32_t max_angular,
-                                void *stream, int64_t *n_records) {
-    return guarded([&] {
-        RUNE_REQUIRE(nl && (d_positions || n_atoms == 0) && h_cells && h_pbc,
-                     RUNE_ERR_ARGUMENT, "null argument");
-        RUNE_REQUIRE(rc_radial > 0 && rc_angular > 0, RUNE_ERR_ARGUMENT,
-                     "radial and angular cutoffs must be positive");
-        RUNE_REQUIRE(max_radial >= 1 && max_angular >= 1, RUNE_ERR_ARGUMENT,
-                     "radial and angular max-neighbor counts must be positive");
-        hipStream_t s = as_stream(stream);
-        set_structures(nl, n_atoms, n_structures, h_struct_ptr, s);
-        nl->rc_radial = rc_radial;
-        nl->rc_angular = rc_angular;
-        nl->from_padded = false;
-        const int n = int(n_atoms);
-        const double rc = std::max(rc_radial, rc_angular);
-        std::vector<Geo> geo(n_structures);
-        int total_bins = 0;
-        for (int b = 0; b < n_structures; ++b) {
-            int na = int(h_struct_ptr[b + 1] - h_struct_ptr[b]);
-            geo[b] = make_geo(h_cells + 9 * b, h_pbc + 3 * b, rc, na, total_bins,
-                              int(h_struct_ptr[b]));
-            total_bins += geo[b].nb[0] * geo[b].nb[1] * geo[b].nb[2];
-        }
-        // working memory
-        Arena ar;
-        size_t o_geo = ar.add(sizeof(Geo) * n_structures);
-        size_t o_abin = ar.add(4 * size_t(n + 1));
-        size_t o_wrap = ar.add(12 * size_t(n + 1));
-        size_t o_cell = ar.add(12 * size_t(n + 1));
-        size_t o_bcnt = ar.add(4 * size_t(total_bins + 1));
-        size_t o_bst = ar.add(4 * size_t(total_bins + 2));
-        size_t o_bcur = ar.add(4 * size_t(total_bins + 1));
-        size_t o_batm = ar.add(4 * size_t(n + 1));
-        size_t o_cu = ar.add(4 * size_t(n + 1));
-        size_t o_cr = ar.add(4 * size_t(n + 1));
-        size_t o_ca = ar.add(4 * size_t(n + 1));
-        size_t o_flag = ar.add(16);
-        size_t o_scan = ar.add(4 * scan_tmp_ints(std::max(n, total_bins) + 1));
-        size_t o_indeg = ar.add(4 * size_t(n + 1));
-        size_t o_perm = ar.add(4 * size_t(total_bins + 1));
-        size_t o_rcnt = ar.add(4 * size_t(total_bins + 1));
-        size_t o_rst = ar.add(4 * size_t(total_bins + 2));
-        nl->work.reserve(ar.total);
-        char *base = nl->work.as<char>();
-        Work w;
-        w.geo = reinterpret_cast<Geo *>(base + o_geo);
-        w.atom_bin = reinterpret_cast<int32_t *>(base + o_abin);
-        w.atom_wrap = reinterpret_cast<int32_t *>(base + o_wrap);
-        w.atom_cell = reinterpret_cast<int32_t *>(base + o_cell);
-        w.bin_count = reinterpret_cast<int32_t *>(base + o_bcnt);
-        w.bin_start = reinterpret_cast<int32_t *>(base + o_bst);
-        w.bin_cursor = reinterpret_cast<int32_t *>(base + o_bcur);
-        w.bin_atoms = reinterpret_cast<int32_t *>(base + o_batm);
-        w.cnt_union = reinterpret_cast<int32_t *>(base + o_cu);
-        w.cnt_r = reinterpret_cast<int32_t *>(base + o_cr);
-        w.cnt_a = reinterpret_cast<int32_t *>(base + o_ca);
-        w.flag = reinterpret_cast<int32_t *>(base + o_flag);
-        w.scan_tmp = reinterpret_cast<int32_t *>(base + o_scan);
-        w.indeg = reinterpret_cast<int32_t *>(base + o_indeg);
-        RUNE_HIP_CHECK(hipMemcpyAsync(w.geo, geo.data(), sizeof(Geo) * n_structures,
-                                      hipMemcpyHostToDevice, s));
+// Shared body of rune_nlist_build and rune_nlist_update.  skin == 0: one
+// enumeration at the model cutoffs.  skin > 0: when `search` is set, the
+// candidates within max(rc) + skin are enumerated into nl->cand_keys (and the
+// positions kept in nl->ref_pos); either way the candidates are then re-tested
+// at the current positions into nl->keys.  The rest (counts, records,
+// transpose) is the same for all paths, so all give identical records.
+static void build_lists(rune_nlist *nl, int64_t n_atoms, const double *d_positions,
+                        int32_t n_structures, const int64_t *h_struct_ptr, const double *h_cells,
+                        const int32_t *h_pbc, double rc_radial, double rc_angular,
+                        int32_t max_radial, int32_t max_angular, double skin, bool search,
+                        hipStream_t s, int64_t *n_records) {
+    set_structures(nl, n_atoms, n_structures, h_struct_ptr, s);
+    nl->rc_radial = rc_radial;
+    nl->rc_angular = rc_angular;
+    nl->from_padded = false;
+    const int n = int(n_atoms);
+    const double rc = std::max(rc_radial, rc_angular), rc_bin = rc + skin;
+    std::vector<Geo> geo(n_structures);
+    int total_bins = 0;
+    for (int b = 0; b < n_structures; ++b) {
+        int na = int(h_struct_ptr[b + 1] - h_struct_ptr[b]);
+        geo[b] = make_geo(h_cells + 9 * b, h_pbc + 3 * b, rc_bin, na, total_bins,
+                          int(h_struct_ptr[b]));
+        total_bins += geo[b].nb[0] * geo[b].nb[1] * geo[b].nb[2];
+    }
+    // working memory
+    Arena ar;
+    size_t o_geo = ar.add(sizeof(Geo) * n_structures);
+    size_t o_abin = ar.add(4 * size_t(n + 1));
+    size_t o_wrap = ar.add(12 * size_t(n + 1));
+    size_t o_cell = ar.add(12 * size_t(n + 1));
+    size_t o_bcnt = ar.add(4 * size_t(total_bins + 1));
+    size_t o_bst = ar.add(4 * size_t(total_bins + 2));
+    size_t o_bcur = ar.add(4 * size_t(total_bins + 1));
+    size_t o_batm = ar.add(4 * size_t(n + 1));
+    size_t o_cu = ar.add(4 * size_t(n + 1));
+    size_t o_cr = ar.add(4 * size_t(n + 1));
+    size_t o_ca = ar.add(4 * size_t(n + 1));
+    size_t o_flag = ar.add(16);
+    size_t o_scan = ar.add(4 * scan_tmp_ints(std::max(n, total_bins) + 1));
+    size_t o_indeg = ar.add(4 * size_t(n + 1));
+    size_t o_perm = ar.add(4 * size_t(total_bins + 1));
+    size_t o_rcnt = ar.add(4 * size_t(total_bins + 1));
+    size_t o_rst = ar.add(4 * size_t(total_bins + 2));
+    nl->work.reserve(ar.total);
+    char *base = nl->work.as<char>();
+    Work w;
+    w.geo = reinterpret_cast<Geo *>(base + o_geo);
+    w.atom_bin = reinterpret_cast<int32_t *>(base + o_abin);
+    w.atom_wrap = reinterpret_cast<int32_t *>(base + o_wrap);
+    w.atom_cell = reinterpret_cast<int32_t *>(base + o_cell);
+    w.bin_count = reinterpret_cast<int32_t *>(base + o_bcnt);
+    w.bin_start = reinterpret_cast<int32_t *>(base + o_bst);
+    w.bin_cursor = reinterpret_cast<int32_t *>(base + o_bcur);
+    w.bin_atoms = reinterpret_cast<int32_t *>(base + o_batm);
+    w.cnt_union = reinterpret_cast<int32_t *>(base + o_cu);
+    w.cnt_r = reinterpret_cast<int32_t *>(base + o_cr);
+    w.cnt_a = reinterpret_cast<int32_t *>(base + o_ca);
+    w.flag = reinterpret_cast<int32_t *>(base + o_flag);
+    w.scan_tmp = reinterpret_cast<int32_t *>(base + o_scan);
+    w.indeg = reinterpret_cast<int32_t *>(base + o_indeg);
+    RUNE_HIP_CHECK(hipMemcpyAsync(w.geo, geo.data(), sizeof(Geo) * n_structures,
+                                  hipMemcpyHostToDevice, s));
+    RUNE_HIP_CHECK(hipMemsetAsync(w.flag, 0, 16, s));
+    nl->ptr.reserve(4 * size_t(n + 1));
+    nl->view.reserve(16 * size_t(n + 1));
+    int gb = ceil_div(std::max(n, 1), kThreads);
+    const int32_t *sptr = nl->sptr.as<int32_t>();
+    // one row of sorted keys per centre, as wide as the larger neighbour limit
+    const int cap = std::max(max_radial, max_angular);
+    nl->keys.reserve(8 * size_t(std::max(n, 1)) * size_t(cap));
+    const double rc2_r = rc_radial * rc_radial, rc2_a = rc_angular * rc_angular, rc2 = rc * rc;
+    const bool binned = skin == 0.0 || search;
+    if (binned) {
         RUNE_HIP_CHECK(hipMemsetAsync(w.bin_count, 0, 4 * size_t(total_bins + 1), s));
         RUNE_HIP_CHECK(hipMemsetAsync(w.bin_cursor, 0, 4 * size_t(total_bins + 1), s));
-        RUNE_HIP_CHECK(hipMemsetAsync(w.flag, 0, 16, s));
-        nl->ptr.reserve(4 * size_t(n + 1));
-        nl->view.reserve(16 * size_t(n + 1));
-        int gb = ceil_div(std::max(n, 1), kThreads);
-        const int32_t *sptr = nl->sptr.as<int32_t>();
-        // one row of sorted keys per centre, as wide as the larger neighbour limit
-        const int cap = std::max(max_radial, max_angular);
-        nl->keys.reserve(8 * size_t(std::max(n, 1)) * size_t(cap));
-        if (n > 0) {
+        if (n > 0)
             hipLaunchKernelGGL(bin_atoms, dim3(gb), dim3(kThreads), 0, s, n, d_positions, sptr,
                                n_structures, w.geo, w.atom_bin, w.atom_wrap, w.atom_cell,
                                w.bin_count);
-        }
         exclusive_scan(w.bin_count, w.bin_start, total_bins, w.scan_tmp, s);
-        if (n > 0) {
+        if (n > 0)
             hipLaunchKernelGGL(fill_bins, dim3(gb), dim3(kThreads), 0, s, n, w.atom_bin,
                                w.bin_start, w.bin_cursor, w.bin_atoms);
+    }
+    if (skin == 0.0) {
+        if (n > 0)
             hipLaunchKernelGGL(enumerate_flat, dim3(ceil_div(n, 4)), dim3(256), 0, s, n,
                                d_positions, sptr, n_structures, w.geo, w.atom_wrap, w.atom_cell,
-                               w.bin_start, w.bin_atoms, rc_radial * rc_radial,
-                               rc_angular * rc_angular, rc * rc, max_radial, max_angular, cap,
-                               w.cnt_union, w.cnt_r, w.cnt_a, w.flag, nl->keys.as<uint64_t>());
+                               w.bin_start, w.bin_atoms, rc2_r, rc2_a, rc2, max_radial,
+                               max_angular, cap, w.cnt_union, w.cnt_r, w.cnt_a, w.flag,
+                               nl->keys.as<uint64_t>());
+    } else {
+        if (search) {
+            // candidates within rc + skin, all of class 0 (sorted by (j, S));
+            // a row that overflows the candidate width widens it and repeats
+            const double rb2 = rc_bin * rc_bin;
+            nl->cand_cnt.reserve(4 * size_t(n + 1));
+            for (int attempt = 0;; ++attempt) {
+                nl->cand_keys.reserve(8 * size_t(std::max(n, 1)) * size_t(nl->cand_cap));
+                if (n > 0)
+                    hipLaunchKernelGGL(enumerate_flat, dim3(ceil_div(n, 4)), dim3(256), 0, s, n,
+                                       d_positions, sptr, n_structures, w.geo, w.atom_wrap,
+                                       w.atom_cell, w.bin_start, w.bin_atoms, rb2, rb2, rb2,
+                                       nl->cand_cap, nl->cand_cap, nl->cand_cap,
+                                       nl->cand_cnt.as<int32_t>(), w.cnt_r, w.cnt_a, w.flag,
+                                       nl->cand_keys.as<uint64_t>());
+                RUNE_HIP_CHECK(hipGetLastError());
+                int32_t over = 0;
+                RUNE_HIP_CHECK(hipMemcpyAsync(&over, w.flag, 4, hipMemcpyDeviceToHost, s));
+                RUNE_HIP_CHECK(hipStreamSynchronize(s));
+                if (!over) break;
+                RUNE_REQUIRE(attempt < 3, RUNE_ERR_STATE, "neighbour candidate search did not fit");
+                std::vector<int32_t> cc(n);
+                RUNE_HIP_CHECK(hipMemcpy(cc.data(), nl->cand_cnt.ptr, 4 * size_t(n),
+                                         hipMemcpyDeviceToHost));
+                const int most = n ? *std::max_element(cc.begin(), cc.end()) : 0;
+                nl->cand_cap = std::max(nl->cand_cap + 1, most + most / 4 + 8);
+                RUNE_HIP_CHECK(hipMemsetAsync(w.flag, 0, 16, s));
+            }
+            nl->ref_pos.reserve(24 * size_t(std::max(n, 1)));
+            if (n > 0)
+                RUNE_HIP_CHECK(hipMemcpyAsync(nl->ref_pos.ptr, d_positions, 24 * size_t(n),
+                                              hipMemcpyDeviceToDevice, s));
         }
-        exclusive_scan(w.cnt_union, nl->ptr.as<int32_t>(), n, w.scan_tmp, s);
-        RUNE_HIP_CHECK(hipGetLastError());
-        int32_t host[2] = {0, 0};
-        RUNE_HIP_CHECK(hipMemcpyAsync(&host[0], nl->ptr.as<int32_t>() + n, 4,
-                                      hipMemcpyDeviceToHost, s));
-        RUNE_HIP_CHECK(hipMemcpyAsync(&host[1], w.flag, 4, hipMemcpyDeviceToHost, s));
-        RUNE_HIP_CHECK(hipStreamSynchronize(s));
-        if (host[1]) {
-            std::vector<int32_t> cr(n), ca(n);
-            RUNE_HIP_CHECK(hipMemcpy(cr.data(), w.cnt_r, 4 * size_t(n), hipMemcpyDeviceToHost));
-            RUNE_HIP_CHECK(hipMemcpy(ca.data(), w.cnt_a, 4 * size_t(n), hipMemcpyDeviceToHost));
-            nl->n_records = 0;
-            throw Error(RUNE_ERR_OVERFLOW, overflow_message(cr, ca, max_radial, max_angular));
-        }
-        int64_t e = host[0];
-        nl->n_records = e;
-        size_t ecap = size_t(std::max<int64_t>(e, 1));
-        nl->nbr.reserve(4 * ecap);
-        nl->shift.reserve(12 * ecap);
-        nl->vec.reserve(16 * ecap);
-        nl->ctr.reserve(4 * ecap);
-        if (n > 0) {
-            hipLaunchKernelGGL(decode_wave, dim3(ceil_div(n, 4)), dim3(256), 0, s, n, d_positions,
-                               sptr, n_structures, w.geo, cap, nl->ptr.as<int32_t>(), w.cnt_r,
-                               w.cnt_a, nl->keys.as<uint64_t>(), nl->view.as<int32_t>(),
-                               nl->nbr.as<int32_t>(), nl->shift.as<int32_t>(),
-                               nl->vec.as<float4>(), nl->ctr.as<int32_t>());
-        }
-        RUNE_HIP_CHECK(hipGetLastError());
-        build_transpose(nl, w.indeg, w.scan_tmp, s);
-        // processing order: atoms bin by bin, bins in Morton order
+        if (n > 0)
+            hipLaunchKernelGGL(refilter_wave, dim3(ceil_div(n, 4)), dim3(256), 0, s, n,
+                               d_positions, sptr, n_structures, w.geo,
+                               nl->cand_keys.as<uint64_t>(), nl->cand_cap,
+                               nl->cand_cnt.as<int32_t>(), rc2_r, rc2_a, rc2, max_radial,
+                               max_angular, cap, w.cnt_union, w.cnt_r, w.cnt_a, w.flag,
+                               nl->keys.as<uint64_t>());
+    }
+    exclusive_scan(w.cnt_union, nl->ptr.as<int32_t>(), n, w.scan_tmp, s);
+    RUNE_HIP_CHECK(hipGetLastError());
+    int32_t host[2] = {0, 0};
+    RUNE_HIP_CHECK(hipMemcpyAsync(&host[0], nl->ptr.as<int32_t>() + n, 4,
+                                  hipMemcpyDeviceToHost, s));
+    RUNE_HIP_CHECK(hipMemcpyAsync(&host[1], w.flag, 4, hipMemcpyDeviceToHost, s));
+    RUNE_HIP_CHECK(hipStreamSynchronize(s));
+    if (host[1]) {
+        std::vector<int32_t> cr(n), ca(n);
+        RUNE_HIP_CHECK(hipMemcpy(cr.data(), w.cnt_r, 4 * size_t(n), hipMemcpyDeviceToHost));
+        RUNE_HIP_CHECK(hipMemcpy(ca.data(), w.cnt_a, 4 * size_t(n), hipMemcpyDeviceToHost));
+        nl->n_records = 0;
+        throw Error(RUNE_ERR_OVERFLOW, overflow_message(cr, ca, max_radial, max_angular));
+    }
+    int64_t e = host[0];
+    nl->n_records = e;
+    size_t ecap = size_t(std::max<int64_t>(e, 1));
+    nl->nbr.reserve(4 * ecap);
+    nl->shift.reserve(12 * ecap);
+    nl->vec.reserve(16 * ecap);
+    nl->ctr.reserve(4 * ecap);
+    if (n > 0) {
+        hipLaunchKernelGGL(decode_wave, dim3(ceil_div(n, 4)), dim3(256), 0, s, n, d_positions,
+                           sptr, n_structures, w.geo, cap, nl->ptr.as<int32_t>(), w.cnt_r,
+                           w.cnt_a, nl->keys.as<uint64_t>(), nl->view.as<int32_t>(),
+                           nl->nbr.as<int32_t>(), nl->shift.as<int32_t>(), nl->vec.as<float4>(),
+                           nl->ctr.as<int32_t>());
+    }
+    RUNE_HIP_CHECK(hipGetLastError());
+    build_transpose(nl, w.indeg, w.scan_tmp, s);
+    // processing order: atoms bin by bin, bins in Morton order (kept from the
+    // last binning when the candidates are reused; it only orders the work)
+    if (binned) {
         nl->order.reserve(4 * size_t(std::max(n, 1)));
         if (n > 0) {
             std::vector<int32_t> &perm = nl->h_perm;   // outlives the asynchronous upload
@@ -745,7 +864,80 @@ extern "C" int rune_nlist_build(rune_nlist *nl, int64_t n_atoms, const double *d
             RUNE_HIP_CHECK(hipGetLastError());
         }
         nl->has_order = true;
-        if (n_records) *n_records = e;
+    }
+    if (n_records) *n_records = e;
+}
+
+static void check_build_args(rune_nlist *nl, int64_t n_atoms, const double *d_positions,
+                             const double *h_cells, const int32_t *h_pbc, double rc_radial,
+                             double rc_angular, int32_t max_radial, int32_t max_angular) {
+    RUNE_REQUIRE(nl && (d_positions || n_atoms == 0) && h_cells && h_pbc, RUNE_ERR_ARGUMENT,
+                 "null argument");
+    RUNE_REQUIRE(rc_radial > 0 && rc_angular > 0, RUNE_ERR_ARGUMENT,
+                 "radial and angular cutoffs must be positive");
+    RUNE_REQUIRE(max_radial >= 1 && max_angular >= 1, RUNE_ERR_ARGUMENT,
+                 "radial and angular max-neighbor counts must be positive");
+}
+
+extern "C" int rune_nlist_build(rune_nlist *nl, int64_t n_atoms, const double *d_positions,
+                                int32_t n_structures, const int64_t *h_struct_ptr,
+                                const double *h_cells, const int32_t *h_pbc, double rc_radial,
+                                double rc_angular, int32_t max_radial, int32_t max_angular,
+                                void *stream, int64_t *n_records) {
+    return guarded([&] {
+        check_build_args(nl, n_atoms, d_positions, h_cells, h_pbc, rc_radial, rc_angular,
+                         max_radial, max_angular);
+        nl->cand_valid = false;
+        build_lists(nl, n_atoms, d_positions, n_structures, h_struct_ptr, h_cells, h_pbc,
+                    rc_radial, rc_angular, max_radial, max_angular, 0.0, true, as_stream(stream),
+                    n_records);
+    });
+}
+
+extern "C" int rune_nlist_update(rune_nlist *nl, int64_t n_atoms, const double *d_positions,
+                                 int32_t n_structures, const int64_t *h_struct_ptr,
+                                 const double *h_cells, const int32_t *h_pbc, double rc_radial,
+                                 double rc_angular, int32_t max_radial, int32_t max_angular,
+                                 double skin, void *stream, int64_t *n_records,
+                                 int32_t *searched) {
+    return guarded([&] {
+        check_build_args(nl, n_atoms, d_positions, h_cells, h_pbc, rc_radial, rc_angular,
+                         max_radial, max_angular);
+        RUNE_REQUIRE(skin > 0 && std::isfinite(skin), RUNE_ERR_ARGUMENT, "skin must be positive");
+        RUNE_REQUIRE(n_structures >= 1 && h_struct_ptr, RUNE_ERR_ARGUMENT,
+                     "need at least one structure");
+        hipStream_t s = as_stream(stream);
+        // everything the candidates depend on besides the positions
+        std::vector<double> key;
+        key.reserve(6 + 13 * size_t(n_structures));
+        key.insert(key.end(), {double(n_atoms), rc_radial, rc_angular, double(max_radial),
+                               double(max_angular), skin});
+        for (int b = 0; b < n_structures; ++b) {
+            key.push_back(double(h_struct_ptr[b + 1]));
+            key.insert(key.end(), h_cells + 9 * b, h_cells + 9 * b + 9);
+            for (int d = 0; d < 3; ++d) key.push_back(h_pbc[3 * b + d] ? 1.0 : 0.0);
+        }
+        bool search = !nl->cand_valid || key != nl->cand_key;
+        if (!search && n_atoms > 0) {
+            int32_t *flag = nl->cand_flag.as<int32_t>();
+            RUNE_HIP_CHECK(hipMemsetAsync(flag, 0, 4, s));
+            hipLaunchKernelGGL(check_displacement, dim3(ceil_div(n_atoms, kThreads)),
+                               dim3(kThreads), 0, s, int(n_atoms), d_positions,
+                               nl->ref_pos.as<double>(), 0.25 * skin * skin, flag);
+            RUNE_HIP_CHECK(hipGetLastError());
+            int32_t moved = 0;
+            RUNE_HIP_CHECK(hipMemcpyAsync(&moved, flag, 4, hipMemcpyDeviceToHost, s));
+            RUNE_HIP_CHECK(hipStreamSynchronize(s));
+            search = moved != 0;
+        }
+        nl->cand_valid = false;
+        if (nl->cand_cap < 1) nl->cand_cap = std::max(max_radial, max_angular);
+        nl->cand_flag.reserve(16);
+        build_lists(nl, n_atoms, d_positions, n_structures, h_struct_ptr, h_cells, h_pbc,
+                    rc_radial, rc_angular, max_radial, max_angular, skin, search, s, n_records);
+        nl->cand_key = key;
+        nl->cand_valid = true;
+        if (searched) *searched = search ? 1 : 0;
     });
 }
 

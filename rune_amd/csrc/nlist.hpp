@@ -28,6 +28,15 @@ struct rune_nlist {
     rune::DeviceBuffer order;    // int32 [N]
     bool has_order = false;
     std::vector<int32_t> h_perm; // host bin ranks behind the last order upload
+    // skin reuse (rune_nlist_update): candidates within max(rc) + skin of the
+    // last search, the positions it saw, and what else it depended on
+    rune::DeviceBuffer cand_keys;   // uint64 [N, cand_cap], sorted per centre
+    rune::DeviceBuffer cand_cnt;    // int32 [N]
+    rune::DeviceBuffer ref_pos;     // fp64 [N, 3]
+    rune::DeviceBuffer cand_flag;   // int32 displacement flag
+    int cand_cap = 0;
+    bool cand_valid = false;
+    std::vector<double> cand_key;
     // working memory of the builder
     rune::DeviceBuffer work;
     rune::DeviceBuffer keys;     // uint64 [N, max(max_radial, max_angular)] sorted per centre
