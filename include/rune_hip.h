@@ -181,6 +181,24 @@ int rune_model_set_tensor(rune_model *model, const char *name, const float *h_da
 /* Check that every required tensor was given, pack and upload the weights. */
 int rune_model_finalize(rune_model *model);
 
+/* Create and finalize a model from its text artifact, so a C/C++ caller needs
+ * no PyTorch pickle: "mobius1" files (rune/mobius/export.py:120-146, read and
+ * validated as the GPUMD evaluator's read_model, rune/mobius/src/mobius.cu:
+ * 26-151, with its messages) or "nep4" / "nep4_zbl" files (reader of
+ * rune/nep/model.py:284-489; load_model of rune/nep/plugin.py:57-75 for
+ * *.txt).  The weights equal those of the PyTorch loaders bit for bit. */
+int rune_model_load(const char *path, rune_model **out);
+
+/* Cutoffs of a model and, for models made by rune_model_load, the neighbour
+ * limits its file names (0 for models made from a config).  Any output
+ * pointer may be NULL.  (The reference reads them from model_params.) */
+int rune_model_limits(const rune_model *model, double *rc_radial, double *rc_angular,
+                      int32_t *max_radial, int32_t *max_angular);
+
+/* Element symbol of type `type` (type ids follow the model's element order;
+ * "" when out of range or when the model was created without symbols). */
+const char *rune_model_element(const rune_model *model, int32_t type);
+
 /* Energies, forces and virials: Mobius.forward / NEP.forward
  * (rune/mobius/model.py:307-393, rune/nep/model.py:87-155).
  * d_types int32 [N]; outputs (device, may be NULL when not wanted):

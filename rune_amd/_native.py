@@ -77,6 +77,10 @@ def library():
         "rune_nlist_records": (i64, [vp]),
         "rune_model_create": (C.c_int, [C.POINTER(ModelConfig), C.POINTER(vp)]),
         "rune_model_destroy": (None, [vp]),
+        "rune_model_load": (C.c_int, [C.c_char_p, C.POINTER(vp)]),
+        "rune_model_limits": (C.c_int, [vp, C.POINTER(f64), C.POINTER(f64), C.POINTER(i32),
+                                        C.POINTER(i32)]),
+        "rune_model_element": (C.c_char_p, [vp, i32]),
         "rune_model_set_tensor": (C.c_int, [vp, C.c_char_p, vp, i64]),
         "rune_model_finalize": (C.c_int, [vp]),
         "rune_model_compute": (C.c_int, [vp, vp, vp, i32, i32, vp, vp, vp, vp, vp, vp]),
@@ -326,6 +330,30 @@ class NativeModel:
             _ptr(out["energies"]), _ptr(out["energy"]), _ptr(out.get("forces")),
             _ptr(out.get("virial")), _ptr(out.get("atom_virial")), _stream(dev)))
         return out
+
+    @classmethod
+    def load(cls, path):
+        """A model read natively from its text artifact (mobius.txt or nep.txt)."""
+        lib = library()
+        h = C.c_void_p()
+        check(lib.rune_model_load(str(path).encode(), C.byref(h)))
+        self = cls.__new__(cls)
+        self._h = h
+        with open(path, encoding="utf-8") as fh:
+            head = fh.readline().split()
+        self.family = FAMILY_MOBIUS if head and head[0] == "mobius1" else FAMILY_NEP
+        return self
+
+    def limits(self):
+        """(rc_radial, rc_angular, max_radial, max_angular); limits are 0 unless
+        the model was read from a text artifact."""
+        rr, ra, mr, ma = C.c_double(), C.c_double(), C.c_int32(), C.c_int32()
+        check(library().rune_model_limits(self._h, C.byref(rr), C.byref(ra), C.byref(mr),
+                                          C.byref(ma)))
+        return rr.value, ra.value, mr.value, ma.value
+
+    def element(self, t):
+        return library().rune_model_element(self._h, int(t)).decode()
 
     def workspace_bytes(self):
         return int(library().rune_model_workspace_bytes(self._h))

@@ -560,8 +560,6 @@ void local_backward(ModelImpl &m, LocalPlan &p, int N, float *dh, float *dq, int
 
 using namespace rune;
 
-struct rune_model : ModelImpl {};
-
 extern "C" const char *rune_last_error(void) { return g_last_error_ptr(); }
 
 extern "C" const char *rune_version(void) { return "rune_hip 0.1.0 (gfx950)"; }

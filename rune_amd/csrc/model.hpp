@@ -99,6 +99,8 @@ struct MessagePlan {
 struct ModelImpl {
     rune_model_config cfg{};
     std::vector<std::string> elements;
+    // neighbour limits from a text artifact (0 when created from a config)
+    int max_radial = 0, max_angular = 0;
     int Q = 0;
     std::map<std::string, int64_t> expected;
     std::map<std::string, std::vector<float>> host;
@@ -169,3 +171,6 @@ void local_backward(ModelImpl &m, LocalPlan &p, int N, float *dh, float *dq, int
                     hipStream_t s);
 
 }  // namespace rune
+
+// The C-ABI handle (include/rune_hip.h).
+struct rune_model : rune::ModelImpl {};
