@@ -213,6 +213,21 @@ int rune_model_compute(rune_model *model, const rune_nlist *nl, const int32_t *d
                        float *d_energies, float *d_energy, float *d_forces,
                        float *d_virial, float *d_atom_virial, void *stream);
 
+/* GPUMD-style per-atom outputs, accumulated (+=) in fp64 as GPUMD's
+ * potentials do (rune/mobius/src/force.cu:47-84): d_potential [N];
+ * d_force [3N] as three atom arrays x[0..N), y, z; d_virial [9N] as nine atom
+ * arrays in the order xx, yy, zz, xy, xz, yz, yx, zx, zy of -r (x) g attributed
+ * to the neighbour (the transpose of rune_model_compute's d_atom_virial).
+ * Any output pointer may be NULL. */
+int rune_model_compute_gpumd(rune_model *model, const rune_nlist *nl, const int32_t *d_types,
+                             double *d_potential, double *d_force, double *d_virial,
+                             void *stream);
+
+/* 1 when the model supports GPUMD's heat-current / HNEMD observables (models
+ * without message blocks: rune/mobius/src/mobius.cuh:18, the rejection of
+ * rune/mobius/install_gpumd.py:38-46), else 0. */
+int rune_model_supports_heat_current(const rune_model *model);
+
 /* Bytes of device workspace the handle currently holds. */
 int64_t rune_model_workspace_bytes(const rune_model *model);
 

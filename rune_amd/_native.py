@@ -81,6 +81,8 @@ def library():
         "rune_model_limits": (C.c_int, [vp, C.POINTER(f64), C.POINTER(f64), C.POINTER(i32),
                                         C.POINTER(i32)]),
         "rune_model_element": (C.c_char_p, [vp, i32]),
+        "rune_model_compute_gpumd": (C.c_int, [vp, vp, vp, vp, vp, vp, vp]),
+        "rune_model_supports_heat_current": (C.c_int, [vp]),
         "rune_model_set_tensor": (C.c_int, [vp, C.c_char_p, vp, i64]),
         "rune_model_finalize": (C.c_int, [vp]),
         "rune_model_compute": (C.c_int, [vp, vp, vp, i32, i32, vp, vp, vp, vp, vp, vp]),
@@ -351,6 +353,20 @@ class NativeModel:
         check(library().rune_model_limits(self._h, C.byref(rr), C.byref(ra), C.byref(mr),
                                           C.byref(ma)))
         return rr.value, ra.value, mr.value, ma.value
+
+    def compute_gpumd(self, nlist, types, potential=None, force=None, virial=None):
+        """Adds GPUMD-style fp64 per-atom outputs into the given device arrays
+        (potential [N], force [3N] SoA, virial [9N] SoA)."""
+        dev = nlist.device
+        types = types.to(device=dev, dtype=torch.int32).contiguous()
+        for t in (potential, force, virial):
+            assert t is None or (t.dtype == torch.float64 and t.is_contiguous())
+        check(library().rune_model_compute_gpumd(self._h, nlist.handle, _ptr(types),
+                                                 _ptr(potential), _ptr(force), _ptr(virial),
+                                                 _stream(dev)))
+
+    def supports_heat_current(self):
+        return bool(library().rune_model_supports_heat_current(self._h))
 
     def element(self, t):
         return library().rune_model_element(self._h, int(t)).decode()

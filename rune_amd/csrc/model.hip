@@ -666,6 +666,51 @@ extern "C" int rune_model_compute(rune_model *model, const rune_nlist *nl, const
     });
 }
 
+namespace rune {
+namespace {
+// GPUMD's per-atom arrays (rune/mobius/src/force.cu:47-84): potential[n],
+// forces as three atom arrays, the virial as nine atom arrays in the order
+// xx, yy, zz, xy, xz, yz, yx, zx, zy of -r (x) g, i.e. component (a, b) is
+// this library's atom virial W[b][a].  Added in fp64, one thread per atom.
+__global__ void k_gpumd_accumulate(int n, const float *e, const float *f, const float *w,
+                                   double *pot, double *force, double *vir) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    if (pot) pot[i] += double(e[i]);
+    if (force)
+        for (int d = 0; d < 3; ++d) force[size_t(d) * n + i] += double(f[3 * size_t(i) + d]);
+    if (vir) {
+        const int a[9] = {0, 1, 2, 0, 0, 1, 1, 2, 2}, b[9] = {0, 1, 2, 1, 2, 2, 0, 0, 1};
+        for (int k = 0; k < 9; ++k)
+            vir[size_t(k) * n + i] += double(w[9 * size_t(i) + 3 * b[k] + a[k]]);
+    }
+}
+}  // namespace
+}  // namespace rune
+
+extern "C" int rune_model_compute_gpumd(rune_model *model, const rune_nlist *nl,
+                                        const int32_t *d_types, double *d_potential,
+                                        double *d_force, double *d_virial, void *stream) {
+    return guarded([&] {
+        RUNE_REQUIRE(model && nl, RUNE_ERR_ARGUMENT, "null argument");
+        const int64_t n = nl->n_atoms;
+        hipStream_t s = as_stream(stream);
+        model->gpumd_out.reserve(4 * size_t(std::max<int64_t>(n, 1)) * 13);
+        float *e = model->gpumd_out.as<float>(), *f = e + n, *w = f + 3 * n;
+        compute(*model, nl, d_types, 1, d_virial != nullptr, e, nullptr, f, nullptr,
+                d_virial ? w : nullptr, s);
+        if (n > 0)
+            hipLaunchKernelGGL(k_gpumd_accumulate, dim3(ceil_div(n, 256)), dim3(256), 0, s,
+                               int(n), e, f, w, d_potential, d_force, d_virial);
+        RUNE_HIP_CHECK(hipGetLastError());
+    });
+}
+
+extern "C" int rune_model_supports_heat_current(const rune_model *model) {
+    return model && (model->cfg.family == RUNE_FAMILY_NEP || model->cfg.message_layers == 0) ? 1
+                                                                                            : 0;
+}
+
 extern "C" int64_t rune_model_workspace_bytes(const rune_model *model) {
     return model ? int64_t(model->work.bytes) : 0;
 }
