@@ -228,6 +228,23 @@ int rune_model_compute_gpumd(rune_model *model, const rune_nlist *nl, const int3
  * rune/mobius/install_gpumd.py:38-46), else 0. */
 int rune_model_supports_heat_current(const rune_model *model);
 
+/* Width Q of the descriptor vector q: n_desc_radial + n_desc_angular * num_L
+ * (the model's input_dim, rune/mobius/model.py:165). */
+int32_t rune_model_input_dim(const rune_model *model);
+
+/* Componentwise extrema of the raw descriptor values q (before q_scaler)
+ * over the atoms of `nl`: the per-batch step of compute_descriptor_min_max
+ * (rune/mobius/model.py:406-445, rune/nep/model.py:608-636) on the device.
+ * d_q_min / d_q_max: float [Q] device; accumulate != 0 combines with the
+ * values already there (the running min / max over batches), else they are
+ * overwritten (+inf / -inf for an empty list).  NaN propagates as in
+ * torch.amin / torch.minimum.  The scaler is then 1 / (max - min) where
+ * max - min > 1e-12, else 1 (set_descriptor_scaler_from_min_max,
+ * rune/mobius/model.py:446-465). */
+int rune_model_descriptor_extrema(rune_model *model, const rune_nlist *nl,
+                                  const int32_t *d_types, float *d_q_min, float *d_q_max,
+                                  int32_t accumulate, void *stream);
+
 /* Bytes of device workspace the handle currently holds. */
 int64_t rune_model_workspace_bytes(const rune_model *model);
 

@@ -83,6 +83,8 @@ def library():
         "rune_model_element": (C.c_char_p, [vp, i32]),
         "rune_model_compute_gpumd": (C.c_int, [vp, vp, vp, vp, vp, vp, vp]),
         "rune_model_supports_heat_current": (C.c_int, [vp]),
+        "rune_model_descriptor_extrema": (C.c_int, [vp, vp, vp, vp, vp, i32, vp]),
+        "rune_model_input_dim": (i32, [vp]),
         "rune_model_set_tensor": (C.c_int, [vp, C.c_char_p, vp, i64]),
         "rune_model_finalize": (C.c_int, [vp]),
         "rune_model_compute": (C.c_int, [vp, vp, vp, i32, i32, vp, vp, vp, vp, vp, vp]),
@@ -364,6 +366,24 @@ class NativeModel:
         check(library().rune_model_compute_gpumd(self._h, nlist.handle, _ptr(types),
                                                  _ptr(potential), _ptr(force), _ptr(virial),
                                                  _stream(dev)))
+
+    def descriptor_extrema(self, nlist, types, q_min=None, q_max=None):
+        """Raw-descriptor extrema over the atoms of ``nlist``; pass the previous
+        (q_min, q_max) to accumulate over batches.  Returns (q_min, q_max)."""
+        dev = nlist.device
+        types = types.to(device=dev, dtype=torch.int32).contiguous()
+        accumulate = q_min is not None
+        if not accumulate:
+            n = self.input_dim()
+            q_min = torch.empty(n, dtype=torch.float32, device=dev)
+            q_max = torch.empty(n, dtype=torch.float32, device=dev)
+        check(library().rune_model_descriptor_extrema(self._h, nlist.handle, _ptr(types),
+                                                      _ptr(q_min), _ptr(q_max), int(accumulate),
+                                                      _stream(dev)))
+        return q_min, q_max
+
+    def input_dim(self):
+        return int(library().rune_model_input_dim(self._h))
 
     def supports_heat_current(self):
         return bool(library().rune_model_supports_heat_current(self._h))

@@ -706,6 +706,83 @@ extern "C" int rune_model_compute_gpumd(rune_model *model, const rune_nlist *nl,
     });
 }
 
+namespace rune {
+namespace {
+// Column extrema of q [n, ldq] (first Q columns), one block per column; NaN
+// propagates as in torch.amin / torch.minimum.  accumulate: combine with the
+// values already in qmin / qmax.
+__device__ inline float nan_min(float a, float b) { return (a < b || a != a) ? a : b; }
+__device__ inline float nan_max(float a, float b) { return (a > b || a != a) ? a : b; }
+
+__global__ void __launch_bounds__(256) k_column_extrema(int n, const float *q, int ldq,
+                                                        float *qmin, float *qmax, int accumulate) {
+    __shared__ float smin[256], smax[256];
+    const int col = blockIdx.x, t = threadIdx.x;
+    float lo = INFINITY, hi = -INFINITY;
+    for (int i = t; i < n; i += 256) {
+        const float v = q[size_t(i) * ldq + col];
+        lo = nan_min(v, lo);
+        hi = nan_max(v, hi);
+    }
+    smin[t] = lo;
+    smax[t] = hi;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (t < w) {
+            smin[t] = nan_min(smin[t + w], smin[t]);
+            smax[t] = nan_max(smax[t + w], smax[t]);
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        qmin[col] = accumulate ? nan_min(smin[0], qmin[col]) : smin[0];
+        qmax[col] = accumulate ? nan_max(smax[0], qmax[col]) : smax[0];
+    }
+}
+}  // namespace
+}  // namespace rune
+
+extern "C" int rune_model_descriptor_extrema(rune_model *model, const rune_nlist *nl,
+                                             const int32_t *d_types, float *d_q_min,
+                                             float *d_q_max, int32_t accumulate, void *stream) {
+    return guarded([&] {
+        RUNE_REQUIRE(model && nl && d_q_min && d_q_max, RUNE_ERR_ARGUMENT, "null argument");
+        ModelImpl &m = *model;
+        RUNE_REQUIRE(m.finalized, RUNE_ERR_STATE, "model handle is not finalized");
+        if (!nl->from_padded)
+            RUNE_REQUIRE(nl->rc_radial == m.cfg.rc_radial && nl->rc_angular == m.cfg.rc_angular,
+                         RUNE_ERR_STATE, "neighbour list was built with other cutoffs");
+        hipStream_t s = as_stream(stream);
+        const int N = int(nl->n_atoms);
+        const DescTables &d = m.desc;
+        const int ldq = (m.Q + 3) & ~3;
+        Arena ar;
+        const size_t o_flag = ar.add(16);
+        const size_t o_q = ar.add(4 * size_t(std::max(N, 1)) * ldq);
+        const size_t o_s = ar.add(4 * size_t(std::max(N, 1)) * d.na * d.nlm);
+        m.work.reserve(ar.total);
+        char *base = m.work.as<char>();
+        int32_t *flag = reinterpret_cast<int32_t *>(base + o_flag);
+        RUNE_HIP_CHECK(hipMemsetAsync(flag, 0, 16, s));
+        if (N > 0)
+            hipLaunchKernelGGL(k_check_types, dim3(ceil_div(N, 256)), dim3(256), 0, s, N,
+                               d_types, m.cfg.n_types, flag);
+        int32_t hflag = 0;
+        RUNE_HIP_CHECK(hipMemcpyAsync(&hflag, flag, 4, hipMemcpyDeviceToHost, s));
+        RUNE_HIP_CHECK(hipStreamSynchronize(s));
+        RUNE_REQUIRE(hflag == 0, RUNE_ERR_TYPE, "atom type outside [0, n_types)");
+        float *q = reinterpret_cast<float *>(base + o_q);
+        if (N > 0)
+            descriptor_forward(d, records_of(nl), d_types, q, ldq,
+                               reinterpret_cast<float *>(base + o_s), s);
+        hipLaunchKernelGGL(k_column_extrema, dim3(m.Q), dim3(256), 0, s, N, q, ldq, d_q_min,
+                           d_q_max, int(accumulate != 0));
+        RUNE_HIP_CHECK(hipGetLastError());
+    });
+}
+
+extern "C" int32_t rune_model_input_dim(const rune_model *model) { return model ? model->Q : 0; }
+
 extern "C" int rune_model_supports_heat_current(const rune_model *model) {
     return model && (model->cfg.family == RUNE_FAMILY_NEP || model->cfg.message_layers == 0) ? 1
                                                                                             : 0;

@@ -56,3 +56,44 @@ def test_nep_supports_heat_current():
     model = seeded_nep(seed=9)
     native = N.NativeModel(model.params, model.state_dict(), N.FAMILY_NEP)
     assert native.supports_heat_current()
+
+
+@pytest.mark.parametrize("name", ["loc", "eq"])
+def test_descriptor_extrema_match_oracle(name):
+    """Per-batch extrema of the raw descriptor (compute_descriptor_min_max,
+    rune/mobius/model.py:406-445) against the oracle's descriptor, and the
+    running min / max over two batches."""
+    from oracle import model as OM
+    from oracle import neighbors as ONB
+    from rune_amd import _native as N
+    from rune_amd.api import Evaluator
+    p, w = load_weights(name, torch.float32)
+    _, w64 = load_weights(name, torch.float64)
+    ev = Evaluator(p, w, N.FAMILY_MOBIUS)
+    batches = [W.amorphous(seed=52, n_atoms=150), W.fcc_alloy(seed=53, reps=2)]
+    qmin = qmax = None
+    ref_min = ref_max = None
+    for s in batches:
+        types = ev.types_of(s.numbers)
+        nl = N.NeighborList().build(torch.as_tensor(s.positions, device="cuda"), [0, len(s)],
+                                    [s.cell], [np.ones(3, np.int32)], p["rcut_radial"],
+                                    p["rcut_angular"], p["max_neighbors_radial"],
+                                    p["max_neighbors_angular"])
+        one_min, one_max = ev.native.descriptor_extrema(nl, torch.as_tensor(types))
+        qmin, qmax = ev.native.descriptor_extrema(nl, torch.as_tensor(types), qmin, qmax) \
+            if qmin is not None else (one_min.clone(), one_max.clone())
+        onb = ONB.split(ONB.build(s.positions, s.cell, s.pbc, p["rcut_radial"],
+                                  p["rcut_angular"]))
+        mk = lambda k: OM.Edges(torch.as_tensor(onb[k][0]), torch.as_tensor(onb[k][1]),
+                                torch.as_tensor(onb[k][2], dtype=torch.float64))
+        q = OM._descriptor(w64, p, torch.as_tensor(s.positions), torch.as_tensor(types,
+                           dtype=torch.long), mk("radial"), mk("angular"))[3]
+        lo, hi = q.min(0).values, q.max(0).values
+        tol = 1e-5 * (1.0 + q.abs().max(0).values)
+        assert torch.all((one_min.cpu().double() - lo).abs() <= tol)
+        assert torch.all((one_max.cpu().double() - hi).abs() <= tol)
+        ref_min = lo if ref_min is None else torch.minimum(ref_min, lo)
+        ref_max = hi if ref_max is None else torch.maximum(ref_max, hi)
+    tol = 1e-5 * (1.0 + torch.maximum(ref_min.abs(), ref_max.abs()))
+    assert torch.all((qmin.cpu().double() - ref_min).abs() <= tol)
+    assert torch.all((qmax.cpu().double() - ref_max).abs() <= tol)
