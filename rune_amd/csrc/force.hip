@@ -9,36 +9,54 @@
 namespace rune {
 namespace {
 
-__global__ void k_forces(Records r, const float4 *g, float *forces, float *atom_virial) {
-    int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= r.n_atoms) return;
-    float fx = 0.0f, fy = 0.0f, fz = 0.0f;
-    for (int e = r.ptr[i]; e < r.ptr[i + 1]; ++e) {
-        float4 v = g[e];
-        fx += v.x;
-        fy += v.y;
-        fz += v.z;
-    }
+// Eight lanes per atom: lane j of the atom's group takes records j, j + 8,
+// ... of its own list (+g) and of its transposed list (-g, virial), then the
+// group sums with a fixed xor tree, so the result is the same on every call.
+constexpr int kForceLanes = 8;
+
+__global__ void __launch_bounds__(256) k_forces(Records r, const float4 *g, float *forces,
+                                                float *atom_virial) {
+    const int tid = blockIdx.x * blockDim.x + threadIdx.x;
+    const int i = tid / kForceLanes, j = tid % kForceLanes;
+    const bool on = i < r.n_atoms;
+    float f[3] = {0.0f, 0.0f, 0.0f};
     float w[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
-    for (int t = r.tptr[i]; t < r.tptr[i + 1]; ++t) {
-        int e = r.tidx[t];
-        float4 v = g[e];
-        fx -= v.x;
-        fy -= v.y;
-        fz -= v.z;
-        if (atom_virial) {
-            float4 d = r.vec[e];
-            float gv[3] = {v.x, v.y, v.z}, rv[3] = {d.x, d.y, d.z};
+    if (on) {
+        for (int e = r.ptr[i] + j; e < r.ptr[i + 1]; e += kForceLanes) {
+            const float4 v = g[e];
+            f[0] += v.x;
+            f[1] += v.y;
+            f[2] += v.z;
+        }
+        for (int t = r.tptr[i] + j; t < r.tptr[i + 1]; t += kForceLanes) {
+            const int e = r.tidx[t];
+            const float4 v = g[e];
+            f[0] -= v.x;
+            f[1] -= v.y;
+            f[2] -= v.z;
+            if (atom_virial) {
+                const float4 d = r.vec[e];
+                const float gv[3] = {v.x, v.y, v.z}, rv[3] = {d.x, d.y, d.z};
 #pragma unroll
-            for (int a = 0; a < 3; ++a)
+                for (int a = 0; a < 3; ++a)
 #pragma unroll
-                for (int b = 0; b < 3; ++b) w[3 * a + b] -= gv[a] * rv[b];
+                    for (int b = 0; b < 3; ++b) w[3 * a + b] -= gv[a] * rv[b];
+            }
         }
     }
+    // every lane of the wave takes part in the shuffles
+#pragma unroll
+    for (int off = kForceLanes / 2; off > 0; off >>= 1) {
+#pragma unroll
+        for (int a = 0; a < 3; ++a) f[a] += __shfl_xor(f[a], off, kForceLanes);
+#pragma unroll
+        for (int k = 0; k < 9; ++k) w[k] += __shfl_xor(w[k], off, kForceLanes);
+    }
+    if (!on || j != 0) return;
     if (forces) {
-        forces[3 * i + 0] = fx;
-        forces[3 * i + 1] = fy;
-        forces[3 * i + 2] = fz;
+        forces[3 * i + 0] = f[0];
+        forces[3 * i + 1] = f[1];
+        forces[3 * i + 2] = f[2];
     }
     if (atom_virial)
         for (int k = 0; k < 9; ++k) atom_virial[9 * size_t(i) + k] = w[k];
@@ -69,7 +87,8 @@ __global__ void __launch_bounds__(256) k_structure_sum(const int32_t *sptr, cons
 void forces_and_virial(const Records &r, const float4 *g, float *forces, float *atom_virial,
                        hipStream_t s) {
     if (r.n_atoms == 0) return;
-    hipLaunchKernelGGL(k_forces, dim3(ceil_div(r.n_atoms, 256)), dim3(256), 0, s, r, g, forces,
+    hipLaunchKernelGGL(k_forces, dim3(ceil_div(int64_t(r.n_atoms) * kForceLanes, 256)), dim3(256),
+                       0, s, r, g, forces,
                        atom_virial);
     RUNE_HIP_CHECK(hipGetLastError());
 }

@@ -465,11 +465,29 @@ __global__ void transpose_centres(int64_t e, const int32_t *tidx, const int32_t 
     if (t < e) tctr[t] = ctr[tidx[t]];
 }
 
-__global__ void sort_in(int n, const int32_t *tptr, int32_t *tidx) {
-    int a = blockIdx.x * blockDim.x + threadIdx.x;
+// Each atom's transposed records in ascending record order: one atom per
+// wave, ranked in LDS (record ids are distinct, so each value's rank is the
+// number of smaller ones); an atom with more than kWaveKeys falls back to
+// lane 0's insertion sort in global memory.
+__global__ void __launch_bounds__(256) sort_in(int n, const int32_t *tptr, int32_t *tidx) {
+    __shared__ int32_t kl[4][kWaveKeys];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int a = blockIdx.x * 4 + wave;
     if (a >= n) return;
     int32_t *k = tidx + tptr[a];
-    int c = tptr[a + 1] - tptr[a];
+    const int c = tptr[a + 1] - tptr[a];
+    if (c <= kWaveKeys) {
+        for (int p = lane; p < c; p += kWave) kl[wave][p] = k[p];
+        wave_fence();
+        for (int p = lane; p < c; p += kWave) {
+            const int32_t x = kl[wave][p];
+            int rank = 0;
+            for (int b = 0; b < c; ++b) rank += kl[wave][b] < x ? 1 : 0;
+            k[rank] = x;
+        }
+        return;
+    }
+    if (lane != 0) return;
     for (int p = 1; p < c; ++p) {
         int32_t x = k[p];
         int q = p - 1;
@@ -607,7 +625,7 @@ void build_transpose(rune_nlist *nl, int32_t *indeg, int32_t *scan_tmp, hipStrea
         hipLaunchKernelGGL(fill_in, dim3(ceil_div(e, kThreads)), dim3(kThreads), 0, s, e,
                            nl->nbr.as<int32_t>(), nl->tptr.as<int32_t>(), indeg,
                            nl->tidx.as<int32_t>());
-        hipLaunchKernelGGL(sort_in, dim3(ceil_div(n, kThreads)), dim3(kThreads), 0, s, n,
+        hipLaunchKernelGGL(sort_in, dim3(ceil_div(n, 4)), dim3(256), 0, s, n,
                            nl->tptr.as<int32_t>(), nl->tidx.as<int32_t>());
     }
     nl->tctr.reserve(sizeof(int32_t) * std::max<int64_t>(e, 1));
