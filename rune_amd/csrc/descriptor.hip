@@ -98,6 +98,24 @@ __device__ inline void powers(float x, float y, float z, int l_max, Powers &p) {
     }
 }
 
+// sum_k c[k] f[k] over one padded c-table row (16-byte loads; the padding is
+// zero and f is zero there, so the sum equals the unpadded one term by term).
+template <int KMAX>
+__device__ inline float row_dot(const float *row, int k4, const float *f) {
+    const float4 *r4 = reinterpret_cast<const float4 *>(row);
+    float a = 0.0f;
+#pragma unroll
+    for (int q = 0; q < KMAX / 4; ++q) {
+        if (4 * q >= k4) break;
+        const float4 c = r4[q];
+        a += c.x * f[4 * q];
+        a += c.y * f[4 * q + 1];
+        a += c.z * f[4 * q + 2];
+        a += c.w * f[4 * q + 3];
+    }
+    return a;
+}
+
 // z-polynomial of order L, |m| = n1 (descriptor.py:601-613) and d/dz.
 __device__ inline void zpoly(const DescTables &t, int L, int n1, const Powers &p, float &zf,
                              float &zfp) {
@@ -232,19 +250,13 @@ __global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Reco
     for (int e = rb + lane; e < re; e += kWave) {
         float4 v = r.vec[e];
         int tj = types[r.nbr[e]];
-        float f[kMaxKr];
+        float f[kMaxKr] = {};
         chebyshev<kMaxKr>(v.w, t.rc_r, t.kr, f);
-        const float *row = t.c_radial + size_t(ti * t.n_types + tj) * t.nr * t.kr;
+        const float *row = t.c_radial + size_t(ti * t.n_types + tj) * t.nr * t.kr4;
 #pragma unroll
         for (int n = 0; n < kMaxNr; ++n) {
             if (n >= t.nr) break;
-            float a = 0.0f;
-#pragma unroll
-            for (int k = 0; k < kMaxKr; ++k) {
-                if (k >= t.kr) break;
-                a += row[n * t.kr + k] * f[k];
-            }
-            qr[n] += a;
+            qr[n] += row_dot<kMaxKr>(row + n * t.kr4, t.kr4, f);
         }
     }
 #pragma unroll
@@ -266,18 +278,10 @@ __global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Reco
         if (e < ae) {
             float4 v = r.vec[e];
             int tj = types[r.nbr[e]];
-            float f[kMaxKa];
+            float f[kMaxKa] = {};
             chebyshev<kMaxKa>(v.w, t.rc_a, t.ka, f);
-            const float *row = t.c_angular + size_t(ti * t.n_types + tj) * t.na * t.ka;
-            for (int n = 0; n < na; ++n) {
-                float a = 0.0f;
-#pragma unroll
-                for (int k = 0; k < kMaxKa; ++k) {
-                    if (k >= t.ka) break;
-                    a += row[n * t.ka + k] * f[k];
-                }
-                gl[n] = a;
-            }
+            const float *row = t.c_angular + size_t(ti * t.n_types + tj) * t.na * t.ka4;
+            for (int n = 0; n < na; ++n) gl[n] = row_dot<kMaxKa>(row + n * t.ka4, t.ka4, f);
             float inv = 1.0f / fmaxf(v.w, 1.0e-12f);
             Powers p;
             powers(v.x * inv, v.y * inv, v.z * inv, t.l_max, p);
@@ -402,38 +406,37 @@ __global__ void __launch_bounds__(kWave) k_descriptor_reverse(
         bool in_r = e >= rb && e < re;
         bool in_a = e >= ab && e < ae;
         if (want_grad && in_r) {
-            float f[kMaxKr], fp[kMaxKr];
+            float f[kMaxKr] = {}, fp[kMaxKr] = {};
             chebyshev_d<kMaxKr>(d, t.rc_r, t.kr, f, fp);
-            const float *row = t.c_radial + size_t(ti * t.n_types + tj) * t.nr * t.kr;
+            const float *row = t.c_radial + size_t(ti * t.n_types + tj) * t.nr * t.kr4;
             float gs = 0.0f;
-            for (int n = 0; n < t.nr; ++n) {
-                float a = 0.0f;
-#pragma unroll
-                for (int k = 0; k < kMaxKr; ++k) {
-                    if (k >= t.kr) break;
-                    a += row[n * t.kr + k] * fp[k];
-                }
-                gs += dqL[n] * a;
-            }
+            for (int n = 0; n < t.nr; ++n) gs += dqL[n] * row_dot<kMaxKr>(row + n * t.kr4, t.kr4, fp);
             gx += gs * ux;
             gy += gs * uy;
             gz += gs * uz;
         }
         if (want_grad && in_a) {
-            float f[kMaxKa], fp[kMaxKa];
+            float f[kMaxKa] = {}, fp[kMaxKa] = {};
             chebyshev_d<kMaxKa>(d, t.rc_a, t.ka, f, fp);
-            const float *row = t.c_angular + size_t(ti * t.n_types + tj) * t.na * t.ka;
+            const float *row = t.c_angular + size_t(ti * t.n_types + tj) * t.na * t.ka4;
             float gn[kMaxNa], gnp[kMaxNa];
 #pragma unroll
             for (int n = 0; n < kMaxNa; ++n) {
                 float a = 0.0f, b = 0.0f;
                 if (n < na) {
+                    const float4 *r4 = reinterpret_cast<const float4 *>(row + n * t.ka4);
 #pragma unroll
-                    for (int k = 0; k < kMaxKa; ++k) {
-                        if (k >= t.ka) break;
-                        float c = row[n * t.ka + k];
-                        a += c * f[k];
-                        b += c * fp[k];
+                    for (int q = 0; q < kMaxKa / 4; ++q) {
+                        if (4 * q >= t.ka4) break;
+                        const float4 c = r4[q];
+                        a += c.x * f[4 * q];
+                        b += c.x * fp[4 * q];
+                        a += c.y * f[4 * q + 1];
+                        b += c.y * fp[4 * q + 1];
+                        a += c.z * f[4 * q + 2];
+                        b += c.z * fp[4 * q + 2];
+                        a += c.w * f[4 * q + 3];
+                        b += c.w * fp[4 * q + 3];
                     }
                 }
                 gn[n] = a;

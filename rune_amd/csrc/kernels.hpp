@@ -22,8 +22,9 @@ struct DescTables {
     int num_L, Q;                 // angular invariants per channel, q width
     int has_q[6];                 // q222 q1111 q112 q123 q233 q134
     float rc_r, rc_a;
-    const float *c_radial;        // [T,T,nr,kr]
-    const float *c_angular;       // [T,T,na,ka]
+    int kr4, ka4;                 // kr, ka rounded up to 4: row length of the packed c tables
+    const float *c_radial;        // [T,T,nr,kr4], zero past kr
+    const float *c_angular;       // [T,T,na,ka4], zero past ka
     const float *z;               // Z_L[n1][p] flattened, offsets z_off[L]
     int z_off[kMaxL + 2];
     const float *c3b;             // [80]

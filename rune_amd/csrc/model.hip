@@ -154,8 +154,20 @@ std::vector<float> pad_rows(const std::vector<float> &w, int rows, int cols) {
 
 static void pack_descriptor(ModelImpl &m, Packer &pk, std::map<std::string, size_t> &off) {
     const rune_model_config &c = m.cfg;
-    off["c_radial"] = pk.put(m.tensor("descriptor.radial.c_table"));
-    off["c_angular"] = pk.put(m.tensor("descriptor.angular.c_table"));
+    // c tables with each (t1, t2, n) row padded with zeros to a multiple of 4,
+    // so the descriptor kernels read them as 16-byte vectors
+    auto padded = [](const std::vector<float> &t, int k, int k4) {
+        const size_t rows = t.size() / size_t(k);
+        std::vector<float> out(rows * k4, 0.0f);
+        for (size_t r = 0; r < rows; ++r)
+            std::copy(t.begin() + r * k, t.begin() + (r + 1) * k, out.begin() + r * k4);
+        return out;
+    };
+    m.desc.kr4 = (c.k_radial + 3) & ~3;
+    m.desc.ka4 = (c.k_angular + 3) & ~3;
+    off["c_radial"] = pk.put(padded(m.tensor("descriptor.radial.c_table"), c.k_radial, m.desc.kr4));
+    off["c_angular"] =
+        pk.put(padded(m.tensor("descriptor.angular.c_table"), c.k_angular, m.desc.ka4));
     std::vector<float> z;
     int zo = 0;
     for (int L = 1; L <= 8; ++L) {
