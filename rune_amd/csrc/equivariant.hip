@@ -97,7 +97,7 @@ struct EqArgs {
     Records r;
     int H, D, G, C, lq, nq, NG, NP, kb, na, nlm;
     int S;                    // records in flight per wave (lane slots of 64 / S lanes)
-    int gmode;                // group-sum method of k_eq_pair_grp
+    int gmode;                // group-sum method of k_eq_pair_grp (3: k_eq_pair_grp_c)
     float eps, cutoff;
     const float *fc;          // [E]
     const float *tfc;         // [E] fc of transposed record t (fc[tidx[t]])
@@ -1071,6 +1071,106 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_grp(EqArgs a) {
     }
 }
 
+// The same reverse pass with two records in flight per wave: lane c of slot
+// s (32 lanes each) owns the CPL contiguous channels c*CPL .. c*CPL+CPL-1 of
+// its record, all inside one gate group, so the group's dE/dgate needs only a
+// sum over the group's gw / CPL lanes (quad DPP for gw / CPL <= 4) and the
+// message rows are read as 16-byte vectors.  Used when H = 32 CPL and CPL
+// divides the group width (gmode 3).
+template <int CPL>
+__global__ void __launch_bounds__(kBlock) k_eq_pair_grp_c(EqArgs a) {
+    constexpr int S = 2, SW = kWave / S;
+    const int j = wave_atom(a.r);
+    if (j < 0) return;
+    const int lane = threadIdx.x & (kWave - 1), slot = lane / SW, c = lane % SW;
+    const int H = a.H, NG = a.NG, gw = H / a.G, lpg = gw / CPL, g = c / lpg;
+    const bool head = c % lpg == 0;
+    float Vj[CPL], vacc[CPL];
+    {
+        const float4 *vr = reinterpret_cast<const float4 *>(a.node + size_t(j) * a.NP + 2 * a.D +
+                                                            c * CPL);
+#pragma unroll
+        for (int u = 0; u < CPL / 4; ++u) {
+            const float4 v = vr[u];
+            Vj[4 * u] = v.x;
+            Vj[4 * u + 1] = v.y;
+            Vj[4 * u + 2] = v.z;
+            Vj[4 * u + 3] = v.w;
+        }
+    }
+    zero(vacc);
+    const int tb = a.r.tptr[j], te = a.r.tptr[j + 1];
+    for (int t0 = tb; t0 < te; t0 += kWave) {
+        const int cnt = min(kWave, te - t0);
+        int me = 0, mi = 0;
+        float mf = 0.0f, md = 0.0f;
+        if (lane < cnt) {
+            me = a.r.tidx[t0 + lane];
+            mi = a.r.tctr[t0 + lane];
+            mf = a.tfc[t0 + lane];
+            md = a.dfc[me];
+        }
+        // every lane loads (clamped indices) and joins the shuffles
+        auto fetch = [&](int q, int &e, float (&dm)[CPL], float &sg, float &f) {
+            const int qq = min(q, cnt - 1);
+            e = bcast(me, qq);
+            const int i = bcast(mi, qq);
+            const float fq = bcast(mf, qq);
+            f = q < cnt ? fq : 0.0f;
+            const float4 *dr = reinterpret_cast<const float4 *>(a.dmsg + size_t(i) * H + c * CPL);
+#pragma unroll
+            for (int u = 0; u < CPL / 4; ++u) {
+                const float4 v = dr[u];
+                dm[4 * u] = v.x;
+                dm[4 * u + 1] = v.y;
+                dm[4 * u + 2] = v.z;
+                dm[4 * u + 3] = v.w;
+            }
+            sg = a.ag[size_t(e) * NG + g];
+        };
+        int e, e1;
+        float dm[CPL], dm1[CPL], sg, sg1, fc, fc1;
+        fetch(slot, e, dm, sg, fc);
+        fetch(slot + S, e1, dm1, sg1, fc1);
+        for (int q0 = 0; q0 < cnt; q0 += S) {
+            const int q = q0 + slot;
+            int en;
+            float dmn[CPL], sgn, fcn;
+            fetch(q + 2 * S, en, dmn, sgn, fcn);
+            const bool on = fc != 0.0f;
+            float P = 0.0f;
+#pragma unroll
+            for (int u = 0; u < CPL; ++u) {
+                P += dm[u] * Vj[u];
+                vacc[u] += on ? sg * fc * dm[u] : 0.0f;
+            }
+            P = group_sum(P, lpg);
+            if (q < cnt && head)
+                a.dgg[size_t(e) * NG + g] = on ? P * fc * sg * (1.0f - sg) : 0.0f;
+            const float contrib = group_sum(head ? P * sg : 0.0f, SW);
+            const float dold = bcast(md, min(q, kWave - 1));
+            if (q < cnt && on && c == 0) a.dfc[e] = dold + contrib;
+            e = e1;
+            copy(dm, dm1);
+            sg = sg1;
+            fc = fc1;
+            e1 = en;
+            copy(dm1, dmn);
+            sg1 = sgn;
+            fc1 = fcn;
+        }
+    }
+    // the two slots' partial sums, added in a fixed order
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) vacc[u] += __shfl_xor(vacc[u], SW, kWave);
+    if (slot == 0) {
+        float4 *out = reinterpret_cast<float4 *>(a.dnode + size_t(j) * a.NP + 2 * a.D + c * CPL);
+#pragma unroll
+        for (int u = 0; u < CPL / 4; ++u)
+            out[u] = make_float4(vacc[4 * u], vacc[4 * u + 1], vacc[4 * u + 2], vacc[4 * u + 3]);
+    }
+}
+
 // Records per matrix-core batch of the edge-MLP reverse kernels.
 constexpr int kAdjBatch = 16;
 
@@ -1845,9 +1945,13 @@ static EqArgs eq_args(ModelImpl &m, MessagePlan &p, const Records &r, int b) {
     a.nlm = m.desc.nlm;
     a.S = eq_slots(a.C);
     {
-        const int gw = a.H / a.G;
+        const int gw = a.H / a.G, cpl = a.H / 32;
         const bool pow2 = (gw & (gw - 1)) == 0;
-        a.gmode = (pow2 && gw <= kWave) ? 0 : (gw % kWave == 0 ? 1 : 2);
+        const int lpg = cpl > 0 ? gw / cpl : 0;
+        const bool chunked = a.H % 32 == 0 && (cpl == 4 || cpl == 8 || cpl == 16) &&
+                             gw % cpl == 0 && lpg >= 1 && (lpg & (lpg - 1)) == 0 &&
+                             (2 * a.D + a.H) % 4 == 0 && a.NP % 4 == 0;
+        a.gmode = chunked ? 3 : (pow2 && gw <= kWave) ? 0 : (gw % kWave == 0 ? 1 : 2);
     }
     a.eps = float(c.norm_eps);
     a.cutoff = float(c.message_cutoff);
@@ -2028,8 +2132,17 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         }
         {
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
-            hipLaunchKernelGGL(k_eq_pair_grp, dim3(atom_grid), dim3(kBlock),
-                               a.gmode == 2 ? sizeof(float) * kWaves * H : 0, s, a);
+            if (a.gmode == 3) {
+                if (H == 128)
+                    hipLaunchKernelGGL(k_eq_pair_grp_c<4>, dim3(atom_grid), dim3(kBlock), 0, s, a);
+                else if (H == 256)
+                    hipLaunchKernelGGL(k_eq_pair_grp_c<8>, dim3(atom_grid), dim3(kBlock), 0, s, a);
+                else
+                    hipLaunchKernelGGL(k_eq_pair_grp_c<16>, dim3(atom_grid), dim3(kBlock), 0, s, a);
+            } else {
+                hipLaunchKernelGGL(k_eq_pair_grp, dim3(atom_grid), dim3(kBlock),
+                                   a.gmode == 2 ? sizeof(float) * kWaves * H : 0, s, a);
+            }
         }
         RUNE_HIP_CHECK(hipGetLastError());
         if (E > 0) {
