@@ -72,105 +72,67 @@ __device__ inline void store_stage(const float4 (&r)[kRows * 8 / 256], float *S,
     }
 }
 
-// Epilogue of a (32*WM) x (32*WN) tile through LDS, 32 rows of the tile at a
-// time: the waves owning those rows store their accumulators (row stride
-// kLdo = BN + 4 puts the four lane groups on distinct banks); the rows' own
-// data goes to LDS; then all 256 threads apply the epilogue row-contiguously,
-// kB elements per thread at once so that each term's loads are issued
-// together.  Out-of-range elements load from clamped indices and store
-// nothing.  smem must hold 32 * (32 * WN + 4) floats and be free to reuse.
+// Epilogue straight from the accumulators: element (a, b, v) of this lane is
+// row wm + 16a + 4g + v, column wn + 16b + rr of the tile (the MFMA output
+// layout), so each store instruction writes 64-byte row segments and no LDS
+// staging or block barrier is needed.  All loads of the terms come first (the
+// stores to C cannot alias them then), in the order row scale, bias,
+// embedding, residual, gathered rows; then the pre-activation store, the
+// activation (act2 from column act_split on) and the activation derivative.
+// Out-of-range elements load from clamped indices and store nothing.
 template <int WM, int WN, int WMW>
-__device__ inline void tile_epilogue(floatx4 (&acc)[WM][WN], float *smem, int M, int N,
+__device__ inline void tile_epilogue(floatx4 (&acc)[WM][WN], float *, int M, int N,
                                      float *__restrict__ C, int ldc, const Epilogue &ep,
                                      int m0, int n0) {
     constexpr int WNW = 4 / WMW;
-    constexpr int kBM = 16 * WM * WMW, BN = 16 * WN * WNW, kLdo = BN + 4;
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
-    const int wn = (wave % WNW) * 16 * WN;
+    const int wm = (wave / WNW) * 16 * WM, wn = (wave % WNW) * 16 * WN;
     const int g = lane >> 4, rr = lane & 15;
-    constexpr int kE = 32 * BN / 256;
-    constexpr int kB = kE % 12 == 0 ? 12 : kE % 10 == 0 ? 10 : kE % 8 == 0 ? 8 : 4;
-    static_assert(kE % kB == 0, "epilogue batch must divide the per-thread count");
-    __shared__ float s_rs[32];
-    __shared__ int s_ix[4][32];
+    float x[WM][4][WN], du[WM][4][WN];
 #pragma unroll
-    for (int part = 0; part < kBM / 32; ++part) {
-        // accumulator row block a of this wave is 16-row block blk of the tile
+    for (int a = 0; a < WM; ++a)
 #pragma unroll
-        for (int a = 0; a < WM; ++a) {
-            const int blk = (wave / WNW) * WM + a;
-            if ((blk >> 1) == part) {
+        for (int v = 0; v < 4; ++v) {
+            const int rc = min(m0 + wm + 16 * a + 4 * g + v, M - 1);
+            const float rs = ep.row_scale ? ep.row_scale[rc] : 1.0f;
+            const int te = ep.emb ? ep.types[rc] : 0;
+            int gi[3];
 #pragma unroll
-                for (int b = 0; b < WN; ++b)
+            for (int k = 0; k < 3; ++k) gi[k] = ep.gtab[k] ? ep.gidx[k][rc] : 0;
 #pragma unroll
-                    for (int v = 0; v < 4; ++v)
-                        smem[(16 * (blk & 1) + 4 * g + v) * kLdo + wn + 16 * b + rr] =
-                            acc[a][b][v];
+            for (int b = 0; b < WN; ++b) {
+                const int cc = min(n0 + wn + 16 * b + rr, N - 1);
+                float t = acc[a][b][v] * rs;
+                if (ep.bias) t += ep.bias[cc];
+                if (ep.emb) t += ep.emb[size_t(te) * ep.ld_emb + cc];
+                if (ep.residual) t += ep.residual[size_t(rc) * ep.ldr + cc];
+#pragma unroll
+                for (int k = 0; k < 3; ++k)
+                    if (ep.gtab[k]) t += ep.gtab[k][size_t(gi[k]) * ep.gld[k] + cc];
+                x[a][v][b] = t;
+                du[a][v][b] = ep.dact_from ? ep.dact_from[size_t(rc) * ep.ldu + cc] : 0.0f;
             }
         }
-        if (tid < 32) {
-            int row = min(m0 + 32 * part + tid, M - 1);
-            s_rs[tid] = ep.row_scale ? ep.row_scale[row] : 1.0f;
-            s_ix[0][tid] = ep.emb ? ep.types[row] : 0;
 #pragma unroll
-            for (int k = 0; k < 3; ++k) s_ix[1 + k][tid] = ep.gtab[k] ? ep.gidx[k][row] : 0;
-        }
-        __syncthreads();
-        for (int j0 = 0; j0 < kE; j0 += kB) {
-            float x[kB], du[kB];
-            int lr[kB], cc[kB], rc[kB];
+    for (int a = 0; a < WM; ++a)
 #pragma unroll
-            for (int u = 0; u < kB; ++u) {
-                int idx = tid + 256 * (j0 + u);
-                lr[u] = idx / BN;
-                int lc = idx - lr[u] * BN;
-                cc[u] = min(n0 + lc, N - 1);
-                rc[u] = min(m0 + 32 * part + lr[u], M - 1);
-                x[u] = smem[lr[u] * kLdo + lc] * s_rs[lr[u]];
-            }
-            if (ep.bias) {
+        for (int v = 0; v < 4; ++v) {
+            const int row = m0 + wm + 16 * a + 4 * g + v;
 #pragma unroll
-                for (int u = 0; u < kB; ++u) x[u] += ep.bias[cc[u]];
-            }
-            if (ep.emb) {
-#pragma unroll
-                for (int u = 0; u < kB; ++u)
-                    x[u] += ep.emb[size_t(s_ix[0][lr[u]]) * ep.ld_emb + cc[u]];
-            }
-            if (ep.residual) {
-#pragma unroll
-                for (int u = 0; u < kB; ++u) x[u] += ep.residual[size_t(rc[u]) * ep.ldr + cc[u]];
-            }
-#pragma unroll
-            for (int k = 0; k < 3; ++k) {
-                if (ep.gtab[k]) {
-#pragma unroll
-                    for (int u = 0; u < kB; ++u)
-                        x[u] += ep.gtab[k][size_t(s_ix[1 + k][lr[u]]) * ep.gld[k] + cc[u]];
-                }
-            }
-            if (ep.dact_from) {
-#pragma unroll
-                for (int u = 0; u < kB; ++u) du[u] = ep.dact_from[size_t(rc[u]) * ep.ldu + cc[u]];
-            }
-#pragma unroll
-            for (int u = 0; u < kB; ++u) {
-                int idx = tid + 256 * (j0 + u);
-                int row = m0 + 32 * part + lr[u], col = n0 + idx - lr[u] * BN;
+            for (int b = 0; b < WN; ++b) {
+                const int col = n0 + wn + 16 * b + rr;
                 if (row >= M || col >= N) continue;
-                float v = x[u];
-                if (ep.pre) ep.pre[size_t(row) * ep.ldp + col] = v;
+                float t = x[a][v][b];
+                if (ep.pre) ep.pre[size_t(row) * ep.ldp + col] = t;
                 if (ep.act_split >= 0 && col >= ep.act_split)
-                    v = act_f(ep.act2, v);
+                    t = act_f(ep.act2, t);
                 else if (ep.act >= 0)
-                    v = act_f(ep.act, v);
-                if (ep.dact_from) v *= act_d(ep.dact, du[u]);
-                C[size_t(row) * ldc + col] = v;
+                    t = act_f(ep.act, t);
+                if (ep.dact_from) t *= act_d(ep.dact, du[a][v][b]);
+                C[size_t(row) * ldc + col] = t;
             }
         }
-        __syncthreads();
-    }
 }
 
 // C[M,N] = A[M,K] Bt[N,K]^T with the fused epilogue.  256 threads in WMW x
@@ -201,8 +163,7 @@ __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *
         Bt += size_t(w) * bt.sb;
     }
     constexpr int WNW = 4 / WMW;
-    constexpr int kBM = 16 * WM * WMW, BN = 16 * WN * WNW, kLdo = BN + 4;
-    static_assert(32 * kLdo <= (kBM + BN) * kLdk, "epilogue staging exceeds the tile LDS");
+    constexpr int kBM = 16 * WM * WMW, BN = 16 * WN * WNW;
     __shared__ __attribute__((aligned(16))) float smem[(kBM + BN) * kLdk];
     float *As = smem, *Bs = smem + kBM * kLdk;
     const int tid = threadIdx.x;
