@@ -28,7 +28,7 @@ COPY_KERNEL = "__amd_rocclr_copyBuffer"
 
 # per-record message kernels of the MP and EQ blocks (bench.py "edge_kernels")
 EDGE_KERNELS = ("k_eq_edge_nbr", "k_eq_edge_centre", "k_eq_aggregate", "k_eq_pair_dir",
-                "k_eq_pair_grp", "k_eq_edge_adj", "k_eq_harmonic_backward", "k_edge_prep",
+                "k_eq_pair_grp", "k_eq_pair_grp_c", "k_eq_edge_adj", "k_eq_harmonic_backward", "k_edge_prep",
                 "k_gather_f", "k_edge_rb_backward", "k_edge_direct", "k_mp_aggregate",
                 "k_mp_edge_backward", "k_mp_neighbor_backward")
 
