@@ -79,23 +79,15 @@ __device__ inline void chebyshev_d(float r, float rc, int k_max, float *f, float
     }
 }
 
-struct Powers {
-    float zp[kMaxL + 1];
-    float wr[kMaxL + 1];
-    float wi[kMaxL + 1];
-};
-
-__device__ inline void powers(float x, float y, float z, int l_max, Powers &p) {
-    p.zp[0] = 1.0f;
-    p.wr[0] = 1.0f;
-    p.wi[0] = 0.0f;
-#pragma unroll
-    for (int k = 1; k <= kMaxL; ++k) {
-        if (k > l_max) break;
-        p.zp[k] = p.zp[k - 1] * z;
-        p.wr[k] = p.wr[k - 1] * x - p.wi[k - 1] * y;
-        p.wi[k] = p.wr[k - 1] * y + p.wi[k - 1] * x;
-    }
+// Powers of the unit vector are formed as running products while the (L, |m|)
+// loops advance, never stored in an array: a per-lane array indexed by a
+// runtime order would live in scratch memory.
+//   (x + iy)^m:  w_m = w_{m-1} * (x + iy), w_0 = 1
+//   z^q:         z^q = z^{q-1} * z, z^0 = 1
+__device__ inline void next_w(float x, float y, float &wr, float &wi) {
+    float r = wr * x - wi * y;
+    wi = wr * y + wi * x;
+    wr = r;
 }
 
 // sum_k c[k] f[k] over one padded c-table row (16-byte loads; the padding is
@@ -117,14 +109,19 @@ __device__ inline float row_dot(const float *row, int k4, const float *f) {
 }
 
 // z-polynomial of order L, |m| = n1 (descriptor.py:601-613) and d/dz.
-__device__ inline void zpoly(const DescTables &t, int L, int n1, const Powers &p, float &zf,
+__device__ inline void zpoly(const DescTables &t, int L, int n1, float z, float &zf,
                              float &zfp) {
     const float *Z = t.z + t.z_off[L] + n1 * (L + 1);
+    int q = (L + n1) & 1;
+    float zq = q ? z : 1.0f;   // z^q
+    float zq1 = 1.0f;          // z^(q-1), used once q > 0
     zf = 0.0f;
     zfp = 0.0f;
-    for (int q = ((L + n1) & 1); q <= L - n1; q += 2) {
-        zf += Z[q] * p.zp[q];
-        if (q > 0) zfp += float(q) * Z[q] * p.zp[q - 1];
+    for (; q <= L - n1; q += 2) {
+        zf += Z[q] * zq;
+        if (q > 0) zfp += float(q) * Z[q] * zq1;
+        zq1 = zq * z;
+        zq = zq1 * z;
     }
 }
 
@@ -283,18 +280,19 @@ __global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Reco
             const float *row = t.c_angular + size_t(ti * t.n_types + tj) * t.na * t.ka4;
             for (int n = 0; n < na; ++n) gl[n] = row_dot<kMaxKa>(row + n * t.ka4, t.ka4, f);
             float inv = 1.0f / fmaxf(v.w, 1.0e-12f);
-            Powers p;
-            powers(v.x * inv, v.y * inv, v.z * inv, t.l_max, p);
+            const float ux = v.x * inv, uy = v.y * inv, uz = v.z * inv;
             int idx = 0;
             for (int L = 1; L <= t.l_max; ++L) {
+                float wr = 1.0f, wi = 0.0f;   // (x + iy)^n1
                 for (int n1 = 0; n1 <= L; ++n1) {
                     float zf, zfp;
-                    zpoly(t, L, n1, p, zf, zfp);
+                    zpoly(t, L, n1, uz, zf, zfp);
                     if (n1 == 0) {
                         bl[idx++] = zf;
                     } else {
-                        bl[idx++] = zf * p.wr[n1];
-                        bl[idx++] = zf * p.wi[n1];
+                        next_w(ux, uy, wr, wi);
+                        bl[idx++] = zf * wr;
+                        bl[idx++] = zf * wi;
                     }
                 }
             }
@@ -442,45 +440,38 @@ __global__ void __launch_bounds__(kWave) k_descriptor_reverse(
                 gn[n] = a;
                 gnp[n] = b;
             }
-            Powers p;
-            powers(ux, uy, uz, t.l_max, p);
             float rs = 0.0f, dx = 0.0f, dy = 0.0f, dz = 0.0f, proj = 0.0f;
             int c = 0;
+            // one angular channel c with basis value b and gradient (bx, by, bz)
+            auto channel = [&](float b, float bx, float by, float bz) {
+                float wsum = 0.0f, wsump = 0.0f;
+#pragma unroll
+                for (int n = 0; n < kMaxNa; ++n) {
+                    if (n >= na) break;
+                    float w = WL[n * nlm + c];
+                    wsum += w * gn[n];
+                    wsump += w * gnp[n];
+                }
+                rs += wsump * b;
+                dx += wsum * bx;
+                dy += wsum * by;
+                dz += wsum * bz;
+                proj += wsum * (ux * bx + uy * by + uz * bz);
+                ++c;
+            };
             for (int L = 1; L <= t.l_max; ++L) {
+                float wr = 1.0f, wi = 0.0f;   // (x + iy)^n1
                 for (int n1 = 0; n1 <= L; ++n1) {
                     float zf, zfp;
-                    zpoly(t, L, n1, p, zf, zfp);
-                    for (int part = 0; part < (n1 == 0 ? 1 : 2); ++part, ++c) {
-                        float b, bx, by, bz;
-                        if (n1 == 0) {
-                            b = zf;
-                            bx = 0.0f;
-                            by = 0.0f;
-                            bz = zfp;
-                        } else if (part == 0) {
-                            b = zf * p.wr[n1];
-                            bx = zf * float(n1) * p.wr[n1 - 1];
-                            by = -zf * float(n1) * p.wi[n1 - 1];
-                            bz = zfp * p.wr[n1];
-                        } else {
-                            b = zf * p.wi[n1];
-                            bx = zf * float(n1) * p.wi[n1 - 1];
-                            by = zf * float(n1) * p.wr[n1 - 1];
-                            bz = zfp * p.wi[n1];
-                        }
-                        float wr = 0.0f, wrp = 0.0f;
-#pragma unroll
-                        for (int n = 0; n < kMaxNa; ++n) {
-                            if (n >= na) break;
-                            float w = WL[n * nlm + c];
-                            wr += w * gn[n];
-                            wrp += w * gnp[n];
-                        }
-                        rs += wrp * b;
-                        dx += wr * bx;
-                        dy += wr * by;
-                        dz += wr * bz;
-                        proj += wr * (ux * bx + uy * by + uz * bz);
+                    zpoly(t, L, n1, uz, zf, zfp);
+                    if (n1 == 0) {
+                        channel(zf, 0.0f, 0.0f, zfp);
+                    } else {
+                        const float pr = wr, pi = wi;   // (x + iy)^(n1-1)
+                        next_w(ux, uy, wr, wi);
+                        const float zn = zf * float(n1);
+                        channel(zf * wr, zn * pr, -zn * pi, zfp * wr);
+                        channel(zf * wi, zn * pi, zn * pr, zfp * wi);
                     }
                 }
             }
