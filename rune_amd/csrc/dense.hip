@@ -146,7 +146,7 @@ __device__ inline void tile_epilogue(floatx4 (&acc)[WM][WN], float *, int M, int
 // Batched launches (gridDim.y > 1) offset A, C by z times their batch strides
 // and Bt by sb times z, or times L(z) - 1 (L the harmonic order of component z)
 // when the batches share one weight block per order.
-template <int WM, int WN, int WMW, bool kVec>
+template <int WM, int WN, int WMW, bool kVec, bool kActA = false>
 __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *__restrict__ A,
                                               int lda, const float *__restrict__ Bt, int ldb,
                                               float *__restrict__ C, int ldc, Epilogue ep,
@@ -193,6 +193,12 @@ __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *
     };
     fetch(0);
     for (int k0 = 0; k0 < K; k0 += kBK) {
+        if constexpr (kActA) {
+#pragma unroll
+            for (int it = 0; it < kBM * 8 / 256; ++it)
+                ra[it] = make_float4(act_f(ep.a_act, ra[it].x), act_f(ep.a_act, ra[it].y),
+                                     act_f(ep.a_act, ra[it].z), act_f(ep.a_act, ra[it].w));
+        }
         store_stage<kBM>(ra, As, tid);
         store_stage<BN>(rb, Bs, tid);
         __syncthreads();
@@ -331,7 +337,13 @@ static void launch_gemm(bool vec, int M, int N, int K, const float *A, int lda, 
     if (blocks > 0x7fffffff || bt.count > 65535)
         throw Error(RUNE_ERR_ARGUMENT, "gemm: problem too large");
     const dim3 grid(unsigned(blocks), unsigned(bt.count));
-    if (vec)
+    if (vec && ep.a_act >= 0)
+        hipLaunchKernelGGL((k_gemm<WM, WN, WMW, true, true>), grid, dim3(256), 0, s, M, N, K, A,
+                           lda, Bt, ldb, C, ldc, ep, nbn, bt);
+    else if (ep.a_act >= 0)
+        hipLaunchKernelGGL((k_gemm<WM, WN, WMW, false, true>), grid, dim3(256), 0, s, M, N, K, A,
+                           lda, Bt, ldb, C, ldc, ep, nbn, bt);
+    else if (vec)
         hipLaunchKernelGGL((k_gemm<WM, WN, WMW, true>), grid, dim3(256), 0, s, M, N, K, A, lda, Bt,
                            ldb, C, ldc, ep, nbn, bt);
     else

@@ -63,23 +63,30 @@ __global__ void __launch_bounds__(256) k_forces(Records r, const float4 *g, floa
 }
 
 // One workgroup per structure; thread t sums atoms t, t+256, ... then a tree.
-__global__ void __launch_bounds__(256) k_structure_sum(const int32_t *sptr, const float *x,
-                                                       int ncol, float *out) {
-    __shared__ double lds[256];
-    int b = blockIdx.x;
-    int beg = sptr[b], end = sptr[b + 1];
-    for (int c = 0; c < ncol; ++c) {
-        double s = 0.0;
-        for (int m = beg + threadIdx.x; m < end; m += 256) s += double(x[size_t(m) * ncol + c]);
-        lds[threadIdx.x] = s;
-        __syncthreads();
-        for (int off = 128; off > 0; off >>= 1) {
-            if (threadIdx.x < off) lds[threadIdx.x] += lds[threadIdx.x + off];
-            __syncthreads();
-        }
-        if (threadIdx.x == 0) out[size_t(b) * ncol + c] = float(lds[0]);
+// Column sums of x [atoms, ncol] over the atoms of each structure, in fp64.
+// One 1024-thread block per structure reads the structure's rows as one flat
+// coalesced range; the threads in use are a multiple of ncol, so thread t
+// always meets column t % ncol.  The per-thread partials of each column are
+// then combined by a fixed tree, so the result does not depend on timing.
+__global__ void __launch_bounds__(1024) k_structure_sum(const int32_t *sptr, const float *x,
+                                                        int ncol, float *out) {
+    __shared__ double lds[1024];
+    const int b = blockIdx.x, t = threadIdx.x;
+    const int per = 1024 / ncol, lanes = per * ncol;
+    const int64_t beg = int64_t(sptr[b]) * ncol, end = int64_t(sptr[b + 1]) * ncol;
+    double s = 0.0;
+    if (t < lanes)
+        for (int64_t f = beg + t; f < end; f += lanes) s += double(x[f]);
+    lds[t] = s;
+    __syncthreads();
+    const int k = t / ncol;
+    int half = 1;
+    while (2 * half < per) half *= 2;
+    for (; half >= 1; half >>= 1) {
+        if (t < lanes && k < half && k + half < per) lds[t] += lds[t + half * ncol];
         __syncthreads();
     }
+    if (t < ncol) out[size_t(b) * ncol + t] = float(lds[t]);
 }
 
 }  // namespace
@@ -95,7 +102,8 @@ void forces_and_virial(const Records &r, const float4 *g, float *forces, float *
 
 void structure_sum(const Records &r, const float *x, int ncol, float *out, hipStream_t s) {
     if (r.n_structures == 0) return;
-    hipLaunchKernelGGL(k_structure_sum, dim3(r.n_structures), dim3(256), 0, s, r.sptr, x, ncol,
+    if (ncol < 1 || ncol > 1024) throw Error(RUNE_ERR_ARGUMENT, "structure_sum: bad column count");
+    hipLaunchKernelGGL(k_structure_sum, dim3(r.n_structures), dim3(1024), 0, s, r.sptr, x, ncol,
                        out);
     RUNE_HIP_CHECK(hipGetLastError());
 }

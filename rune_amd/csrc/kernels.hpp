@@ -95,6 +95,10 @@ struct Epilogue {
     const float *dact_from = nullptr;   // v *= act'(U[m, n]) with U [M, ldu]
     int ldu = 0;
     int dact = -1;                      // activation whose derivative is used
+    // RUNE_ACT_* applied to every A element as it is staged (A holds
+    // pre-activations), -1 none; the padding of a partial K stage is
+    // multiplied by zero B columns, so act(0) there does not matter
+    int a_act = -1;
 };
 // C[M,N] = A[M,K] Bt[N,K]^T (+ epilogue); row-major with leading dimensions.
 void gemm(int M, int N, int K, const float *A, int lda, const float *Bt, int ldb, float *C,

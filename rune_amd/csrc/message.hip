@@ -579,7 +579,6 @@ MessagePlan plan_messages(ModelImpl &m, Arena &ar, int N, int64_t E) {
         bb.rin = p.add(ar, 4 * n);
         bb.vs = p.add(ar, 4 * n * NP);
         bb.ue = p.add(ar, 4 * e * D);
-        bb.eh = p.add(ar, 4 * e * D);
         bb.gv = p.add(ar, 4 * e * NG);
         bb.msg = p.add(ar, 4 * n * H);
         bb.rm = p.add(ar, 4 * n);
@@ -713,19 +712,18 @@ float *messages_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Recor
             e1.gtab[0] = w.pair_proj;
             e1.gidx[0] = reinterpret_cast<const int32_t *>(p.at(p.i_pair));
             e1.gld[0] = D;
-            e1.pre = p.at(bb.ue);
-            e1.ldp = D;
-            e1.act = act;
             {
                 Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
-                gemm(int(E), D, w.KX, p.at(p.i_rb), p.ldrb, w.edge_x, w.ld_edge_x, p.at(bb.eh),
+                gemm(int(E), D, w.KX, p.at(p.i_rb), p.ldrb, w.edge_x, w.ld_edge_x, p.at(bb.ue),
                      D, e1, s);
             }
+            // the gate GEMM activates the pre-activations as it stages them
             Epilogue e2;
             e2.bias = w.gate_b;
+            e2.a_act = act;
             {
                 Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
-                gemm(int(E), w.NG, D, p.at(bb.eh), D, w.gate, D, p.at(bb.gv), w.NG, e2, s);
+                gemm(int(E), w.NG, D, p.at(bb.ue), D, w.gate, D, p.at(bb.gv), w.NG, e2, s);
             }
         }
         MpArgs a = mp_args(m, p, r, b);
