@@ -291,31 +291,47 @@ __global__ void __launch_bounds__(256) k_readout(int M, int H, const float *h, i
     }
 }
 
-__global__ void k_nep_mlp(int M, int Q, int Hn, const float *q, int ldq, const int32_t *types,
-                          const float *w0, const float *b0, const float *w1, float shared_bias,
-                          float *energies, float *dq, int want_grad) {
-    int row = blockIdx.x * blockDim.x + threadIdx.x;
-    if (row >= M) return;
-    int t = types[row];
-    const float *x = q + size_t(row) * ldq;
+// NEP per-element MLP, one wave per atom (4 per block): the atom's q row is
+// staged in LDS; lane h computes hidden unit h (u = sum_k W0[h, k] q_k,
+// a = tanh(u + b0)), the energy is the wave sum of W1[h] a_h, and for the
+// gradient lane k forms dq_k = sum_h W1[h] (1 - a_h^2) W0[h, k] from the
+// per-unit factors in LDS.
+__global__ void __launch_bounds__(256) k_nep_mlp(int M, int Q, int Hn, const float *q, int ldq,
+                                                 const int32_t *types, const float *w0,
+                                                 const float *b0, const float *w1,
+                                                 float shared_bias, float *energies, float *dq,
+                                                 int want_grad) {
+    extern __shared__ float lds[];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + wave;
+    const bool live = row < M;
+    float *xs = lds + wave * (Q + Hn), *ds = xs + Q;
+    const int t = live ? types[row] : 0;
     const float *W0 = w0 + size_t(t) * Hn * Q;
     const float *B0 = b0 + size_t(t) * Hn;
     const float *W1 = w1 + size_t(t) * Hn;
+    if (live)
+        for (int k = lane; k < Q; k += 64) xs[k] = q[size_t(row) * ldq + k];
+    __syncthreads();
     float e = 0.0f;
-    float *g = want_grad ? dq + size_t(row) * ldq : nullptr;
-    if (g)
-        for (int k = 0; k < Q; ++k) g[k] = 0.0f;
-    for (int h = 0; h < Hn; ++h) {
-        float u = 0.0f;
-        for (int k = 0; k < Q; ++k) u += W0[h * Q + k] * x[k];
-        float a = tanhf(u + B0[h]);
-        e += W1[h] * a;
-        if (g) {
-            float d = W1[h] * (1.0f - a * a);
-            for (int k = 0; k < Q; ++k) g[k] += d * W0[h * Q + k];
+    if (live)
+        for (int h = lane; h < Hn; h += 64) {
+            float u = 0.0f;
+            for (int k = 0; k < Q; ++k) u += W0[h * Q + k] * xs[k];
+            const float a = tanhf(u + B0[h]);
+            e += W1[h] * a;
+            ds[h] = W1[h] * (1.0f - a * a);
         }
-    }
-    energies[row] = e - shared_bias;
+    e = wave_sum(e);
+    __syncthreads();
+    if (!live) return;
+    if (lane == 0) energies[row] = e - shared_bias;
+    if (want_grad)
+        for (int k = lane; k < Q; k += 64) {
+            float g = 0.0f;
+            for (int h = 0; h < Hn; ++h) g += ds[h] * W0[h * Q + k];
+            dq[size_t(row) * ldq + k] = g;
+        }
 }
 
 }  // namespace
@@ -400,8 +416,9 @@ void nep_mlp(int M, int Q, int Hn, const float *q, int ldq, const int32_t *types
              const float *w0, const float *b0, const float *w1, float shared_bias,
              float *energies, float *dq, int want_grad, hipStream_t s) {
     if (M == 0) return;
-    hipLaunchKernelGGL(k_nep_mlp, dim3(ceil_div(M, 128)), dim3(128), 0, s, M, Q, Hn, q, ldq,
-                       types, w0, b0, w1, shared_bias, energies, dq, want_grad);
+    hipLaunchKernelGGL(k_nep_mlp, dim3(ceil_div(M, 4)), dim3(256),
+                       sizeof(float) * 4 * size_t(Q + Hn), s, M, Q, Hn, q, ldq, types, w0, b0, w1,
+                       shared_bias, energies, dq, want_grad);
     RUNE_HIP_CHECK(hipGetLastError());
 }
 

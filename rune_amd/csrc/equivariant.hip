@@ -127,8 +127,7 @@ struct EqArgs {
     float *dgg;               // [E, NG]
     float4 *dv;               // [E]
     float *dfc;               // [E] dE/dfc of the message terms, all blocks
-    float *dy;                // [E, nq] dE/dY, centre-side shares
-    float *dyn;               // [E, nq] dE/dY, neighbour-side shares
+    float *dy;                // [E, nq] dE/dY (both sides' shares, accumulated in turn)
     float *dnode;             // [N, NP]
     float *dmix;              // [N, C*nq]
     const float *due;         // [E, D]
@@ -1233,7 +1232,7 @@ __global__ void __launch_bounds__(kBlock, 2) k_eq_edge_adj(EqArgs a) {
     const int ldd = a.ldd, ldq = 2 * ldd, D = a.D;
     const int b0 = SIDE ? a.r.tptr[n] : a.r.view[4 * n];
     const int b1 = SIDE ? a.r.tptr[n + 1] : a.r.view[4 * n + 1];
-    float *dyo = SIDE ? a.dyn : a.dy;
+    float *dyo = a.dy;
     const float *Qn = a.qbuf + size_t(n) * NQ * ldq + SIDE * ldd;
     float *dQo = a.dqbuf + size_t(n) * NQ * ldq + SIDE * ldd;
     for (int c0 = 0; c0 < ldd; c0 += CW) {
@@ -1407,7 +1406,7 @@ __global__ void __launch_bounds__(256) k_eq_encoder_backward(int N, const float 
 // gains dE/dfc fc'(d) and the radial-basis term sum_k dE/drb_k drb_k/dd.
 template <int LQ>
 __global__ void k_eq_harmonic_backward(int64_t E, Records r, const float *fcv, const float *dy,
-                                       const float *dyn, const float *dfc, const float *drb,
+                                       const float *dfc, const float *drb,
                                        const float *rbd, int ldrb, int kb, float cutoff,
                                        const float *ztab, EdgeZ zoff, const float *scale,
                                        float4 *dv) {
@@ -1416,9 +1415,8 @@ __global__ void k_eq_harmonic_backward(int64_t E, Records r, const float *fcv, c
     if (e >= E) return;
     int i = r.ctr[e];
     if (!(e >= r.view[4 * i] && e < r.view[4 * i + 1])) return;
-    float gs[NQ], g2[NQ];
+    float gs[NQ];
     load_row(gs, dy + size_t(e) * NQ);
-    load_row(g2, dyn + size_t(e) * NQ);
     float4 v = r.vec[e];
     float inv = 1.0f / fmaxf(v.w, 1.0e-12f);
     float x = v.x * inv, y = v.y * inv, z = v.z * inv;
@@ -1447,7 +1445,7 @@ __global__ void k_eq_harmonic_backward(int64_t E, Records r, const float *fcv, c
             }
 #pragma unroll
             for (int part = 0; part < (n1 == 0 ? 1 : 2); ++part, ++idx) {
-                float w = (gs[idx] + g2[idx]) * scale[idx];
+                float w = gs[idx] * scale[idx];
                 if (n1 == 0) {
                     dz += w * zfp;
                 } else if (part == 0) {
@@ -1882,7 +1880,6 @@ MessagePlan plan_equivariant(ModelImpl &m, Arena &ar, int N, int64_t E) {
     p.i_dv = p.add(ar, 16 * e);
     p.i_harm = p.add(ar, 4 * e * nq);
     p.i_dharm = p.add(ar, 4 * e * nq);
-    p.i_dharm_n = p.add(ar, 4 * e * nq);
     p.i_dfc = p.add(ar, 4 * e);
     p.i_drb = p.add(ar, 4 * e * p.ldrb);
     p.i_rbd = p.add(ar, 4 * e * p.ldrb);
@@ -1985,7 +1982,6 @@ static EqArgs eq_args(ModelImpl &m, MessagePlan &p, const Records &r, int b) {
     a.dv = reinterpret_cast<float4 *>(p.at(p.i_dv));
     a.dfc = p.at(p.i_dfc);
     a.dy = p.at(p.i_dharm);
-    a.dyn = p.at(p.i_dharm_n);
     a.dnode = p.at(p.t_dvs);
     a.dmix = p.at(p.t_dmix);
     a.due = p.at(p.t_due);
@@ -2015,7 +2011,6 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
                                p.at(p.i_fc), p.at(p.i_tfc));
         }
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dharm), 0, 4 * size_t(E) * nq, s));
-        RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dharm_n), 0, 4 * size_t(E) * nq, s));
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dfc), 0, 4 * size_t(E), s));
     }
     {
@@ -2211,7 +2206,7 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         {
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
             EQ_LAUNCH(k_eq_harmonic_backward, lq, dim3(ceil_div(E, 256)), dim3(256), 0, s, E, r,
-                      p.at(p.i_fc), p.at(p.i_dharm), p.at(p.i_dharm_n), p.at(p.i_dfc),
+                      p.at(p.i_fc), p.at(p.i_dharm), p.at(p.i_dfc),
                       p.at(p.i_drb), p.at(p.i_rbd), p.ldrb, kb, float(c.message_cutoff),
                       m.desc.z, zo, m.harm_scale, reinterpret_cast<float4 *>(p.at(p.i_dv)));
         }
