@@ -4,6 +4,8 @@
 // model.py:23-44) using the neighbour-grouped transpose list, and the per-atom
 // virial W_a = -sum_{e: neighbour a} g_e (x) r_e attributed to the neighbour
 // like the reference.  Structure totals use a fixed-order fp64 reduction.
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace rune {
@@ -64,16 +66,20 @@ __global__ void __launch_bounds__(256) k_forces(Records r, const float4 *g, floa
 
 // One workgroup per structure; thread t sums atoms t, t+256, ... then a tree.
 // Column sums of x [atoms, ncol] over the atoms of each structure, in fp64.
-// One 1024-thread block per structure reads the structure's rows as one flat
-// coalesced range; the threads in use are a multiple of ncol, so thread t
-// always meets column t % ncol.  The per-thread partials of each column are
-// then combined by a fixed tree, so the result does not depend on timing.
+// Block (p, b) takes part p of structure b's atoms (one part unless the
+// structure is large) and reads them as one flat coalesced range; the
+// threads in use are a multiple of ncol, so thread t always meets column
+// t % ncol.  The per-thread partials of each column are combined by a fixed
+// tree.  With one part the result goes to out, else to part[b, p, :].
 __global__ void __launch_bounds__(1024) k_structure_sum(const int32_t *sptr, const float *x,
-                                                        int ncol, float *out) {
+                                                        int ncol, int parts, double *part,
+                                                        float *out) {
     __shared__ double lds[1024];
-    const int b = blockIdx.x, t = threadIdx.x;
+    const int b = blockIdx.y, p = blockIdx.x, t = threadIdx.x;
     const int per = 1024 / ncol, lanes = per * ncol;
-    const int64_t beg = int64_t(sptr[b]) * ncol, end = int64_t(sptr[b + 1]) * ncol;
+    const int a0 = sptr[b], n = sptr[b + 1] - a0, chunk = (n + parts - 1) / parts;
+    const int lo = a0 + min(n, p * chunk), hi = a0 + min(n, (p + 1) * chunk);
+    const int64_t beg = int64_t(lo) * ncol, end = int64_t(hi) * ncol;
     double s = 0.0;
     if (t < lanes)
         for (int64_t f = beg + t; f < end; f += lanes) s += double(x[f]);
@@ -86,7 +92,27 @@ __global__ void __launch_bounds__(1024) k_structure_sum(const int32_t *sptr, con
         if (t < lanes && k < half && k + half < per) lds[t] += lds[t + half * ncol];
         __syncthreads();
     }
-    if (t < ncol) out[size_t(b) * ncol + t] = float(lds[t]);
+    if (t < ncol) {
+        if (parts == 1)
+            out[size_t(b) * ncol + t] = float(lds[t]);
+        else
+            part[(size_t(b) * parts + p) * ncol + t] = lds[t];
+    }
+}
+
+// out[b, c] = sum of the parts of structure b in part order.
+__global__ void k_structure_sum_parts(int n_structures, int ncol, int parts, const double *part,
+                                      float *out) {
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= n_structures * ncol) return;
+    const int b = q / ncol, c = q - b * ncol;
+    double s = 0.0;
+    for (int p = 0; p < parts; ++p) s += part[(size_t(b) * parts + p) * ncol + c];
+    out[q] = float(s);
+}
+
+static int sum_parts(const Records &r) {
+    return std::max(1, std::min(64, ceil_div(r.max_struct_atoms, kSumChunk)));
 }
 
 }  // namespace
@@ -100,11 +126,22 @@ void forces_and_virial(const Records &r, const float4 *g, float *forces, float *
     RUNE_HIP_CHECK(hipGetLastError());
 }
 
-void structure_sum(const Records &r, const float *x, int ncol, float *out, hipStream_t s) {
+size_t structure_sum_scratch(const Records &r, int ncol) {
+    const int parts = sum_parts(r);
+    return parts == 1 ? 0 : size_t(r.n_structures) * parts * ncol;
+}
+
+void structure_sum(const Records &r, const float *x, int ncol, float *out, double *scratch,
+                   hipStream_t s) {
     if (r.n_structures == 0) return;
     if (ncol < 1 || ncol > 1024) throw Error(RUNE_ERR_ARGUMENT, "structure_sum: bad column count");
-    hipLaunchKernelGGL(k_structure_sum, dim3(r.n_structures), dim3(1024), 0, s, r.sptr, x, ncol,
-                       out);
+    const int parts = sum_parts(r);
+    if (parts > 1 && !scratch) throw Error(RUNE_ERR_STATE, "structure_sum: no scratch");
+    hipLaunchKernelGGL(k_structure_sum, dim3(parts, r.n_structures), dim3(1024), 0, s, r.sptr, x,
+                       ncol, parts, scratch, out);
+    if (parts > 1)
+        hipLaunchKernelGGL(k_structure_sum_parts, dim3(ceil_div(r.n_structures * ncol, 256)),
+                           dim3(256), 0, s, r.n_structures, ncol, parts, scratch, out);
     RUNE_HIP_CHECK(hipGetLastError());
 }
 

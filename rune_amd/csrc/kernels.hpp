@@ -62,6 +62,7 @@ struct Records {
     const int32_t *sptr;          // [B+1]
     int n_structures;
     const int32_t *order;         // [N] spatially coherent processing order, or null
+    int max_struct_atoms;         // atoms of the largest structure
 };
 
 // ---- descriptor (descriptor.hip) ----
@@ -130,6 +131,12 @@ void nep_mlp(int M, int Q, int Hn, const float *q, int ldq, const int32_t *types
 void forces_and_virial(const Records &r, const float4 *g, float *forces, float *atom_virial,
                        hipStream_t s);
 // out[b, c] = sum over atoms of structure b of x[m, c] (fixed order, fp64 accumulation)
-void structure_sum(const Records &r, const float *x, int ncol, float *out, hipStream_t s);
+// (fixed order for a given structure layout).  Structures larger than
+// kSumChunk atoms are split over several blocks whose fp64 partials go to
+// scratch; structure_sum_scratch(r, ncol) doubles are needed (0: none).
+constexpr int kSumChunk = 8192;
+size_t structure_sum_scratch(const Records &r, int ncol);
+void structure_sum(const Records &r, const float *x, int ncol, float *out, double *scratch,
+                   hipStream_t s);
 
 }  // namespace rune

@@ -352,6 +352,10 @@ static Records records_of(const rune_nlist *nl) {
     r.sptr = nl->sptr.as<int32_t>();
     r.n_structures = nl->n_structures;
     r.order = nl->has_order ? nl->order.as<int32_t>() : nullptr;
+    r.max_struct_atoms = 0;
+    for (size_t b = 0; b + 1 < nl->h_struct_ptr.size(); ++b)
+        r.max_struct_atoms = std::max(r.max_struct_atoms,
+                                      int(nl->h_struct_ptr[b + 1] - nl->h_struct_ptr[b]));
     return r;
 }
 
@@ -454,10 +458,12 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     descriptor_reverse(d, m.zbl, r, types, dq, ldq, mom, dmom, g_direct, energies, g,
                        grad ? 1 : 0, s);
     mark(7);
-    if (d_energy) structure_sum(r, energies, 1, d_energy, s);
+    m.sums.reserve(sizeof(double) * std::max<size_t>(1, structure_sum_scratch(r, 9)));
+    double *sums = m.sums.as<double>();
+    if (d_energy) structure_sum(r, energies, 1, d_energy, sums, s);
     if (grad) {
         forces_and_virial(r, g, forces, atom_virial, s);
-        if (want_w && d_virial) structure_sum(r, atom_virial, 9, d_virial, s);
+        if (want_w && d_virial) structure_sum(r, atom_virial, 9, d_virial, sums, s);
     }
     mark(8);
 }

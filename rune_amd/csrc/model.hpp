@@ -107,6 +107,7 @@ struct ModelImpl {
     bool finalized = false;
     DeviceBuffer weights;
     DeviceBuffer work;
+    DeviceBuffer sums;        // fp64 partial sums of the split structure reductions
     DeviceBuffer gpumd_out;   // fp32 energies, forces, atom virial of rune_model_compute_gpumd
     DescTables desc{};
     ZblTables zbl{};
