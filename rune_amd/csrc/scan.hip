@@ -1,4 +1,5 @@
-// Deterministic exclusive scan of int32 counts (three passes, fixed order).
+// Deterministic exclusive scan of int32 counts (fixed order): one workgroup
+// for short inputs, three passes otherwise.
 #include "nlist.hpp"
 
 namespace rune {
@@ -57,11 +58,36 @@ __global__ void add_offsets(int32_t *out, int64_t n, const int32_t *block_sums,
     if (i < n) out[i] += block_sums[blockIdx.x];
     if (i == n) out[n] = *grand_total;
 }
+// Single workgroup, for short inputs: thread t scans its own contiguous run
+// of per elements serially, the run totals are scanned across the block, and
+// each run is written with its offset.  One launch instead of three.
+constexpr int kOneBlockMax = kScanBlock * 64;
+__global__ void __launch_bounds__(kScanBlock) scan_one_block(const int32_t *in, int32_t *out,
+                                                             int n) {
+    __shared__ int32_t lds[kScanBlock];
+    __shared__ int32_t total;
+    const int per = (n + kScanBlock - 1) / kScanBlock;
+    const int lo = min(n, int(threadIdx.x) * per), hi = min(n, lo + per);
+    int32_t run = 0;
+    for (int i = lo; i < hi; ++i) run += in[i];
+    int32_t off = block_exclusive(run, lds, &total);
+    for (int i = lo; i < hi; ++i) {
+        const int32_t v = in[i];
+        out[i] = off;
+        off += v;
+    }
+    if (threadIdx.x == 0) out[n] = total;
+}
 }  // namespace
 
 size_t scan_tmp_ints(int64_t n) { return size_t(ceil_div(n + 1, kScanBlock)) + 2; }
 
 void exclusive_scan(const int32_t *in, int32_t *out, int64_t n, int32_t *tmp, hipStream_t s) {
+    if (n <= kOneBlockMax) {
+        hipLaunchKernelGGL(scan_one_block, dim3(1), dim3(kScanBlock), 0, s, in, out, int(n));
+        RUNE_HIP_CHECK(hipGetLastError());
+        return;
+    }
     int nb = ceil_div(n + 1, kScanBlock);
     int32_t *sums = tmp;
     int32_t *grand = tmp + nb;
