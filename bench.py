@@ -137,8 +137,8 @@ def group_model(ev, prep, n_records, params):
             + E * (8 * G + 12 + 8) + N * 4 * H * 3
             # edge adjoints, both sides: dE/du, harm, dE/dY r/w, ids; Q in; dQ, dA | dB out
             + 2 * (E * (4 * D + 4 * nq + 8 * nq + 4) + 2 * qbytes + N * 4 * D))
-        # harmonic reverse: vec, fc, dE/dY (two), dE/dfc, dE/drb, rb derivative, dv r/w
-        once = (prep_bytes + direct + E * (16 + 4 + 8 * nq + 4 + 8 * ldrb + 32) + N * 16)
+        # harmonic reverse: vec, fc, dE/dY, dE/dfc, dE/drb, rb derivative, dv r/w
+        once = (prep_bytes + direct + E * (16 + 4 + 4 * nq + 4 + 8 * ldrb + 32) + N * 16)
     else:
         vc = p["vector_channels"]
         NP, NG = H + vc, G + vc
