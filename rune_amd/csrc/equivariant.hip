@@ -1465,8 +1465,19 @@ __global__ void k_eq_harmonic_backward(int64_t E, Records r, const float *fcv, c
     acc.y += dyy;
     acc.z += dz;
     if (fcv[e] != 0.0f) {
+        // 16-byte row reads (ldrb is a multiple of 4); the padding columns
+        // are skipped, so the sum is the plain k-ordered one
+        const float4 *d4 = reinterpret_cast<const float4 *>(drb + size_t(e) * ldrb);
+        const float4 *r4 = reinterpret_cast<const float4 *>(rbd + size_t(e) * ldrb);
         float t = 0.0f;
-        for (int k = 0; k < kb; ++k) t += drb[size_t(e) * ldrb + k] * rbd[size_t(e) * ldrb + k];
+        for (int q = 0; 4 * q < kb; ++q) {
+            const float4 a = d4[q], b = r4[q];
+            const int k = 4 * q;
+            t += a.x * b.x;
+            if (k + 1 < kb) t += a.y * b.y;
+            if (k + 2 < kb) t += a.z * b.z;
+            if (k + 3 < kb) t += a.w * b.w;
+        }
         acc.w += dfc[e] * cutoff_slope(v.w, cutoff) + t;
     }
     dv[e] = acc;
