@@ -128,6 +128,7 @@ struct EqArgs {
     float4 *dv;               // [E]
     float *dfc;               // [E] dE/dfc of the message terms, all blocks
     float *dy;                // [E, nq] dE/dY (both sides' shares, accumulated in turn)
+    const float *dy_old;      // dy, or (first reverse block) a zero row: nothing to add to
     float *dnode;             // [N, NP]
     float *dmix;              // [N, C*nq]
     const float *due;         // [E, D]
@@ -846,7 +847,9 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
             f = q < cnt ? fq : 0.0f;
             e = q < cnt ? ec : -1;
 #pragma unroll
-            for (int u = 0; u < KQ; ++u) yo[u] = a.dy[size_t(ec) * NQ + min(ln.c + W * u, NQ - 1)];
+            for (int u = 0; u < KQ; ++u)
+                yo[u] = a.dy_old[(a.dy_old == a.dy ? size_t(ec) * NQ : 0) +
+                                 min(ln.c + W * u, NQ - 1)];
             load_row(dh, a.dht + size_t(i) * CN + cl * NQ);
             const float *gr = a.ag + size_t(ec) * NG + G + cl;
 #pragma unroll
@@ -905,7 +908,9 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
             const float dold = bcast(md, min(q, kWave - 1));
             if (on && ln.c == 0) a.dfc[e] = dold + contrib;
             wave_sync();
-            if (on) {
+            // the first reverse block writes every record's row (dy holds no
+            // earlier shares, so it is not cleared beforehand)
+            if (on || (e >= 0 && a.dy_old != a.dy)) {
 #pragma unroll
                 for (int u = 0; u < KQ; ++u) {
                     const int k = ln.c + W * u;
@@ -922,7 +927,7 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
                         }
                         float sum = (s4.x + s4.y) + (s4.z + s4.w);
                         for (; c < C; ++c) sum += row[c];
-                        a.dy[size_t(e) * NQ + k] = yo[u] + sum;
+                        a.dy[size_t(e) * NQ + k] = yo[u] + (on ? sum : 0.0f);
                     }
                 }
             }
@@ -1891,6 +1896,7 @@ MessagePlan plan_equivariant(ModelImpl &m, Arena &ar, int N, int64_t E) {
     p.i_dv = p.add(ar, 16 * e);
     p.i_harm = p.add(ar, 4 * e * nq);
     p.i_dharm = p.add(ar, 4 * e * nq);
+    p.i_zero = p.add(ar, 4 * 64);   // a zero row of >= nq floats
     p.i_dfc = p.add(ar, 4 * e);
     p.i_drb = p.add(ar, 4 * e * p.ldrb);
     p.i_rbd = p.add(ar, 4 * e * p.ldrb);
@@ -1993,6 +1999,7 @@ static EqArgs eq_args(ModelImpl &m, MessagePlan &p, const Records &r, int b) {
     a.dv = reinterpret_cast<float4 *>(p.at(p.i_dv));
     a.dfc = p.at(p.i_dfc);
     a.dy = p.at(p.i_dharm);
+    a.dy_old = a.dy;
     a.dnode = p.at(p.t_dvs);
     a.dmix = p.at(p.t_dmix);
     a.due = p.at(p.t_due);
@@ -2021,7 +2028,8 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
             hipLaunchKernelGGL(k_gather_f, dim3(ceil_div(E, 256)), dim3(256), 0, s, E, r.tidx,
                                p.at(p.i_fc), p.at(p.i_tfc));
         }
-        RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dharm), 0, 4 * size_t(E) * nq, s));
+        // dE/dY needs no clearing: the first reverse block writes every row
+        RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_zero), 0, 4 * 64, s));
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dfc), 0, 4 * size_t(E), s));
     }
     {
@@ -2120,6 +2128,7 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         const MessageWeights &w = m.msg[b];
         const BlockBuffers &bb = p.blocks[b];
         EqArgs a = eq_args(m, p, r, b);
+        if (b == c.message_layers - 1) a.dy_old = p.at(p.i_zero);
         a.ddir_out = ddir_out;
         a.ddir_in = ddir_in;
         Epilogue e0;

@@ -82,7 +82,7 @@ struct MessagePlan {
     size_t o_gd = 0, o_dmom = 0;
     int ldrb = 0;
     int ld_edge = 0;              // EQ: row stride of the per-record [E, D] arrays
-    int i_rb = -1, i_fc = -1, i_tfc = -1, i_pair = -1, i_dv = -1, i_harm = -1, i_dharm = -1;
+    int i_rb = -1, i_fc = -1, i_tfc = -1, i_pair = -1, i_dv = -1, i_harm = -1, i_dharm = -1, i_zero = -1;
     int i_dfc = -1, i_drb = -1, i_rbd = -1;
     std::vector<BlockBuffers> blocks;
     // reverse-pass temporaries shared by the blocks
