@@ -295,12 +295,30 @@ __global__ void __launch_bounds__(256) k_eq_mix(int N, const float *mixw, const 
         }
         __syncthreads();
     }
-    for (int n0 = blockIdx.x * 4; n0 < N; n0 += gridDim.x * 4) {
-        const int n = n0 + wave;
-        if (n >= N) continue;
+    // the next atom's input row is loaded into registers while this one is
+    // processed (lane-strided floats, clamped so every lane loads)
+    // (when a row is at most 16 floats per lane; wider rows are staged directly)
+    constexpr int PF = (16 * MT * NQ + kWave - 1) / kWave;
+    constexpr bool kPre = PF <= 16;
+    const int stride = int(gridDim.x) * 4;
+    float pre[kPre ? PF : 1];
+    auto load_in = [&](int n) {
+#pragma unroll
+        for (int u = 0; u < (kPre ? PF : 1); ++u)
+            pre[u] = in[size_t(n) * CN + min(lane + kWave * u, CN - 1)];
+    };
+    if constexpr (kPre) load_in(min(int(blockIdx.x) * 4 + wave, N - 1));
+    for (int n = int(blockIdx.x) * 4 + wave; n < N; n += stride) {
         wave_sync();
         // rows move between HBM and LDS contiguously; add_t is transposed in LDS
-        stage_row(row, in + size_t(n) * CN, CN);
+        if constexpr (kPre) {
+#pragma unroll
+            for (int u = 0; u < PF; ++u)
+                if (lane + kWave * u < CN) row[lane + kWave * u] = pre[u];
+            load_in(min(n + stride, N - 1));
+        } else {
+            stage_row(row, in + size_t(n) * CN, CN);
+        }
         if (add) {
             stage_row(res, add + size_t(n) * CN, CN);
         } else {
