@@ -347,7 +347,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build evaluates on one GPU only; the multi-GPU "
-                          "(spatial decomposition) path is a design, see DESIGN.md"}))
+                          "path (spatial domains with ghost halos exchanged over RCCL) is "
+                          "designed, not built"}))
         sys.exit(2)
     res = run_gpu(args)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.workload, args.cpu_budget)
