@@ -149,11 +149,26 @@ __global__ void __launch_bounds__(256) k_eq_encode(int N, const float *s, int na
     float *row = lds + lq * C * na + wave * wrow;    // [na][nlm]
     for (int o = threadIdx.x; o < lq * C * na; o += blockDim.x) W[o] = enc[o];
     __syncthreads();
-    for (int i0 = blockIdx.x * 4; i0 < N; i0 += gridDim.x * 4) {
-        const int i = i0 + wave;
-        if (i >= N) continue;
+    // the next atom's moment row is loaded into registers while this one is
+    // processed (rows of up to 4 floats per lane; longer rows are staged directly)
+    const int RN = na * nlm, stride = int(gridDim.x) * 4;
+    const bool pre = RN <= 4 * kWave;
+    float pv[4];
+    auto load_pre = [&](int i) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) pv[u] = s[size_t(i) * RN + min(lane + kWave * u, RN - 1)];
+    };
+    if (pre) load_pre(min(int(blockIdx.x) * 4 + wave, N - 1));
+    for (int i = int(blockIdx.x) * 4 + wave; i < N; i += stride) {
         wave_sync();
-        stage_row(row, s + size_t(i) * na * nlm, na * nlm);
+        if (pre) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (lane + kWave * u < RN) row[lane + kWave * u] = pv[u];
+            load_pre(min(i + stride, N - 1));
+        } else {
+            stage_row(row, s + size_t(i) * RN, RN);
+        }
         wave_sync();
         for (int o = lane; o < C * nq; o += kWave) {
             const int c = o / nq, k = o - c * nq, L = order_of(k);
