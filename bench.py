@@ -155,6 +155,58 @@ def group_model(ev, prep, n_records, params):
     return {"edge_gemm": ("mfma", flops), "edge_kernels": ("hbm", B * per_block + once)}
 
 
+def algorithmic_model(ev, params, n_atoms, e_radial, e_angular):
+    """Algorithmic work of one evaluation, kernel by kernel: unique compulsory
+    HBM bytes (fp32 values, int32 indices; each per-atom / per-edge array
+    counted once per kernel that reads or writes it; weights and coefficient
+    tables excluded; no cache credit, no re-read penalty) and the FLOPs of the
+    dense layers (forward + input-gradient backward, no weight gradients).
+    Per message block, with H hidden, md message width, vc vector channels,
+    S = 4 C ec bytes of one atom's angular state (C = l(l+2) components,
+    ec channels):
+      MP  forward  8N + 16E_r + 8HN + 16 vc N
+      MP  backward 8N + 16E_r + 12HN + 20 vc N + 24E_r
+      EQ  forward  8N + 16E_r + 8HN + 8 md N + 3 S N
+      EQ  backward 8N + 16E_r + 12HN + 16 md N + 5 S N + 24E_r
+    and per evaluation: neighbour build 24N + 20E_r + 16E_a, descriptor
+    forward 12N + 16(E_r + E_a) + 4QN + 96 n_a N, its reverse 12N + 16(E_r +
+    E_a) + 4QN + 96 n_a N (x2 with EQ moment adjoints) + 12E_r, forces and
+    virials 16N + 32E_r.  Per-edge dense FLOPs of an EQ block count the
+    factored edge MLP (K = kb + 2 ec l), the group gate and the direction
+    gates; of an MP block its edge MLP and gates."""
+    p = params
+    N, Er, Ea = n_atoms, e_radial, e_angular
+    nr, na = p["n_desc_radial"], p["n_desc_angular"]
+    num_L = p["l_max"] + sum(int(p.get(k, 0)) for k in
+                             ("has_q_222", "has_q_1111", "has_q_112", "has_q_123", "has_q_233",
+                              "has_q_134"))
+    Q = nr + na * num_L
+    eq = p.get("message_mode", "scalar") == "equivariant"
+    nb = int(p.get("message_layers", 0)) if ev.family == 0 else 0
+    out = {"neighbors": 24 * N + 20 * Er + 16 * Ea,
+           "descriptor": 12 * N + 16 * (Er + Ea) + 4 * Q * N + 96 * na * N,
+           "reverse": 12 * N + 16 * (Er + Ea) + 4 * Q * N + 96 * na * N * (2 if eq else 1)
+                      + 12 * Er,
+           "forces": 16 * N + 32 * Er, "message_bytes": 0, "message_flops": 0}
+    if nb:
+        H, md = p["hidden_dim"], p["message_dim"]
+        kb, G = p["message_basis_size"], p["message_groups"]
+        if eq:
+            ec, lq = p["equivariant_channels"], p["equivariant_l_max"]
+            S = 4 * lq * (lq + 2) * ec
+            fwd = 8 * N + 16 * Er + 8 * H * N + 8 * md * N + 3 * S * N
+            bwd = 8 * N + 16 * Er + 12 * H * N + 16 * md * N + 5 * S * N + 24 * Er
+            per_edge = 2 * (kb + 2 * ec * lq) * md + 2 * md * G + 2 * md * 2 * ec * lq
+        else:
+            vc, pd = p["vector_channels"], p["pair_dim"]
+            fwd = 8 * N + 16 * Er + 8 * H * N + 16 * vc * N
+            bwd = 8 * N + 16 * Er + 12 * H * N + 20 * vc * N + 24 * Er
+            per_edge = 2 * (kb + pd) * md + 2 * md * (G + vc)
+        out["message_bytes"] = nb * (fwd + bwd)
+        out["message_flops"] = nb * 2 * per_edge * Er
+    return out
+
+
 def measured_traffic(workload, group):
     """HBM bytes per launch of a kernel group from the committed counter
     summary (rocprofv3 FETCH_SIZE / WRITE_SIZE runs, calibrated by a plain copy
@@ -215,9 +267,15 @@ def run_gpu(args):
         nl_ms.append(a.elapsed_time(b))
     n_atoms = prep.n_atoms
     n_records = ev.nlist.n_records
+    view = ev.nlist.export()["view"].long()
+    e_radial = int((view[:, 1] - view[:, 0]).sum())
+    e_angular = int((view[:, 3] - view[:, 2]).sum())
+    algo = algorithmic_model(ev, params, n_atoms, e_radial, e_angular)
     ms_per_step = max(gpu_ms, wall * 1e3) / args.steps
     value = n_atoms * args.steps / (ms_per_step * args.steps / 1e3)
     model = phase_model(ev, prep, n_records, None, params)
+    for name in ("descriptor", "reverse", "forces"):
+        model[name] = ("hbm", algo[name])
     per_phase = {}
     for name, total in phases.items():
         avg = total / max(calls, 1)
@@ -233,8 +291,16 @@ def run_gpu(args):
                 entry.update(bound="mfma", flops=int(work), achieved_TFs=round(ach / 1e12, 2),
                              frac=round(ach / FP32_PEAK, 4))
         per_phase[name] = entry
-    per_phase["neighbors"] = {"ms": round(statistics.median(nl_ms), 4)}
-    # kernel groups: per-launch averages from the events around each launch
+    nb_ms = statistics.median(nl_ms)
+    per_phase["neighbors"] = {"ms": round(nb_ms, 4), "bound": "hbm",
+                              "bytes": int(algo["neighbors"]),
+                              "achieved_GBs": round(algo["neighbors"] / (nb_ms / 1e3) / 1e9, 1),
+                              "frac": round(algo["neighbors"] / (nb_ms / 1e3) / HBM_PEAK, 4),
+                              "note": "events around the whole build, count readback included"}
+    # kernel groups: per-launch averages from the events around each launch.
+    # edge_kernels: the algorithmic bytes are the message blocks' (forward and
+    # backward, all blocks) spread over the group's launches; the build's own
+    # per-record arrays are reported beside them as materialised_bytes.
     gmodel = group_model(ev, prep, n_records, params)
     per_group = {}
     if gmodel:
@@ -242,6 +308,9 @@ def run_gpu(args):
             if launches == 0:
                 continue
             bound, work = gmodel[name]
+            if name == "edge_kernels":
+                materialised = work * calls / launches
+                work = algo["message_bytes"]
             work_launch = work * calls / launches       # model is per call
             avg = ms / launches
             ach = work_launch / (avg / 1e3)
@@ -249,7 +318,8 @@ def run_gpu(args):
                  "avg_ms": round(avg, 4), "bound": bound}
             if bound == "hbm":
                 g.update(bytes_per_launch=int(work_launch), achieved_GBs=round(ach / 1e9, 1),
-                         frac=round(ach / HBM_PEAK, 4))
+                         frac=round(ach / HBM_PEAK, 4),
+                         materialised_bytes_per_launch=int(materialised))
             else:
                 g.update(flops_per_launch=int(work_launch), achieved_TFs=round(ach / 1e12, 2),
                          frac=round(ach / FP32_PEAK, 4))
@@ -271,12 +341,26 @@ def run_gpu(args):
         roof = {"kernel": dom, "bound": "hbm", "achieved": d["achieved_GBs"],
                 "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": d["frac"], "traffic": traffic,
                 "algorithmic_bytes": d["bytes"], "avg_ms": d["ms"]}
+        if "materialised_bytes_per_launch" in d:
+            roof["materialised_bytes"] = d["materialised_bytes_per_launch"]
+            if traffic:
+                roof["traffic_per_step"] = int(traffic * d["launches_per_step"])
     else:
         roof = {"kernel": dom, "bound": "mfma", "achieved": d["achieved_TFs"],
                 "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s", "frac": d["frac"],
                 "traffic": traffic, "algorithmic_flops": d["flops"], "avg_ms": d["ms"]}
+    edge_ms = sum(per_phase.get(k, {}).get("ms", 0.0) for k in
+                  ("neighbors", "descriptor", "reverse", "forces"))
+    edge_ms += per_group.get("edge_kernels", {}).get("ms_per_step", 0.0)
+    edge_bytes = algo["neighbors"] + algo["descriptor"] + algo["reverse"] + algo["forces"] + \
+        algo["message_bytes"]
+    edge_summary = {"bytes_per_step": int(edge_bytes), "ms_per_step": round(edge_ms, 4),
+                    "frac": round(edge_bytes / (edge_ms / 1e3) / HBM_PEAK, 4) if edge_ms else None,
+                    "kernels": "neighbour build, descriptor forward / reverse, forces, "
+                               "per-record message kernels"}
     return {
         "value": value, "ms_per_step": ms_per_step, "n_atoms": n_atoms, "n_records": n_records,
+        "e_radial": e_radial, "e_angular": e_angular, "edge_kernels_hbm": edge_summary,
         "roofline": roof, "phases": per_phase, "groups": per_group,
         "energy": float(out["energy"].double().sum().cpu()),
     }
@@ -329,9 +413,39 @@ def cpu_baseline(workload, budget_s):
         if len(times) >= 3 and time.perf_counter() > t_end:
             break
     med = statistics.median(times[1:]) if len(times) > 1 else times[0]
+    # calculator end to end: the neighbour search (the oracle's cell-list
+    # restatement of batch.py:42-102) plus the same evaluation
+    e2e = []
+    t_end = time.perf_counter() + budget_s / 2
+    while len(e2e) < 2 or (time.perf_counter() < t_end and len(e2e) < 20):
+        t0 = time.perf_counter()
+        nl = ONB.build(struct.positions, struct.cell, struct.pbc, params["rcut_radial"],
+                       params["rcut_angular"])
+        sp = ONB.split(nl)
+        ed = {k: OM.Edges(torch.as_tensor(v[0]), torch.as_tensor(v[1]),
+                          torch.as_tensor(v[2], dtype=torch.float32)) for k, v in sp.items()}
+        fwd(w, params, pos, types, [len(struct)], ed["radial"], ed["angular"])
+        e2e.append(time.perf_counter() - t0)
+    e2e_med = statistics.median(e2e)
     return {"value": len(struct) / med, "unit": "atom-steps/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model(),
+            "calculator_end_to_end": {"value": len(struct) / e2e_med, "unit": "atom-steps/s",
+                                      "ms_per_call": round(e2e_med * 1e3, 2),
+                                      "calls": len(e2e)},
             "sample": f"{sample}; median of {len(times) - 1} calls after 1 warm-up, "
-                      f"{med * 1e3:.1f} ms/call"}
+                      f"{med * 1e3:.1f} ms/call; calculator_end_to_end adds the neighbour "
+                      f"search (median of {len(e2e)} calls)"}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def main():
@@ -359,9 +473,10 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded generator); trained OAM weights / seeded NEP",
         "config": {"workload": args.workload, "description": WORKLOADS[args.workload],
-                   "n_atoms": res["n_atoms"], "records": res["n_records"]},
+                   "n_atoms": res["n_atoms"], "records": res["n_records"],
+                   "radial_edges": res["e_radial"], "angular_edges": res["e_angular"]},
         "roofline": res["roofline"], "cpu_baseline": cpu, "phases": res["phases"],
-        "groups": res["groups"],
+        "groups": res["groups"], "edge_kernels_hbm": res["edge_kernels_hbm"],
     }
     print(json.dumps(line), flush=True)
 

@@ -634,6 +634,8 @@ def _reduce(energies, counts, forces, atomic_virial):
         v = atomic_virial.new_zeros((nb, 9))
         v.scatter_add_(0, sid.unsqueeze(-1).expand_as(atomic_virial), atomic_virial)
         out["virial"] = v
+        # per-atom virial attributed to the neighbour atom (model.py:23-44)
+        out["atom_virial"] = atomic_virial
     return out
 
 

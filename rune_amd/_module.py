@@ -4,8 +4,12 @@ The shell holds parameters and buffers under the reference's state_dict
 names (so ``load_state_dict(strict=True)`` accepts the reference
 checkpoints), and its ``forward(batch)`` evaluates through the HIP library:
 the padded reference batch (``rune/mobius/interface/batch.py:124-166``) is
-converted to records on the device and ``rune_model_compute`` returns
-energies, forces and virials.  There is no PyTorch/CPU evaluation path.
+converted to records on the HIP device and ``rune_model_compute`` returns
+energies, forces and virials.  There is no PyTorch/CPU evaluation path: a
+batch whose tensors live on the host is evaluated on the current HIP device
+and the results come back on the batch's device.  The kernels compute in
+float32; a float64 module (the reference keeps float64 checkpoints float64)
+is evaluated with float32 copies of its weights and returns its own dtype.
 """
 
 from __future__ import annotations
@@ -32,10 +36,7 @@ class HipPotential(nn.Module):
     def native(self):
         key = self._state_key()
         if self._native is None or key != self._native_key:
-            dtypes = {t.dtype for t in self.state_dict().values() if t.is_floating_point()}
-            if dtypes - {torch.float32}:
-                raise TypeError("the HIP evaluator computes in float32; convert the model "
-                                f"with .float() (found {sorted(map(str, dtypes))})")
+            # NativeModel hands the weights over as float32 copies
             self._native = N.NativeModel(self.params, self.state_dict(), self.family)
             self._native_key = key
         return self._native
@@ -53,20 +54,22 @@ class HipPotential(nn.Module):
         compute_forces = bool(batch.get("compute_forces", True))
         compute_virial = bool(batch.get("compute_virial", True))
         positions = batch["positions"]
-        N.require_device(positions.device)
+        dev = N.compute_device(positions.device)
+        to_dev = lambda t, dtype=None: t.detach().to(device=dev, dtype=dtype)
         counts = batch["n_atoms_per_structure"].detach().to("cpu", torch.long)
         struct_ptr = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)]).numpy()
         nl = self.neighbor_list().from_padded(
-            positions.detach().to(torch.float32), batch["radial_neighbors"],
-            batch["radial_offsets"], batch["angular_neighbors"], batch["angular_offsets"],
-            struct_ptr)
-        out = self.native().compute(nl, batch["types"], len(struct_ptr) - 1, compute_forces,
-                                    compute_virial)
-        result = {"energies": out["energies"], "energy": out["energy"]}
+            to_dev(positions, torch.float32), to_dev(batch["radial_neighbors"]),
+            to_dev(batch["radial_offsets"], torch.float32), to_dev(batch["angular_neighbors"]),
+            to_dev(batch["angular_offsets"], torch.float32), struct_ptr)
+        out = self.native().compute(nl, to_dev(batch["types"]), len(struct_ptr) - 1,
+                                    compute_forces, compute_virial)
+        back = lambda t: t.to(device=positions.device, dtype=positions.dtype)
+        result = {"energies": back(out["energies"]), "energy": back(out["energy"])}
         if compute_forces:
-            result["forces"] = out["forces"]
+            result["forces"] = back(out["forces"])
         if compute_virial:
-            result["virial"] = out["virial"]
+            result["virial"] = back(out["virial"])
         return result
 
 

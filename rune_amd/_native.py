@@ -118,6 +118,26 @@ def require_device(device):
     return device
 
 
+def compute_device(device=None):
+    """HIP device that evaluates for a drop-in object placed on ``device``.
+
+    The reference's calculator and batch builder take a torch ``device``
+    (default ``"cpu"``) that decides where the model and its tensors live.
+    Here the evaluation always runs on a HIP device: a ``cuda`` device is used
+    as given, any other placement (``"cpu"``, ``None``) evaluates on the
+    current HIP device and hands results back on the placement device.
+    Raises when no HIP device is visible (there is no CPU evaluation path).
+    """
+    dev = torch.device(device) if device is not None else torch.device("cpu")
+    if dev.type == "cuda":
+        return require_device(dev)
+    if not torch.cuda.is_available():
+        raise RuntimeError(
+            "the rune_amd evaluator runs on an MI355X (HIP) device only and none is visible "
+            f"(placement device {dev!s})")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
 def _ptr(t):
     return C.c_void_p(t.data_ptr()) if t is not None else None
 

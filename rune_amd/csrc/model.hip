@@ -408,7 +408,13 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     RUNE_HIP_CHECK(hipMemcpyAsync(&hflag, flag, 4, hipMemcpyDeviceToHost, s));
     RUNE_HIP_CHECK(hipStreamSynchronize(s));
     RUNE_REQUIRE(hflag == 0, RUNE_ERR_TYPE, "atom type outside [0, n_types)");
-    if (N == 0) return;
+    if (N == 0) {
+        // no atoms: every structure's energy and virial is zero (the sums
+        // over empty ranges read nothing)
+        if (d_energy) structure_sum(r, energies, 1, d_energy, nullptr, s);
+        if (want_w && d_virial) structure_sum(r, atom_virial, 9, d_virial, nullptr, s);
+        return;
+    }
     hipEvent_t *ev = nullptr;
     if (m.timing) {
         if (m.events.empty()) {

@@ -26,7 +26,10 @@ struct Geo {
     double cell[9];     // rows = lattice vectors
     double inv[9];      // inverse of cell (frac = p . inv)
     int pbc[3];
-    int nb[3];          // bins per direction
+    int nb[3];          // periodic directions: bins per cell period
+    double bs[3];       // bins per unit of fractional coordinate (nb when periodic)
+    double lo[3];       // open directions: lowest bin index holding an atom (0 otherwise)
+    int nbin[3];        // bins in use per direction (nb for periodic directions)
     int m[3];           // stencil reach per direction
     int bin_offset;     // first global bin of this structure
     int atom_begin, atom_end;
@@ -64,11 +67,13 @@ __global__ void bin_atoms(int n, const double *pos, const int32_t *sptr, int nst
             w[d] = int(fl);
             fd -= fl;
         }
-        double x = floor(fd * g.nb[d]);
-        x = fmin(fmax(x, 0.0), double(g.nb[d] - 1));
+        // open directions: bins from the lowest one holding an atom, so no
+        // atom is clamped into an edge bin (the clamp is only a safety net)
+        double x = floor(fd * g.bs[d]) - g.lo[d];
+        x = fmin(fmax(x, 0.0), double(g.nbin[d] - 1));
         b[d] = int(x);
     }
-    int flat = g.bin_offset + (b[0] * g.nb[1] + b[1]) * g.nb[2] + b[2];
+    int flat = g.bin_offset + (b[0] * g.nbin[1] + b[1]) * g.nbin[2] + b[2];
     atom_bin[i] = flat;
     atom_wrap[3 * i + 0] = w[0];
     atom_wrap[3 * i + 1] = w[1];
@@ -86,6 +91,41 @@ __global__ void fill_bins(int n, const int32_t *atom_bin, const int32_t *bin_sta
     int b = atom_bin[i];
     int slot = atomicAdd(bin_cursor + b, 1);
     bin_atoms[bin_start[b] + slot] = i;
+}
+
+// Order-preserving map of a double to 64 bits (for integer atomic min / max).
+__device__ inline unsigned long long ordered_bits(double x) {
+    const unsigned long long u = (unsigned long long)__double_as_longlong(x);
+    return (u >> 63) ? ~u : (u | 0x8000000000000000ull);
+}
+
+// Extent of each structure's fractional coordinates along its open
+// (non-periodic) directions: ext[3 s + d] = min, ext[3 (nstruct + s) + d] =
+// max, as ordered bits (min entries start all ones, max entries zero).  Lanes past
+// the end stand in for the last atom (min / max are idempotent); a wave whose
+// lanes share one structure combines them before its atomics.
+__global__ void frac_extent(int n, const double *pos, const int32_t *sptr, int nstruct,
+                            const Geo *geo, unsigned long long *ext) {
+    const int i = min(int(blockIdx.x * blockDim.x + threadIdx.x), n - 1);
+    const int s = find_structure(sptr, nstruct, i);
+    const Geo &g = geo[s];
+    double f[3];
+    frac_of(g, pos + 3 * i, f);
+    double lo[3] = {f[0], f[1], f[2]}, hi[3] = {f[0], f[1], f[2]};
+    const bool uniform = __all(s == __shfl(s, 0)) != 0;
+    if (uniform) {
+        for (int off = 32; off > 0; off >>= 1)
+            for (int d = 0; d < 3; ++d) {
+                lo[d] = fmin(lo[d], __shfl_xor(lo[d], off));
+                hi[d] = fmax(hi[d], __shfl_xor(hi[d], off));
+            }
+    }
+    if (uniform && (threadIdx.x & 63) != 0) return;
+    for (int d = 0; d < 3; ++d) {
+        if (g.pbc[d]) continue;
+        atomicMin(ext + 3 * s + d, ordered_bits(lo[d]));
+        atomicMax(ext + 3 * (nstruct + s) + d, ordered_bits(hi[d]));
+    }
 }
 
 // Atoms listed bin by bin in the rank order perm (bins of all structures):
@@ -118,14 +158,35 @@ __device__ inline double pair_d2(const double *pos, const Geo &g, int i, int j, 
     return r2;
 }
 
-// Packs (class, j, S) into an ordered 64-bit key.
+// Record keys.  A 64-bit key holds the class (bits 62-63), the neighbour
+// index j (bits 32-61; atom counts are below 2^30) and the image shift S as
+// three 10-bit fields offset by kShiftBias (bits 20-29, 10-19, 0-9), so
+// ascending keys order a centre's records by (class, j, S0, S1, S2).  A shift
+// outside [-kShiftBias, kShiftBias) (an atom more than 511 periods from the
+// cell) has no key: the builder reports it instead of aliasing it.
+constexpr int kShiftBias = 512;
+
+__device__ inline bool shift_fits(const int *S) {
+    bool ok = true;
+    for (int d = 0; d < 3; ++d) ok = ok && S[d] >= -kShiftBias && S[d] < kShiftBias;
+    return ok;
+}
+
 __device__ inline uint64_t make_key(int cls, int j, const int *S) {
     uint64_t k = uint64_t(cls) << 62;
-    k |= uint64_t(uint32_t(j)) << 24;
-    k |= uint64_t(uint32_t(S[0] + 128) & 0xff) << 16;
-    k |= uint64_t(uint32_t(S[1] + 128) & 0xff) << 8;
-    k |= uint64_t(uint32_t(S[2] + 128) & 0xff);
+    k |= uint64_t(uint32_t(j)) << 32;
+    k |= uint64_t(uint32_t(S[0] + kShiftBias) & 0x3ff) << 20;
+    k |= uint64_t(uint32_t(S[1] + kShiftBias) & 0x3ff) << 10;
+    k |= uint64_t(uint32_t(S[2] + kShiftBias) & 0x3ff);
     return k;
+}
+
+__device__ inline int key_neighbor(uint64_t key) { return int((key >> 32) & 0x3fffffffull); }
+
+__device__ inline void key_shift(uint64_t key, int *S) {
+    S[0] = int((key >> 20) & 0x3ff) - kShiftBias;
+    S[1] = int((key >> 10) & 0x3ff) - kShiftBias;
+    S[2] = int(key & 0x3ff) - kShiftBias;
 }
 
 // Candidate enumeration, one atom per wave, in one pass: the stencil cells
@@ -218,11 +279,11 @@ __global__ void __launch_bounds__(256) enumerate_flat(
                     bb[d] = b - t * g.nb[d];
                 } else {
                     bb[d] = b;
-                    ok = ok && (b >= 0 && b < g.nb[d]);
+                    ok = ok && (b >= 0 && b < g.nbin[d]);
                 }
             }
             if (ok) {
-                const int flat = g.bin_offset + (bb[0] * g.nb[1] + bb[1]) * g.nb[2] + bb[2];
+                const int flat = g.bin_offset + (bb[0] * g.nbin[1] + bb[1]) * g.nbin[2] + bb[2];
                 beg = bin_start[flat];
                 cnt = bin_start[flat + 1] - beg;
             }
@@ -261,6 +322,10 @@ __global__ void __launch_bounds__(256) enumerate_flat(
                     pass = r2 < rc2_max;
                     in_r = r2 < rc2_r;
                     in_a = r2 < rc2_a;
+                    if (pass && !shift_fits(S)) {
+                        atomicOr(error_flag, 2);
+                        pass = false;
+                    }
                 }
             }
             const uint64_t bp = __ballot(pass);
@@ -306,10 +371,8 @@ __global__ void __launch_bounds__(256) refilter_wave(
         int j = 0, S[3] = {0, 0, 0};
         if (t < m) {
             const uint64_t key = row[t];
-            j = int((key >> 24) & 0x3fffffffffull);
-            S[0] = int((key >> 16) & 0xff) - 128;
-            S[1] = int((key >> 8) & 0xff) - 128;
-            S[2] = int(key & 0xff) - 128;
+            j = key_neighbor(key);
+            key_shift(key, S);
             double v[3];
             const double r2 = pair_d2(pos, g, i, j, S, v);
             pass = r2 < rc2_max;
@@ -368,9 +431,9 @@ __global__ void __launch_bounds__(256) decode_wave(int n, const double *pos, con
     for (int k = lane; k < e - b; k += kWave) {
         const int r = b + k;
         const uint64_t key = row[k];
-        const int j = int((key >> 24) & 0x3fffffffffull);
-        const int S[3] = {int((key >> 16) & 0xff) - 128, int((key >> 8) & 0xff) - 128,
-                          int(key & 0xff) - 128};
+        const int j = key_neighbor(key);
+        int S[3];
+        key_shift(key, S);
         float v[3];
         for (int d = 0; d < 3; ++d) {
             const double o = (double(S[0]) * g.cell[0 * 3 + d] + double(S[1]) * g.cell[1 * 3 + d]) +
@@ -549,14 +612,14 @@ static void morton_bins(const int nb[3], int bin_offset, std::vector<int32_t> &o
     for (const auto &k : keys) out.push_back(k.second);
 }
 
-// Geometry of one structure: bins of width >= rc, stencil reach, capped bin count.
-Geo make_geo(const double *cell_in, const int32_t *pbc, double rc, int n_atoms, int bin_offset,
-             int atom_begin) {
+// Geometry of one structure: lattice, inverse, thickness and the initial bins
+// of width >= rc per direction.  The bin frame is completed by fit_bins.
+Geo make_geo(const double *cell_in, const int32_t *pbc, double rc, double *th) {
     Geo g{};
     std::memcpy(g.cell, cell_in, sizeof(g.cell));
     for (int d = 0; d < 3; ++d) g.pbc[d] = pbc[d] ? 1 : 0;
     // a degenerate row in a non-periodic direction gets an orthogonal stand-in:
-    // its shift is always 0, so it only shapes the (clamped) binning
+    // its shift is always 0, so it only sets the scale of the bins there
     for (int d = 0; d < 3; ++d) {
         if (norm3(g.cell + 3 * d) == 0.0) {
             RUNE_REQUIRE(!g.pbc[d], RUNE_ERR_ARGUMENT,
@@ -577,31 +640,76 @@ Geo make_geo(const double *cell_in, const int32_t *pbc, double rc, int n_atoms, 
     double vol = std::fabs(g.cell[0] * (g.cell[4] * g.cell[8] - g.cell[5] * g.cell[7]) -
                            g.cell[1] * (g.cell[3] * g.cell[8] - g.cell[5] * g.cell[6]) +
                            g.cell[2] * (g.cell[3] * g.cell[7] - g.cell[4] * g.cell[6]));
-    double th[3];
     for (int d = 0; d < 3; ++d) {
         double c[3];
         cross(g.cell + 3 * ((d + 1) % 3), g.cell + 3 * ((d + 2) % 3), c);
         th[d] = vol / norm3(c);
         double nb = std::floor(th[d] / (rc * (1.0 + 1e-9)));
         g.nb[d] = int(std::max(1.0, std::min(nb, 1024.0)));
+        g.bs[d] = double(g.nb[d]);
+        g.lo[d] = 0.0;
+        g.nbin[d] = g.nb[d];
     }
-    int64_t cap = std::max<int64_t>(64, 4 * int64_t(n_atoms));
-    while (int64_t(g.nb[0]) * g.nb[1] * g.nb[2] > cap) {
+    return g;
+}
+
+// Bin frame of one structure.  Periodic directions tile the cell with nb
+// bins; open directions cover exactly the bins that hold atoms, from the
+// extent [flo, fhi] of the atoms' fractional coordinates (an atom outside
+// the cell is never clamped into an edge bin, and a cell-less cluster is
+// binned over its own bounding box).  The bin count is capped at 4 per atom
+// by halving the finest direction, then the stencil reach follows from the
+// bin width th / bs >= rc.
+void fit_bins(Geo &g, const double *th, double rc, int n_atoms, const double *flo,
+              const double *fhi, int bin_offset, int atom_begin) {
+    const int64_t cap = std::max<int64_t>(64, 4 * int64_t(n_atoms));
+    for (;;) {
+        double total = 1.0;
+        for (int d = 0; d < 3; ++d) {
+            if (g.pbc[d]) {
+                g.bs[d] = double(g.nb[d]);
+                g.lo[d] = 0.0;
+                g.nbin[d] = g.nb[d];
+            } else if (n_atoms > 0) {
+                // the same products and floors as the binning kernel
+                g.lo[d] = std::floor(flo[d] * g.bs[d]);
+                const double span = std::floor(fhi[d] * g.bs[d]) - g.lo[d] + 1.0;
+                g.nbin[d] = int(std::min(span, double(int64_t(1) << 30)));
+            } else {
+                g.lo[d] = 0.0;
+                g.nbin[d] = 1;
+            }
+            total *= double(g.nbin[d]);
+        }
+        if (total <= double(cap)) break;
         int d = 0;
         for (int k = 1; k < 3; ++k)
-            if (g.nb[k] > g.nb[d]) d = k;
-        g.nb[d] = std::max(1, g.nb[d] / 2);
+            if (g.nbin[k] > g.nbin[d]) d = k;
+        if (g.pbc[d])
+            g.nb[d] = std::max(1, g.nb[d] / 2);
+        else
+            g.bs[d] *= 0.5;
     }
     for (int d = 0; d < 3; ++d) {
-        g.m[d] = int(std::floor(rc * g.nb[d] / th[d])) + 1;
-        if (!g.pbc[d]) g.m[d] = std::min(g.m[d], g.nb[d]);
+        g.m[d] = int(std::floor(rc * g.bs[d] / th[d])) + 1;
+        if (!g.pbc[d]) g.m[d] = std::min(g.m[d], g.nbin[d]);
         RUNE_REQUIRE(g.m[d] <= 60, RUNE_ERR_ARGUMENT,
                      "cell is too thin for the cutoff (more than 60 images per direction)");
     }
     g.bin_offset = bin_offset;
     g.atom_begin = atom_begin;
     g.atom_end = atom_begin + n_atoms;
-    return g;
+}
+
+const char *const kShiftMessage =
+    "an atom lies more than 511 cell periods from the cell (periodic image shift outside "
+    "[-512, 511]); wrap the positions into the cell";
+
+static double from_ordered_bits(uint64_t k) {
+    const uint64_t u = (k >> 63) ? (k & 0x7fffffffffffffffull) : ~k;
+    double x;
+    std::memcpy(&x, &u, sizeof(x));
+    return x;
 }
 
 struct Work {
@@ -713,12 +821,51 @@ static void build_lists(rune_nlist *nl, int64_t n_atoms, const double *d_positio
     const int n = int(n_atoms);
     const double rc = std::max(rc_radial, rc_angular), rc_bin = rc + skin;
     std::vector<Geo> geo(n_structures);
+    std::vector<double> th(3 * size_t(n_structures));
+    bool open = false;
+    for (int b = 0; b < n_structures; ++b) {
+        geo[b] = make_geo(h_cells + 9 * b, h_pbc + 3 * b, rc_bin, th.data() + 3 * b);
+        const bool has_atoms = h_struct_ptr[b + 1] > h_struct_ptr[b];
+        open = open || (has_atoms && !(geo[b].pbc[0] && geo[b].pbc[1] && geo[b].pbc[2]));
+    }
+    // extent of the atoms along open directions (one readback, only when a
+    // structure with atoms has a non-periodic direction)
+    const bool binned = skin == 0.0 || search;
+    std::vector<double> ext(6 * size_t(n_structures), 0.0);
+    if (open && binned && n > 0) {
+        nl->extent.reserve(sizeof(Geo) * n_structures + 48 * size_t(n_structures));
+        Geo *d_geo = nl->extent.as<Geo>();
+        auto *d_ext = reinterpret_cast<unsigned long long *>(
+            nl->extent.as<char>() + sizeof(Geo) * n_structures);
+        RUNE_HIP_CHECK(hipMemcpyAsync(d_geo, geo.data(), sizeof(Geo) * n_structures,
+                                      hipMemcpyHostToDevice, s));
+        RUNE_HIP_CHECK(hipMemsetAsync(d_ext, 0xff, 24 * size_t(n_structures), s));
+        RUNE_HIP_CHECK(hipMemsetAsync(d_ext + 3 * n_structures, 0x00, 24 * size_t(n_structures),
+                                      s));
+        hipLaunchKernelGGL(frac_extent, dim3(ceil_div(n, kThreads)), dim3(kThreads), 0, s, n,
+                           d_positions, nl->sptr.as<int32_t>(), n_structures, d_geo, d_ext);
+        RUNE_HIP_CHECK(hipGetLastError());
+        std::vector<uint64_t> bits(6 * size_t(n_structures));
+        RUNE_HIP_CHECK(hipMemcpyAsync(bits.data(), d_ext, 48 * size_t(n_structures),
+                                      hipMemcpyDeviceToHost, s));
+        RUNE_HIP_CHECK(hipStreamSynchronize(s));
+        for (int b = 0; b < n_structures; ++b)
+            for (int d = 0; d < 3; ++d) {
+                const bool has_atoms = h_struct_ptr[b + 1] > h_struct_ptr[b];
+                const double lo = from_ordered_bits(bits[3 * b + d]);
+                const double hi = from_ordered_bits(bits[3 * (n_structures + b) + d]);
+                RUNE_REQUIRE(geo[b].pbc[d] || !has_atoms || (std::isfinite(lo) && std::isfinite(hi)),
+                             RUNE_ERR_ARGUMENT, "atom positions must be finite");
+                ext[6 * b + d] = lo;
+                ext[6 * b + 3 + d] = hi;
+            }
+    }
     int total_bins = 0;
     for (int b = 0; b < n_structures; ++b) {
         int na = int(h_struct_ptr[b + 1] - h_struct_ptr[b]);
-        geo[b] = make_geo(h_cells + 9 * b, h_pbc + 3 * b, rc_bin, na, total_bins,
-                          int(h_struct_ptr[b]));
-        total_bins += geo[b].nb[0] * geo[b].nb[1] * geo[b].nb[2];
+        fit_bins(geo[b], th.data() + 3 * b, rc_bin, na, ext.data() + 6 * b,
+                 ext.data() + 6 * b + 3, total_bins, int(h_struct_ptr[b]));
+        total_bins += geo[b].nbin[0] * geo[b].nbin[1] * geo[b].nbin[2];
     }
     // working memory
     Arena ar;
@@ -767,7 +914,6 @@ static void build_lists(rune_nlist *nl, int64_t n_atoms, const double *d_positio
     const int cap = std::max(max_radial, max_angular);
     nl->keys.reserve(8 * size_t(std::max(n, 1)) * size_t(cap));
     const double rc2_r = rc_radial * rc_radial, rc2_a = rc_angular * rc_angular, rc2 = rc * rc;
-    const bool binned = skin == 0.0 || search;
     if (binned) {
         RUNE_HIP_CHECK(hipMemsetAsync(w.bin_count, 0, 4 * size_t(total_bins + 1), s));
         RUNE_HIP_CHECK(hipMemsetAsync(w.bin_cursor, 0, 4 * size_t(total_bins + 1), s));
@@ -806,6 +952,7 @@ static void build_lists(rune_nlist *nl, int64_t n_atoms, const double *d_positio
                 int32_t over = 0;
                 RUNE_HIP_CHECK(hipMemcpyAsync(&over, w.flag, 4, hipMemcpyDeviceToHost, s));
                 RUNE_HIP_CHECK(hipStreamSynchronize(s));
+                RUNE_REQUIRE(!(over & 2), RUNE_ERR_ARGUMENT, kShiftMessage);
                 if (!over) break;
                 RUNE_REQUIRE(attempt < 3, RUNE_ERR_STATE, "neighbour candidate search did not fit");
                 std::vector<int32_t> cc(n);
@@ -835,6 +982,7 @@ static void build_lists(rune_nlist *nl, int64_t n_atoms, const double *d_positio
                                   hipMemcpyDeviceToHost, s));
     RUNE_HIP_CHECK(hipMemcpyAsync(&host[1], w.flag, 4, hipMemcpyDeviceToHost, s));
     RUNE_HIP_CHECK(hipStreamSynchronize(s));
+    RUNE_REQUIRE(!(host[1] & 2), RUNE_ERR_ARGUMENT, kShiftMessage);
     if (host[1]) {
         std::vector<int32_t> cr(n), ca(n);
         RUNE_HIP_CHECK(hipMemcpy(cr.data(), w.cnt_r, 4 * size_t(n), hipMemcpyDeviceToHost));
@@ -866,7 +1014,8 @@ static void build_lists(rune_nlist *nl, int64_t n_atoms, const double *d_positio
             std::vector<int32_t> &perm = nl->h_perm;   // outlives the asynchronous upload
             perm.clear();
             perm.reserve(total_bins);
-            for (int b = 0; b < n_structures; ++b) morton_bins(geo[b].nb, geo[b].bin_offset, perm);
+            for (int b = 0; b < n_structures; ++b)
+                morton_bins(geo[b].nbin, geo[b].bin_offset, perm);
             int32_t *d_perm = reinterpret_cast<int32_t *>(base + o_perm);
             int32_t *rcnt = reinterpret_cast<int32_t *>(base + o_rcnt);
             int32_t *rst = reinterpret_cast<int32_t *>(base + o_rst);

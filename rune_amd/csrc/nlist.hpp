@@ -39,6 +39,7 @@ struct rune_nlist {
     std::vector<double> cand_key;
     // working memory of the builder
     rune::DeviceBuffer work;
+    rune::DeviceBuffer extent;   // bin frames and atom extents of open directions
     rune::DeviceBuffer keys;     // uint64 [N, max(max_radial, max_angular)] sorted per centre
     rune::DeviceBuffer pinned_dummy;
 };

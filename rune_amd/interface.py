@@ -1,17 +1,19 @@
 """ASE calculator and batch builder shared by the Möbius and NEP plugins.
 
-``Calculator(artifact, device="cuda", compute_stress=True, **kwargs)``
-mirrors ``rune/mobius/interface/calculator.py:14-98``: the same implemented
-properties, results (energy, free_energy, forces, Voigt stress = -W/V) and
-errors (``PropertyNotImplementedError`` when stress is disabled,
-``ValueError`` for non-positive volume, unsupported elements and neighbour
-overflow).  The neighbour search and the whole evaluation run on the GPU;
-the reference's default ``device="cpu"`` is not available here -- this
-evaluator has no CPU path and says so.
+``Calculator(artifact, device="cpu", compute_stress=True, **kwargs)``
+mirrors ``rune/mobius/interface/calculator.py:14-98``: the same signature and
+default, implemented properties, results (energy, free_energy, forces, Voigt
+stress = -W/V) and errors (``PropertyNotImplementedError`` when stress is
+disabled, ``ValueError`` for non-positive volume, unsupported elements and
+neighbour overflow).  ``device`` is where the model module lives, as in the
+reference; the neighbour search and the whole evaluation always run on a HIP
+device (the given one when it is a ``cuda`` device, else the current one),
+and there is no CPU evaluation path.
 
-``BatchBuilder.build`` returns the reference's padded batch dict
-(``rune/mobius/interface/batch.py:124-166``) built from the GPU lists.
-ASE is imported lazily; without ASE the array API in ``rune_amd.api`` works.
+``BatchBuilder(params, device, dtype).build`` returns the reference's padded
+batch dict (``rune/mobius/interface/batch.py:124-166``) on ``device``, built
+from the GPU lists.  ASE is imported lazily; without ASE the array API in
+``rune_amd.api`` works.
 """
 
 from __future__ import annotations
@@ -44,7 +46,8 @@ class BatchBuilder:
     """Convert one structure to a reference-format batch (padded lists)."""
 
     def __init__(self, params, device, dtype, kind="Möbius"):
-        self.device = N.require_device(device)
+        self.device = torch.device(device) if device is not None else torch.device("cpu")
+        self.compute_device = N.compute_device(self.device)
         self.dtype = dtype
         self.kind = kind
         self.elements = list(params["elements"])
@@ -57,6 +60,8 @@ class BatchBuilder:
         self.nlist = N.NeighborList()
 
     def types_and_counts(self, numbers):
+        """``_types_and_counts`` (batch.py:168-197) on the compute device; the
+        last atomic-number tuple is cached."""
         numbers = tuple(int(z) for z in numbers)
         if self._cached is not None and self._cached[0] == numbers:
             return self._cached[1], self._cached[2]
@@ -67,15 +72,15 @@ class BatchBuilder:
                 f"{[symbol_of(z) for z in missing]}. "
                 f"Model elements (type-id order): {self.elements}.")
         types = torch.tensor([self.z_to_type[z] for z in numbers], dtype=torch.long,
-                             device=self.device)
-        counts = torch.tensor([len(numbers)], dtype=torch.long, device=self.device)
+                             device=self.compute_device)
+        counts = torch.tensor([len(numbers)], dtype=torch.long, device=self.compute_device)
         self._cached = (numbers, types, counts)
         return types, counts
 
     def neighbors(self, positions, cell, pbc):
         if self.cutoff_radial <= 0.0 or self.cutoff_angular <= 0.0:
             raise ValueError(f"{self.kind} radial and angular cutoffs must be positive.")
-        pos = torch.as_tensor(np.asarray(positions, np.float64), device=self.device)
+        pos = torch.as_tensor(np.asarray(positions, np.float64), device=self.compute_device)
         return self.nlist.build(pos, [0, len(positions)], [np.asarray(cell, np.float64)],
                                 [np.broadcast_to(np.asarray(pbc, bool), (3,))],
                                 self.cutoff_radial, self.cutoff_angular,
@@ -86,24 +91,30 @@ class BatchBuilder:
         n = len(atoms)
         nl = self.neighbors(atoms.positions, atoms.cell[:], atoms.pbc)
         rec = nl.export()
-        ptr = rec["ptr"].long().cpu()
-        view = rec["view"].long().cpu()
-        nbr = rec["nbr"].long().cpu()
-        shift = rec["shift"].double().cpu()
-        cell = torch.as_tensor(np.asarray(atoms.cell[:], np.float64))
+        dev = self.compute_device
+        view = rec["view"].long()
+        nbr = rec["nbr"].long()
+        shift = rec["shift"].double()
+        cell = torch.as_tensor(np.asarray(atoms.cell[:], np.float64), device=dev)
+        # offsets S @ cell in fp64, the order of batch.py:76
         offsets = (shift[:, 0:1] * cell[0] + shift[:, 1:2] * cell[1]) + shift[:, 2:3] * cell[2]
-        out = {"types": types, "n_atoms_per_structure": counts,
+        out = {"types": types.to(self.device), "n_atoms_per_structure": counts.to(self.device),
                "positions": torch.as_tensor(np.asarray(atoms.positions), dtype=self.dtype,
                                             device=self.device),
                "compute_forces": bool(compute_forces), "compute_virial": bool(compute_virial)}
         for kind, cols, cap in (("radial", (0, 1), self.max_neighbors_radial),
                                 ("angular", (2, 3), self.max_neighbors_angular)):
-            nb = torch.full((n, cap), -1, dtype=torch.long)
-            of = torch.zeros((n, cap, 3), dtype=torch.float64)
-            for i in range(n):
-                b, e = int(view[i, cols[0]]), int(view[i, cols[1]])
-                nb[i, :e - b] = nbr[b:e]
-                of[i, :e - b] = offsets[b:e]
+            # each centre's records of this list fill the first slots of its
+            # padded row, in record order (batch.py:9-39)
+            begin, end = view[:, cols[0]], view[:, cols[1]]
+            count = end - begin
+            slot = torch.arange(cap, device=dev)
+            live = slot[None, :] < count[:, None]
+            src = (begin[:, None] + slot[None, :])[live]
+            nb = torch.full((n, cap), -1, dtype=torch.long, device=dev)
+            of = torch.zeros((n, cap, 3), dtype=torch.float64, device=dev)
+            nb[live] = nbr[src]
+            of[live] = offsets[src]
             out[f"{kind}_neighbors"] = nb.to(self.device)
             out[f"{kind}_offsets"] = of.to(device=self.device, dtype=self.dtype)
         return out
@@ -115,9 +126,9 @@ def make_calculator_class(load_model, family_name):
     class Calculator(ASECalculator):
         implemented_properties = ["energy", "free_energy", "forces", "stress"]
 
-        def __init__(self, artifact, device="cuda", compute_stress=True, **kwargs):
+        def __init__(self, artifact, device="cpu", compute_stress=True, **kwargs):
             super().__init__(**kwargs)
-            self.device = N.require_device(device if device is not None else "cuda")
+            self.device = torch.device(device) if device is not None else torch.device("cpu")
             self.model = load_model(artifact, device=self.device)
             self.model.eval()
             self.model.requires_grad_(False)
@@ -150,6 +161,8 @@ def make_calculator_class(load_model, family_name):
             types, _ = self.batch_builder.types_and_counts(atoms.numbers)
             nl = self.batch_builder.neighbors(atoms.positions, atoms.cell[:], atoms.pbc)
             out = self.model.native().compute(nl, types, 1, want_f, want_w)
+            # fp32 kernel results, handed back in the model's dtype like the reference
+            out = {k: v.to(self.batch_builder.dtype) for k, v in out.items()}
             energy = float(out["energy"][0].cpu())
             self.results = {"energy": energy, "free_energy": energy}
             if want_f:

@@ -1,7 +1,5 @@
 """``BatchBuilder`` of ``rune/mobius/interface/batch.py:103-197`` (GPU neighbour lists)."""
 
-from functools import partial
-
 from ...interface import BatchBuilder as _Builder
 
 
