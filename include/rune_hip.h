@@ -213,6 +213,26 @@ int rune_model_compute(rune_model *model, const rune_nlist *nl, const int32_t *d
                        float *d_energies, float *d_energy, float *d_forces,
                        float *d_virial, float *d_atom_virial, void *stream);
 
+/* Allocation-free evaluation.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * outputs and errors as rune_model_compute, but the workspace is a static
+ * device array of rune_model_static_scratch_bytes() bytes (64 MiB) that every
+ * GPU the library runs on holds until the process ends; the call allocates no
+ * device memory.  An evaluation whose workspace exceeds the array fails with
+ * RUNE_ERR_ARGUMENT before any launch (roughly: a few thousand atoms for
+ * descriptor-only and NEP models, about 80 atoms of an OAM-EQ model).  All
+ * calls on one GPU share the array and keep its last contents: calls that
+ * overlap on one GPU (several streams or threads) race.  No phase timing is
+ * recorded. */
+int rune_model_compute_static(rune_model *model, const rune_nlist *nl, const int32_t *d_types,
+                              int32_t compute_forces, int32_t compute_virial,
+                              float *d_energies, float *d_energy, float *d_forces,
+                              float *d_virial, float *d_atom_virial, void *stream);
+
+/* Size in bytes of the static workspace of rune_model_compute_static. */
+int64_t rune_model_static_scratch_bytes(void);
+
 /* GPUMD-style per-atom outputs, accumulated (+=) in fp64 as GPUMD's
  * potentials do (rune/mobius/src/force.cu:47-84): d_potential [N];
  * d_force [3N] as three atom arrays x[0..N), y, z; d_virial [9N] as nine atom

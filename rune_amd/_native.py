@@ -88,6 +88,8 @@ def library():
         "rune_model_set_tensor": (C.c_int, [vp, C.c_char_p, vp, i64]),
         "rune_model_finalize": (C.c_int, [vp]),
         "rune_model_compute": (C.c_int, [vp, vp, vp, i32, i32, vp, vp, vp, vp, vp, vp]),
+        "rune_model_compute_static": (C.c_int, [vp, vp, vp, i32, i32, vp, vp, vp, vp, vp, vp]),
+        "rune_model_static_scratch_bytes": (i64, []),
         "rune_model_workspace_bytes": (i64, [vp]),
         "rune_model_timing": (C.c_int, [vp, i32]),
         "rune_model_timing_read": (C.c_int, [vp, C.POINTER(C.c_double), C.POINTER(i64)]),
@@ -335,7 +337,10 @@ class NativeModel:
             self._h = None
 
     def compute(self, nlist, types, n_structures, compute_forces=True, compute_virial=True,
-                atom_virial=False):
+                atom_virial=False, static=False):
+        """E + F + virial through ``rune_model_compute``, or with ``static``
+        through ``rune_model_compute_static`` (workspace in the library's
+        static device scratch; no device allocation by the library)."""
         dev = nlist.device
         n = nlist.n_atoms
         types = types.to(device=dev, dtype=torch.int32).contiguous()
@@ -349,7 +354,8 @@ class NativeModel:
             out["virial"] = torch.empty((n_structures, 9), dtype=torch.float32, device=dev)
         if atom_virial:
             out["atom_virial"] = torch.empty((n, 9), dtype=torch.float32, device=dev)
-        check(library().rune_model_compute(
+        entry = library().rune_model_compute_static if static else library().rune_model_compute
+        check(entry(
             self._h, nlist.handle, _ptr(types), int(compute_forces), int(compute_virial),
             _ptr(out["energies"]), _ptr(out["energy"]), _ptr(out.get("forces")),
             _ptr(out.get("virial")), _ptr(out.get("atom_virial")), _stream(dev)))

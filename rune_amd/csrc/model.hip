@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <sstream>
 
 #include "model.hpp"
@@ -359,9 +360,13 @@ static Records records_of(const rune_nlist *nl) {
     return r;
 }
 
+// One evaluation.  The workspace is the handle's growing device buffer, or,
+// when `fixed` is given, that caller-owned range of `fixed_bytes` bytes (too
+// small a range is an argument error, raised before any launch).
 static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, int want_f,
                     int want_w, float *d_energies, float *d_energy, float *d_forces,
-                    float *d_virial, float *d_atom_virial, hipStream_t s) {
+                    float *d_virial, float *d_atom_virial, hipStream_t s,
+                    char *fixed = nullptr, size_t fixed_bytes = 0) {
     RUNE_REQUIRE(m.finalized, RUNE_ERR_STATE, "model handle is not finalized");
     RUNE_REQUIRE(nl, RUNE_ERR_ARGUMENT, "null neighbour list");
     if (!nl->from_padded) {
@@ -387,8 +392,20 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     size_t o_f = ar.add(4 * size_t(N) * 3);
     LocalPlan lp = plan_local(m, ar, N);
     MessagePlan mp = plan_messages(m, ar, N, E);
-    m.work.reserve(ar.total);
-    char *base = m.work.as<char>();
+    const size_t o_sums = ar.add(sizeof(double) * std::max<size_t>(1, structure_sum_scratch(r, 9)));
+    char *base = fixed;
+    if (fixed) {
+        if (ar.total > fixed_bytes) {
+            std::ostringstream os;
+            os << "this evaluation needs " << ar.total << " bytes of workspace; the static "
+               << "scratch holds " << fixed_bytes << " (use rune_model_compute)";
+            throw Error(RUNE_ERR_ARGUMENT, os.str());
+        }
+    } else {
+        m.work.reserve(ar.total);
+        base = m.work.as<char>();
+    }
+    double *sums = reinterpret_cast<double *>(base + o_sums);
     int32_t *flag = reinterpret_cast<int32_t *>(base + o_flag);
     float *q = reinterpret_cast<float *>(base + o_q);
     float *dq = reinterpret_cast<float *>(base + o_dq);
@@ -416,7 +433,7 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
         return;
     }
     hipEvent_t *ev = nullptr;
-    if (m.timing) {
+    if (m.timing && !fixed) {
         if (m.events.empty()) {
             m.events.resize(size_t(kTimingRing) * (RUNE_N_PHASES + 1));
             for (auto &e : m.events) RUNE_HIP_CHECK(hipEventCreate(&e));
@@ -464,8 +481,6 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     descriptor_reverse(d, m.zbl, r, types, dq, ldq, mom, dmom, g_direct, energies, g,
                        grad ? 1 : 0, s);
     mark(7);
-    m.sums.reserve(sizeof(double) * std::max<size_t>(1, structure_sum_scratch(r, 9)));
-    double *sums = m.sums.as<double>();
     if (d_energy) structure_sum(r, energies, 1, d_energy, sums, s);
     if (grad) {
         forces_and_virial(r, g, forces, atom_virial, s);
@@ -689,6 +704,63 @@ extern "C" int rune_model_compute(rune_model *model, const rune_nlist *nl, const
                 d_forces, d_virial, d_atom_virial, as_stream(stream));
     });
 }
+
+// ---------------------------------------------------------------------------
+// rune_model_compute_static: the evaluation with its workspace in a static
+// device array instead of the handle's allocation.
+// ---------------------------------------------------------------------------
+
+// 64 MiB per GPU the library runs on, held until the process ends.  Host code
+// must not use the array's name as a device address: each device's copy is
+// found once with hipGetSymbolAddress and kept in g_scratch_addr.
+constexpr size_t kStaticScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) char scratch[kStaticScratchBytes];
+
+namespace rune {
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+char *g_scratch_addr[kMaxDevices] = {};
+
+// Device address of the current device's scratch copy (resolved on the first
+// call on that device, with that device current).
+char *static_scratch() {
+    int dev = 0;
+    RUNE_HIP_CHECK(hipGetDevice(&dev));
+    RUNE_REQUIRE(dev >= 0 && dev < kMaxDevices, RUNE_ERR_STATE, "device ordinal out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_addr[dev]) {
+        void *addr = nullptr;
+        RUNE_HIP_CHECK(hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)));
+        RUNE_REQUIRE(addr != nullptr, RUNE_ERR_HIP, "static scratch has no device address");
+        g_scratch_addr[dev] = static_cast<char *>(addr);
+    }
+    return g_scratch_addr[dev];
+}
+}  // namespace
+}  // namespace rune
+
+extern "C" int rune_model_compute_static(rune_model *model, const rune_nlist *nl,
+                                         const int32_t *d_types, int32_t compute_forces,
+                                         int32_t compute_virial, float *d_energies,
+                                         float *d_energy, float *d_forces, float *d_virial,
+                                         float *d_atom_virial, void *stream) {
+    return guarded([&] {
+        RUNE_REQUIRE(model, RUNE_ERR_ARGUMENT, "null model");
+        char *ws = static_scratch();
+        // no timing events here (creating them is a runtime allocation)
+        struct Untimed {
+            ModelImpl &m;
+            bool was;
+            explicit Untimed(ModelImpl &x) : m(x), was(x.timing) { m.timing = false; }
+            ~Untimed() { m.timing = was; }
+        } untimed(*model);
+        compute(*model, nl, d_types, compute_forces, compute_virial, d_energies, d_energy,
+                d_forces, d_virial, d_atom_virial, as_stream(stream), ws, kStaticScratchBytes);
+    });
+}
+
+extern "C" int64_t rune_model_static_scratch_bytes(void) { return int64_t(kStaticScratchBytes); }
 
 namespace rune {
 namespace {
