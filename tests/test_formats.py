@@ -40,7 +40,7 @@ def test_mobius_txt_preserves_weights_bitwise(name, tmp_path):
 def test_exported_basis_table_evaluates_to_angular_basis():
     """rune tests/test_mobius_export.py:76-96: sparse polynomials == _compute_basis."""
     model = small_export_model("eq")
-    rows, offsets = EX.basis_terms(model.descriptor.angular)
+    rows, offsets = EX.angular_polynomials(model.descriptor.angular)
     rng = np.random.default_rng(0)
     u = rng.normal(size=(50, 3))
     u /= np.linalg.norm(u, axis=1, keepdims=True)
@@ -59,7 +59,7 @@ def test_exported_invariant_table_evaluates_to_invariants():
     """rune tests/test_mobius_export.py:98-122: sparse invariants == _compute_q."""
     model = small_export_model("eq")
     ang = model.descriptor.angular
-    rows, offsets = EX.invariant_terms(ang)
+    rows, offsets = EX.invariant_polynomials(ang)
     s = torch.randn(7, 2, 24, dtype=torch.float64, generator=torch.Generator().manual_seed(1))
     flags = OM.Flags(4, 1, 1, 1, 1, 1, 1)
     w = {f"descriptor.angular.{k}": getattr(ang, k) for k in ("C3B", "C4B", "C5B", "C4B2")}
