@@ -504,11 +504,308 @@ __global__ void __launch_bounds__(kWave) k_descriptor_reverse(
     }
 }
 
+// ---- any channel count and basis size ----
+// The kernels above keep a lane's basis values (<= kMaxKr / kMaxKa) and
+// channel values (<= kMaxNr / kMaxNa) in registers.  These variants give
+// each lane LDS rows for them instead, so every model the reference accepts
+// (any n_max, basis_size) evaluates; same wave-per-centre structure, same
+// fixed summation order per output.
+
+// f_k(r) (and f'_k(r) when fp) for k < k_max into one lane's LDS row.
+__device__ inline void chebyshev_row(float r, float rc, int k_max, float *f, float *fp) {
+    const float rcinv = 1.0f / rc;
+    const float arg = kPi * r * rcinv;
+    const float fc = 0.5f * cosf(arg) + 0.5f;
+    const float fcp = -0.5f * kPi * rcinv * sinf(arg);
+    const float rs = r * rcinv - 1.0f;
+    const float x = 2.0f * rs * rs - 1.0f;
+    const float dxdr = 4.0f * rs * rcinv;
+    f[0] = fc;
+    if (fp) fp[0] = fcp;
+    float t2 = 1.0f, t1 = x, u2 = 1.0f, u1 = 2.0f * x;
+    for (int k = 1; k < k_max; ++k) {
+        if (k == 1) {
+            const float core = 0.5f * (x + 1.0f);
+            f[1] = core * fc;
+            if (fp) fp[1] = 0.5f * dxdr * fc + core * fcp;
+        } else {
+            const float tn = 2.0f * x * t1 - t2, un = 2.0f * x * u1 - u2;
+            const float core = 0.5f * (tn + 1.0f);
+            f[k] = core * fc;
+            if (fp) fp[k] = 0.5f * float(k) * u1 * dxdr * fc + core * fcp;
+            t2 = t1;
+            t1 = tn;
+            u2 = u1;
+            u1 = un;
+        }
+    }
+}
+
+// Output chunk of the moment accumulators of the wide forward kernel.
+constexpr int kWideOut = 16;
+
+__global__ void __launch_bounds__(kWave) k_descriptor_forward_wide(DescTables t, Records r,
+                                                                   const int32_t *types, float *q,
+                                                                   int ldq, float *moments) {
+    extern __shared__ float lds[];
+    const int nlm = t.nlm, na = t.na, nout = na * nlm, kmax = max(t.kr, t.ka);
+    float *fL = lds;                                // [64][kmax + 1] basis rows
+    float *gnL = fL + kWave * (kmax + 1);           // [64][na + 1]
+    float *bL = gnL + kWave * (na + 1);             // [64][nlm + 1]
+    float *sL = bL + kWave * (nlm + 1);             // [na * nlm]
+    const int i = blockIdx.x, lane = threadIdx.x;
+    const int ti = types[i];
+    const int rb = r.view[4 * i], re = r.view[4 * i + 1];
+    const int ab = r.view[4 * i + 2], ae = r.view[4 * i + 3];
+    float *f = fL + lane * (kmax + 1);
+    // radial channels, 16 at a time (the basis rows are rebuilt per group)
+    for (int n0 = 0; n0 < t.nr; n0 += 16) {
+        float qr[16];
+#pragma unroll
+        for (int n = 0; n < 16; ++n) qr[n] = 0.0f;
+        for (int e = rb + lane; e < re; e += kWave) {
+            const float4 v = r.vec[e];
+            const int tj = types[r.nbr[e]];
+            chebyshev_row(v.w, t.rc_r, t.kr, f, nullptr);
+            const float *row = t.c_radial + size_t(ti * t.n_types + tj) * t.nr * t.kr4;
+#pragma unroll
+            for (int n = 0; n < 16; ++n) {
+                if (n0 + n >= t.nr) break;
+                const float *cr = row + (n0 + n) * t.kr4;
+                float a = 0.0f;
+                for (int k = 0; k < t.kr; ++k) a += cr[k] * f[k];
+                qr[n] += a;
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < 16; ++n) {
+            if (n0 + n >= t.nr) break;
+            const float v = wave_sum(qr[n]);
+            if (lane == 0) q[size_t(i) * ldq + n0 + n] = v;
+        }
+    }
+    // angular moments s[n][lm] = sum_e gn[e][n] b[e][lm], outputs in chunks
+    for (int o0 = 0; o0 < nout; o0 += kWideOut * kWave) {
+        float acc[kWideOut];
+#pragma unroll
+        for (int j = 0; j < kWideOut; ++j) acc[j] = 0.0f;
+        for (int base = ab; base < ae; base += kWave) {
+            const int e = base + lane;
+            float *gl = gnL + lane * (na + 1);
+            float *bl = bL + lane * (nlm + 1);
+            if (e < ae) {
+                const float4 v = r.vec[e];
+                const int tj = types[r.nbr[e]];
+                chebyshev_row(v.w, t.rc_a, t.ka, f, nullptr);
+                const float *row = t.c_angular + size_t(ti * t.n_types + tj) * t.na * t.ka4;
+                for (int n = 0; n < na; ++n) {
+                    const float *cr = row + n * t.ka4;
+                    float a = 0.0f;
+                    for (int k = 0; k < t.ka; ++k) a += cr[k] * f[k];
+                    gl[n] = a;
+                }
+                const float inv = 1.0f / fmaxf(v.w, 1.0e-12f);
+                const float ux = v.x * inv, uy = v.y * inv, uz = v.z * inv;
+                int idx = 0;
+                for (int L = 1; L <= t.l_max; ++L) {
+                    float wr = 1.0f, wi = 0.0f;
+                    for (int n1 = 0; n1 <= L; ++n1) {
+                        float zf, zfp;
+                        zpoly(t, L, n1, uz, zf, zfp);
+                        if (n1 == 0) {
+                            bl[idx++] = zf;
+                        } else {
+                            next_w(ux, uy, wr, wi);
+                            bl[idx++] = zf * wr;
+                            bl[idx++] = zf * wi;
+                        }
+                    }
+                }
+            } else {
+                for (int n = 0; n < na; ++n) gl[n] = 0.0f;
+                for (int c = 0; c < nlm; ++c) bl[c] = 0.0f;
+            }
+            __syncthreads();
+            const int cnt = min(kWave, ae - base);
+#pragma unroll
+            for (int j = 0; j < kWideOut; ++j) {
+                const int o = o0 + lane + kWave * j;
+                if (o >= nout) break;
+                const int n = o / nlm, c = o - n * nlm;
+                float a = 0.0f;
+                for (int k = 0; k < cnt; ++k) a += gnL[k * (na + 1) + n] * bL[k * (nlm + 1) + c];
+                acc[j] += a;
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int j = 0; j < kWideOut; ++j) {
+            const int o = o0 + lane + kWave * j;
+            if (o >= nout) break;
+            sL[o] = acc[j];
+            moments[size_t(i) * nout + o] = acc[j];
+        }
+    }
+    __syncthreads();
+    for (int n = lane; n < na; n += kWave)
+        invariants_of(t, sL + n * nlm, q + size_t(i) * ldq + t.nr + n, na);
+}
+
+__global__ void __launch_bounds__(kWave) k_descriptor_reverse_wide(
+    DescTables t, ZblTables z, Records r, const int32_t *types, const float *dq, int ldq,
+    const float *moments, const float *dmom, const float4 *g_direct, float *energies,
+    float4 *g, int want_grad) {
+    extern __shared__ float lds[];
+    const int nlm = t.nlm, na = t.na, nout = na * nlm, kmax = max(t.kr, t.ka);
+    float *dqL = lds;                                   // [Q]
+    float *sL = dqL + t.Q;                              // [na * nlm]
+    float *WL = sL + nout;                              // [na * nlm]
+    float *fL = WL + nout;                              // [64][kmax + 1]
+    float *fpL = fL + kWave * (kmax + 1);               // [64][kmax + 1]
+    float *gnL = fpL + kWave * (kmax + 1);              // [64][na + 1]
+    float *gnpL = gnL + kWave * (na + 1);               // [64][na + 1]
+    const int i = blockIdx.x, lane = threadIdx.x;
+    const int ti = types[i];
+    const int rb = r.view[4 * i], re = r.view[4 * i + 1];
+    const int ab = r.view[4 * i + 2], ae = r.view[4 * i + 3];
+    const int eb = r.ptr[i], ee = r.ptr[i + 1];
+    if (want_grad) {
+        for (int k = lane; k < t.Q; k += kWave) dqL[k] = dq[size_t(i) * ldq + k];
+        for (int o = lane; o < nout; o += kWave) {
+            sL[o] = moments[size_t(i) * nout + o];
+            WL[o] = dmom ? dmom[size_t(i) * nout + o] : 0.0f;
+        }
+        __syncthreads();
+        for (int n = lane; n < na; n += kWave)
+            invariant_gradient(t, sL + n * nlm, dqL + t.nr + n, na, WL + n * nlm);
+        __syncthreads();
+    }
+    float *f = fL + lane * (kmax + 1), *fp = fpL + lane * (kmax + 1);
+    float *gn = gnL + lane * (na + 1), *gnp = gnpL + lane * (na + 1);
+    float zsum = 0.0f;
+    for (int e = eb + lane; e < ee; e += kWave) {
+        const float4 v = r.vec[e];
+        const float d = v.w;
+        const float inv = 1.0f / fmaxf(d, 1.0e-12f);
+        const float ux = v.x * inv, uy = v.y * inv, uz = v.z * inv;
+        const int tj = types[r.nbr[e]];
+        float gx = 0.0f, gy = 0.0f, gz = 0.0f;
+        const bool in_r = e >= rb && e < re;
+        const bool in_a = e >= ab && e < ae;
+        if (want_grad && in_r) {
+            chebyshev_row(d, t.rc_r, t.kr, f, fp);
+            const float *row = t.c_radial + size_t(ti * t.n_types + tj) * t.nr * t.kr4;
+            float gs = 0.0f;
+            for (int n = 0; n < t.nr; ++n) {
+                const float *cr = row + n * t.kr4;
+                float a = 0.0f;
+                for (int k = 0; k < t.kr; ++k) a += cr[k] * fp[k];
+                gs += dqL[n] * a;
+            }
+            gx += gs * ux;
+            gy += gs * uy;
+            gz += gs * uz;
+        }
+        if (want_grad && in_a) {
+            chebyshev_row(d, t.rc_a, t.ka, f, fp);
+            const float *row = t.c_angular + size_t(ti * t.n_types + tj) * t.na * t.ka4;
+            for (int n = 0; n < na; ++n) {
+                const float *cr = row + n * t.ka4;
+                float a = 0.0f, b = 0.0f;
+                for (int k = 0; k < t.ka; ++k) {
+                    a += cr[k] * f[k];
+                    b += cr[k] * fp[k];
+                }
+                gn[n] = a;
+                gnp[n] = b;
+            }
+            float rs = 0.0f, dx = 0.0f, dy = 0.0f, dz = 0.0f, proj = 0.0f;
+            int c = 0;
+            auto channel = [&](float b, float bx, float by, float bz) {
+                float wsum = 0.0f, wsump = 0.0f;
+                for (int n = 0; n < na; ++n) {
+                    const float w = WL[n * nlm + c];
+                    wsum += w * gn[n];
+                    wsump += w * gnp[n];
+                }
+                rs += wsump * b;
+                dx += wsum * bx;
+                dy += wsum * by;
+                dz += wsum * bz;
+                proj += wsum * (ux * bx + uy * by + uz * bz);
+                ++c;
+            };
+            for (int L = 1; L <= t.l_max; ++L) {
+                float wr = 1.0f, wi = 0.0f;
+                for (int n1 = 0; n1 <= L; ++n1) {
+                    float zf, zfp;
+                    zpoly(t, L, n1, uz, zf, zfp);
+                    if (n1 == 0) {
+                        channel(zf, 0.0f, 0.0f, zfp);
+                    } else {
+                        const float pr = wr, pi = wi;
+                        next_w(ux, uy, wr, wi);
+                        const float zn = zf * float(n1);
+                        channel(zf * wr, zn * pr, -zn * pi, zfp * wr);
+                        channel(zf * wi, zn * pi, zn * pr, zfp * wi);
+                    }
+                }
+            }
+            gx += rs * ux + (dx - proj * ux) * inv;
+            gy += rs * uy + (dy - proj * uy) * inv;
+            gz += rs * uz + (dz - proj * uz) * inv;
+        }
+        const bool in_z = z.mode != RUNE_ZBL_NONE && (z.on_angular ? in_a : in_r);
+        if (in_z) {
+            float ez, dez;
+            zbl_pair(z, ti, tj, fmaxf(d, 1.0e-12f), ez, dez);
+            zsum += ez;
+            gx += dez * ux;
+            gy += dez * uy;
+            gz += dez * uz;
+        }
+        if (want_grad) {
+            if (g_direct) {
+                const float4 gd = g_direct[e];
+                gx += gd.x;
+                gy += gd.y;
+                gz += gd.z;
+            }
+            g[e] = make_float4(gx, gy, gz, 0.0f);
+        }
+    }
+    if (z.mode != RUNE_ZBL_NONE) {
+        const float sz = wave_sum(zsum);
+        if (lane == 0) energies[i] += sz;
+    }
+}
+
+// The register kernels cover these sizes; larger ones take the wide kernels.
+bool descriptor_fits_registers(const DescTables &t) {
+    return t.nr <= kMaxNr && t.na <= kMaxNa && t.kr <= kMaxKr && t.ka <= kMaxKa;
+}
+
 }  // namespace
+
+static void allow_lds(const void *kernel, size_t lds) {
+    if (lds > 65536)
+        RUNE_HIP_CHECK(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           int(lds)));
+}
 
 void descriptor_forward(const DescTables &t, const Records &r, const int32_t *types, float *q,
                         int ldq, float *moments, hipStream_t s) {
     if (r.n_atoms == 0) return;
+    if (!descriptor_fits_registers(t)) {
+        const int kmax = std::max(t.kr, t.ka);
+        const size_t lds = sizeof(float) * (kWave * (kmax + 1) + kWave * (t.na + 1) +
+                                             kWave * (t.nlm + 1) + t.na * t.nlm);
+        allow_lds(reinterpret_cast<const void *>(&k_descriptor_forward_wide), lds);
+        hipLaunchKernelGGL(k_descriptor_forward_wide, dim3(r.n_atoms), dim3(kWave), lds, s, t, r,
+                           types, q, ldq, moments);
+        RUNE_HIP_CHECK(hipGetLastError());
+        return;
+    }
     size_t lds = sizeof(float) * (kWave * (t.na + 1) + kWave * (t.nlm + 1) + t.na * t.nlm);
     hipLaunchKernelGGL(k_descriptor_forward, dim3(r.n_atoms), dim3(kWave), lds, s, t, r, types,
                        q, ldq, moments);
@@ -521,6 +818,16 @@ void descriptor_reverse(const DescTables &t, const ZblTables &z, const Records &
                         int want_grad, hipStream_t s) {
     if (r.n_atoms == 0) return;
     if (!want_grad && z.mode == RUNE_ZBL_NONE) return;
+    if (!descriptor_fits_registers(t)) {
+        const int kmax = std::max(t.kr, t.ka);
+        const size_t lds = sizeof(float) * (t.Q + 2 * t.na * t.nlm + 2 * kWave * (kmax + 1) +
+                                             2 * kWave * (t.na + 1));
+        allow_lds(reinterpret_cast<const void *>(&k_descriptor_reverse_wide), lds);
+        hipLaunchKernelGGL(k_descriptor_reverse_wide, dim3(r.n_atoms), dim3(kWave), lds, s, t, z,
+                           r, types, dq, ldq, moments, dmom, g_direct, energies, g, want_grad);
+        RUNE_HIP_CHECK(hipGetLastError());
+        return;
+    }
     size_t lds = sizeof(float) * (t.Q + 2 * t.na * t.nlm);
     hipLaunchKernelGGL(k_descriptor_reverse, dim3(r.n_atoms), dim3(kWave), lds, s, t, z, r,
                        types, dq, ldq, moments, dmom, g_direct, energies, g, want_grad);

@@ -273,7 +273,7 @@ __device__ inline void fold_slots(float (&v)[N]) {
 // plus add[n, c, k] and add_t[n, k, c] when given.  One atom per wave (four
 // per block, blocks loop over atom groups), on the matrix cores: for each
 // order, out_L [C, 2L+1] = W_L [C, C] x in_L [C, 2L+1] as 16 x 16 tiles
-// (channels padded to 16 MT, components to 16).  The W_L fragments stay in
+// (channels padded to 16 MT, components to 16 per tile).  The W_L fragments stay in
 // registers for the whole launch when they fit (MT <= 2), else the block
 // stages them in LDS; the atom's input row is staged in the wave's LDS.
 // MFMA operand layout as in k_eq_edge_adj: lane l supplies A[l%16][l/16] and
@@ -359,32 +359,37 @@ __global__ void __launch_bounds__(256) k_eq_mix(int N, const float *mixw, const 
 #pragma unroll
         for (int L = 1; L <= LQ; ++L) {
             const int st = L * L - 1, w = 2 * L + 1;
-            floatx4 acc[MT];
+            // components of the order in tiles of 16 (two tiles at L = 8)
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int ct = 0; ct < (w + 15) / 16; ++ct) {
+                const int kc = 16 * ct + r;
+                floatx4 acc[MT];
 #pragma unroll
-            for (int s4 = 0; s4 < KS; ++s4) {
-                const int cc = 4 * s4 + g;
-                const float b = (cc < C && r < w) ? row[cc * NQ + st + min(r, w - 1)] : 0.0f;
+                for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    float av;
-                    if constexpr (kRegW)
-                        av = Wr[L - 1][mt][s4];
-                    else
-                        av = Wl[(size_t(L - 1) * CP + 16 * mt + r) * CP + 4 * s4 + g];
-                    acc[mt] = mfma4(av, b, acc[mt]);
-                }
-            }
-            if (r < w) {
-                const int k = st + r;
+                for (int s4 = 0; s4 < KS; ++s4) {
+                    const int cc = 4 * s4 + g;
+                    const float b = (cc < C && kc < w) ? row[cc * NQ + st + min(kc, w - 1)] : 0.0f;
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const int c = 16 * mt + 4 * g + v;
-                        if (c < C) res[c * NQ + k] = acc[mt][v] + res[c * NQ + k];
+                    for (int mt = 0; mt < MT; ++mt) {
+                        float av;
+                        if constexpr (kRegW)
+                            av = Wr[L - 1][mt][s4];
+                        else
+                            av = Wl[(size_t(L - 1) * CP + 16 * mt + r) * CP + 4 * s4 + g];
+                        acc[mt] = mfma4(av, b, acc[mt]);
                     }
+                }
+                if (kc < w) {
+                    const int k = st + kc;
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            const int c = 16 * mt + 4 * g + v;
+                            if (c < C) res[c * NQ + k] = acc[mt][v] + res[c * NQ + k];
+                        }
+                }
             }
         }
         wave_sync();
@@ -827,6 +832,10 @@ __device__ inline float cutoff_slope(float d, float rc) {
     return -0.5f * kPi / rc * sinf(kPi * d / rc);
 }
 
+// Records whose harmonic rows k_eq_pair_dir stages per round: 64, or 32 for
+// orders whose rows would not fit four waves' LDS (nq > 64, order 8).
+__device__ __host__ constexpr int pair_dir_chunk(int nq) { return nq > 64 ? 32 : 64; }
+
 // Reverse pass of the angular messages, walked from the neighbour side: the
 // wave of atom j holds its mixed state M_j, gathers the centre's
 // dE/d(dir_out) once per record and produces the direction-gate adjoints
@@ -841,20 +850,21 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
     constexpr int W = Ln::W;
     constexpr int WT = W + 4;              // T row: channels of one (slot, k), padded
     constexpr int KQ = (NQ + W - 1) / W;   // dE/dY components per lane
+    constexpr int RC = pair_dir_chunk(NQ);   // records staged per round
     extern __shared__ float lds[];
     const int j = wave_atom(a.r);
     if (j < 0) return;
     const Ln ln(a.C);
-    float *Yc = lds + (threadIdx.x >> 6) * (kWave * LY + S * NQ * WT);
-    float *T = Yc + kWave * LY;
+    float *Yc = lds + (threadIdx.x >> 6) * (RC * LY + S * NQ * WT);
+    float *T = Yc + RC * LY;
     const int G = a.G, C = a.C, CN = C * NQ, LC = LQ * C, NG = a.NG;
     float MX[NQ], acc[NQ];
     zero(MX);
     zero(acc);
     if (ln.act) load_row(MX, a.mixst + size_t(j) * CN + ln.c * NQ);
     const int tb = a.r.tptr[j], te = a.r.tptr[j + 1];
-    for (int t0 = tb; t0 < te; t0 += kWave) {
-        const int cnt = min(kWave, te - t0);
+    for (int t0 = tb; t0 < te; t0 += RC) {
+        const int cnt = min(RC, te - t0);
         int me = -1, mi = 0;
         float mf = 0.0f, md = 0.0f;
         wave_sync();
@@ -1533,7 +1543,7 @@ static void expect(ModelImpl &m, const std::string &name, int64_t n) { m.expecte
 // one channel per lane.
 static int eq_slots(int C) { return C > 32 ? 1 : C > 16 ? 2 : 4; }
 
-// Launches kernel template k<LQ> for the runtime order lq (1..7).
+// Launches kernel template k<LQ> for the runtime order lq (1..8).
 #define EQ_LAUNCH(k, lq, grid, block, lds, s, ...)                                         \
     do {                                                                                  \
         switch (lq) {                                                                     \
@@ -1543,19 +1553,28 @@ static int eq_slots(int C) { return C > 32 ? 1 : C > 16 ? 2 : 4; }
         case 4: hipLaunchKernelGGL(k<4>, grid, block, lds, s, __VA_ARGS__); break;        \
         case 5: hipLaunchKernelGGL(k<5>, grid, block, lds, s, __VA_ARGS__); break;        \
         case 6: hipLaunchKernelGGL(k<6>, grid, block, lds, s, __VA_ARGS__); break;        \
-        default: hipLaunchKernelGGL(k<7>, grid, block, lds, s, __VA_ARGS__); break;       \
+        case 7: hipLaunchKernelGGL(k<7>, grid, block, lds, s, __VA_ARGS__); break;        \
+        default: hipLaunchKernelGGL(k<8>, grid, block, lds, s, __VA_ARGS__); break;       \
         }                                                                                 \
         RUNE_HIP_CHECK(hipGetLastError());                                                \
     } while (0)
 
-#define EQ_CASE_S(k, L, S, ...)                                                           \
-    case S: hipLaunchKernelGGL((k<L, S>), __VA_ARGS__); break;
+#define EQ_CASE_S(k, L, S, grid, block, lds, s, ...)                                      \
+    case S:                                                                               \
+        if ((lds) > 65536)                                                                \
+            RUNE_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&k<L, S>), \
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                               int(lds)));                                \
+        hipLaunchKernelGGL((k<L, S>), grid, block, lds, s, __VA_ARGS__);                  \
+        break;
 #define EQ_CASE_L(k, L, S, ...)                                                           \
     case L:                                                                               \
         switch (S) {                                                                      \
         EQ_CASE_S(k, L, 1, __VA_ARGS__)                                                   \
         EQ_CASE_S(k, L, 2, __VA_ARGS__)                                                   \
-        default: hipLaunchKernelGGL((k<L, 4>), __VA_ARGS__); break;                       \
+        default:                                                                          \
+        switch (4) { EQ_CASE_S(k, L, 4, __VA_ARGS__) }                                    \
+        break;                                                                            \
         }                                                                                 \
         break;
 // Launches kernel template k<LQ, S> of the per-atom record loops.
@@ -1569,6 +1588,7 @@ static int eq_slots(int C) { return C > 32 ? 1 : C > 16 ? 2 : 4; }
         EQ_CASE_L(k, 5, S, __VA_ARGS__)                                                   \
         EQ_CASE_L(k, 6, S, __VA_ARGS__)                                                   \
         EQ_CASE_L(k, 7, S, __VA_ARGS__)                                                   \
+        EQ_CASE_L(k, 8, S, __VA_ARGS__)                                                   \
         }                                                                                 \
         RUNE_HIP_CHECK(hipGetLastError());                                                \
     } while (0)
@@ -1623,7 +1643,8 @@ static int adj_ntc(int lq, int ldd) {
                 hipLaunchKernelGGL((k<5, 4, S>), __VA_ARGS__);                            \
             break;                                                                        \
         case 6: hipLaunchKernelGGL((k<6, 4, S>), __VA_ARGS__); break;                     \
-        default: hipLaunchKernelGGL((k<7, 4, S>), __VA_ARGS__); break;                    \
+        case 7: hipLaunchKernelGGL((k<7, 4, S>), __VA_ARGS__); break;                     \
+        default: hipLaunchKernelGGL((k<8, 4, S>), __VA_ARGS__); break;                    \
         }                                                                                 \
         RUNE_HIP_CHECK(hipGetLastError());                                                \
     } while (0)
@@ -1671,7 +1692,11 @@ static int adj_ntc(int lq, int ldd) {
         EQ_CASE_L2(k, 5, dmc, __VA_ARGS__)                                                \
         EQ_CASE_L2(k, 6, dmc, __VA_ARGS__)                                                \
         default:                                                                          \
-            switch (1) { EQ_CASE_D(k, 7, 1, __VA_ARGS__) }                                \
+            if (lq == 7) {                                                                \
+                switch (1) { EQ_CASE_D(k, 7, 1, __VA_ARGS__) }                            \
+            } else {                                                                      \
+                switch (1) { EQ_CASE_D(k, 8, 1, __VA_ARGS__) }                            \
+            }                                                                             \
             break;                                                                        \
         }                                                                                 \
         RUNE_HIP_CHECK(hipGetLastError());                                                \
@@ -1711,15 +1736,16 @@ static void launch_mix(int lq, int C, int N, const float *w, const float *in, in
     case 4: launch_mix_lq<4>(C, N, w, in, trans, add, add_t, out, s); break;
     case 5: launch_mix_lq<5>(C, N, w, in, trans, add, add_t, out, s); break;
     case 6: launch_mix_lq<6>(C, N, w, in, trans, add, add_t, out, s); break;
-    default: launch_mix_lq<7>(C, N, w, in, trans, add, add_t, out, s); break;
+    case 7: launch_mix_lq<7>(C, N, w, in, trans, add, add_t, out, s); break;
+    default: launch_mix_lq<8>(C, N, w, in, trans, add, add_t, out, s); break;
     }
 }
 
 void validate_equivariant(ModelImpl &m) {
     const rune_model_config &c = m.cfg;
     const int lq = c.equivariant_l_max, C = c.equivariant_channels;
-    RUNE_REQUIRE(lq >= 1 && lq <= std::min(c.l_max, 7), RUNE_ERR_ARGUMENT,
-                 "equivariant blocks support equivariant_l_max in 1..min(l_max, 7)");
+    RUNE_REQUIRE(lq >= 1 && lq <= std::min(c.l_max, kMaxL), RUNE_ERR_ARGUMENT,
+                 "equivariant_l_max must be in 1..min(l_max, 8)");
     RUNE_REQUIRE(C >= 1 && C <= kWave, RUNE_ERR_ARGUMENT,
                  "equivariant blocks support equivariant_channels in 1..64");
     RUNE_REQUIRE(c.message_groups >= 1 && c.message_groups <= kWave, RUNE_ERR_ARGUMENT,
@@ -1929,7 +1955,7 @@ MessagePlan plan_equivariant(ModelImpl &m, Arena &ar, int N, int64_t E) {
     p.i_dv = p.add(ar, 16 * e);
     p.i_harm = p.add(ar, 4 * e * nq);
     p.i_dharm = p.add(ar, 4 * e * nq);
-    p.i_zero = p.add(ar, 4 * 64);   // a zero row of >= nq floats
+    p.i_zero = p.add(ar, 4 * 128);   // a zero row of >= nq floats
     p.i_dfc = p.add(ar, 4 * e);
     p.i_drb = p.add(ar, 4 * e * p.ldrb);
     p.i_rbd = p.add(ar, 4 * e * p.ldrb);
@@ -2062,7 +2088,7 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
                                p.at(p.i_fc), p.at(p.i_tfc));
         }
         // dE/dY needs no clearing: the first reverse block writes every row
-        RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_zero), 0, 4 * 64, s));
+        RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_zero), 0, 4 * 128, s));
         RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dfc), 0, 4 * size_t(E), s));
     }
     {
@@ -2174,9 +2200,9 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         hipLaunchKernelGGL(k_eq_node_backward, dim3(N), dim3(kWave), 0, s, a);
         {
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
-            EQ_LAUNCH_S(k_eq_pair_dir, lq, a.S, dim3(atom_grid), dim3(kBlock),
-                        sizeof(float) * kWaves * (kWave * ly + a.S * nq * (kWave / a.S + 4)),
-                        s, a);
+            const size_t lds_pd = sizeof(float) * kWaves *
+                                  (pair_dir_chunk(nq) * ly + a.S * nq * (kWave / a.S + 4));
+            EQ_LAUNCH_S(k_eq_pair_dir, lq, a.S, dim3(atom_grid), dim3(kBlock), lds_pd, s, a);
         }
         {
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);

@@ -608,15 +608,24 @@ extern "C" int rune_model_create(const rune_model_config *config, rune_model **o
         RUNE_REQUIRE(config && out, RUNE_ERR_ARGUMENT, "null argument");
         const rune_model_config &c = *config;
         RUNE_REQUIRE(c.n_types >= 1, RUNE_ERR_ARGUMENT, "n_types must be positive");
-        RUNE_REQUIRE(c.n_desc_radial >= 1 && c.n_desc_radial <= kMaxNr, RUNE_ERR_ARGUMENT,
-                     "n_desc_radial outside [1, 16]");
-        RUNE_REQUIRE(c.k_radial >= 1 && c.k_radial <= kMaxKr, RUNE_ERR_ARGUMENT,
-                     "k_radial outside [1, 24]");
-        RUNE_REQUIRE(c.n_desc_angular >= 1 && c.n_desc_angular <= kMaxNa, RUNE_ERR_ARGUMENT,
-                     "n_desc_angular outside [1, 16]");
-        RUNE_REQUIRE(c.k_angular >= 1 && c.k_angular <= kMaxKa, RUNE_ERR_ARGUMENT,
-                     "k_angular outside [1, 24]");
+        RUNE_REQUIRE(c.n_desc_radial >= 1 && c.k_radial >= 1 && c.n_desc_angular >= 1 &&
+                         c.k_angular >= 1, RUNE_ERR_ARGUMENT,
+                     "descriptor channel counts and basis sizes must be positive");
         RUNE_REQUIRE(c.l_max >= 1 && c.l_max <= kMaxL, RUNE_ERR_ARGUMENT, "l_max outside [1, 8]");
+        {
+            // the descriptor kernels for wide models keep per-lane rows of
+            // the basis and channel values in LDS (one 64-lane wave per atom)
+            int num_L = c.l_max;
+            for (int k = 0; k < 6; ++k) num_L += c.has_q[k] ? 1 : 0;
+            const size_t nlm = size_t(c.l_max) * (c.l_max + 2), na = c.n_desc_angular;
+            const size_t kmax = std::max(c.k_radial, c.k_angular);
+            const size_t Q = c.n_desc_radial + na * num_L;
+            const size_t lds = 4 * std::max(64 * (kmax + 1 + na + 1 + nlm + 1) + na * nlm,
+                                            Q + 2 * na * nlm + 128 * (kmax + 1) + 128 * (na + 1));
+            RUNE_REQUIRE(lds <= 160 * 1024, RUNE_ERR_ARGUMENT,
+                         "descriptor too wide for one 64-lane wave per atom (n_max / basis_size "
+                         "need more than 160 KB of LDS)");
+        }
         RUNE_REQUIRE(c.rc_radial > 0 && c.rc_angular > 0, RUNE_ERR_ARGUMENT, "bad cutoffs");
         if ((c.has_q[0] || c.has_q[2]) && c.l_max < 2)
             throw Error(RUNE_ERR_ARGUMENT, "q222 / q112 require l_max >= 2");

@@ -160,11 +160,29 @@ def test_descriptor_derivatives_across_angular_orders(order):
     check(model, small_atoms(), f"order-{order}")
 
 
-@pytest.mark.parametrize("channels", [2, 3, 5])
+@pytest.mark.parametrize("channels", [2, 3, 5, 17, 33])
 def test_radial_channels_and_basis_group_boundaries(channels):
+    """Channel counts past 16 and long bases run the descriptor kernels that
+    keep per-lane rows in LDS."""
     model = model_for("local", n_max_radial=channels - 1, n_max_angular=channels - 1,
                       basis_size_radial=20, basis_size_angular=18)
     check(model, small_atoms(), f"channels-{channels}")
+
+
+@pytest.mark.parametrize("mode", ["scalar", "equivariant"])
+def test_wide_descriptor_with_message_blocks(mode):
+    """17 radial / 19 angular channels and 30 / 26 basis functions feeding MP
+    and EQ blocks (the direction encoder projects 19 angular channels)."""
+    model = model_for(mode, n_max_radial=16, n_max_angular=18, basis_size_radial=29,
+                      basis_size_angular=25)
+    check(model, small_atoms(), f"{mode}-wide-descriptor")
+
+
+def test_equivariant_order_eight():
+    """equivariant_l_max = 8, the reference's largest (rune/mobius/plugin.py:81-86)."""
+    model = model_for("equivariant", l_max=8, equivariant_l_max=8)
+    check(model, small_atoms(), "eq-order-8")
+    check(model, large_atoms(), "eq-order-8-large")
 
 
 def test_mixed_pbc_and_additional_model_options():
