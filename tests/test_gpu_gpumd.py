@@ -48,6 +48,32 @@ def test_gpumd_outputs_follow_gpumd_layout(name, heat):
     for k in range(9):
         got[A[k], B[k]] = total[k]
     torch.testing.assert_close(got, wsum.T, rtol=1e-5, atol=1e-4)
+    # against the oracle: energies, forces and the transposed per-atom virial
+    # attributed to the neighbour atom (rune/mobius/model.py:23-44); bar: the
+    # fp32 tolerances, or 2x the reference fp32 path's own deviation
+    r64 = _oracle(p, w, s, types.cpu(), torch.float64)
+    r32 = _oracle(p, w, s, types.cpu(), torch.float32)
+    wa64 = r64["atom_virial"].view(n, 3, 3)
+    expect64 = torch.stack([wa64[:, B[k], A[k]] for k in range(9)])
+    hip = (np.abs(pot.cpu() - 1.0 - r64["energies"]).max().item(),
+           np.abs(force.view(3, n).cpu() - 2.0 - r64["forces"].T).max().item(),
+           np.abs(vir.view(9, n).cpu() - 3.0 - expect64).max().item())
+    ref = tuple((r32[k].double() - r64[k]).abs().max().item()
+                for k in ("energies", "forces", "atom_virial"))
+    print(f"{name}: GPUMD arrays - fp64 oracle {hip}; reference fp32 - fp64 {ref}")
+    for h, r, t in zip(hip, ref, (1e-5, 1e-4, 1e-4)):
+        assert h <= max(t, 2.0 * r), (hip, ref)
+
+
+def _oracle(p, w, s, types, dtype):
+    from oracle import model as OM
+    from oracle import neighbors as ONB
+    sp = ONB.split(ONB.build(s.positions, s.cell, s.pbc, p["rcut_radial"], p["rcut_angular"]))
+    mk = lambda k: OM.Edges(torch.as_tensor(sp[k][0]), torch.as_tensor(sp[k][1]),
+                            torch.as_tensor(sp[k][2], dtype=dtype))
+    wt = {k: v.to(dtype) if v.is_floating_point() else v for k, v in w.items()}
+    return OM.forward(wt, p, torch.as_tensor(s.positions, dtype=dtype), types.long(),
+                      [len(s)], mk("radial"), mk("angular"))
 
 
 def test_nep_supports_heat_current():

@@ -1,18 +1,24 @@
 """Models read natively from text artifacts (``rune_model_load``) against the
-same models built from their state dicts (needs an MI355X; run with ``-m gpu``).
+same models built from their state dicts, and against the CPU oracle (needs
+an MI355X; run with ``-m gpu``).
 
 mobius1: the fixtures written by the reference's exporter
 (``tests/golden/export_*.mobius.txt``, rune/mobius/export.py:120-146) against
 this build's seeded models that produced them.  nep4 / nep4_zbl: files written
 by the nep.txt writer, read natively and by the Python reader
-(rune/nep/model.py:284-489 semantics).  Outputs must be bitwise equal.
+(rune/nep/model.py:284-489 semantics).  Native and state-dict outputs must be
+bitwise equal; the native outputs are also compared with the fp64 oracle
+evaluating the weights as the text file holds them (fp32 tolerances).
 """
 
 import numpy as np
 import pytest
 import torch
 
+from oracle import model as OM
+from oracle import neighbors as ONB
 from rune_amd import workloads as W
+from rune_amd.mobius import export as EX
 from tests.golden.make_golden import small_export_model
 from tests.helpers import GOLDEN
 
@@ -31,6 +37,22 @@ def _assert_equal(a, b):
         assert torch.equal(a[k], b[k]), k
 
 
+def _assert_matches_oracle(out, weights, params, s, types, nep=False):
+    """fp32 native outputs against the fp64 oracle on the same weights."""
+    nl = ONB.build(s.positions, s.cell, s.pbc, params["rcut_radial"], params["rcut_angular"])
+    sp = ONB.split(nl)
+    mk = lambda k: OM.Edges(torch.as_tensor(sp[k][0]), torch.as_tensor(sp[k][1]),
+                            torch.as_tensor(sp[k][2]))
+    fwd = OM.nep_forward if nep else OM.forward
+    ref = fwd(weights, params, torch.as_tensor(s.positions), torch.as_tensor(types).long(),
+              [len(s)], mk("radial"), mk("angular"))
+    de = (out["energies"].cpu().double() - ref["energies"]).abs().max().item()
+    df = (out["forces"].cpu().double() - ref["forces"]).abs().max().item()
+    dw = (out["virial"].cpu().double() - ref["virial"]).abs().max().item() / len(s)
+    print(f"native vs fp64 oracle: dE {de:.1e} dF {df:.1e} dW/atom {dw:.1e}")
+    assert de <= 1e-5 and df <= 1e-4 and dw <= 1e-5, (de, df, dw)
+
+
 @pytest.mark.parametrize("kind", ["local", "mp", "eq"])
 def test_reference_exported_mobius_txt_loads_natively(kind):
     from rune_amd import _native as N
@@ -44,8 +66,12 @@ def test_reference_exported_mobius_txt_loads_natively(kind):
     assert [native.element(t) for t in range(2)] == ["Fe", "C"]
     s = W.si_diamond(seed=41, reps=2, a=4.2)
     types = np.arange(len(s)) % 2
-    _assert_equal(_outputs(native, s, types, rc_r, rc_a, max_r, max_a),
-                  _outputs(ref, s, types, rc_r, rc_a, max_r, max_a))
+    out = _outputs(native, s, types, rc_r, rc_a, max_r, max_a)
+    _assert_equal(out, _outputs(ref, s, types, rc_r, rc_a, max_r, max_a))
+    # the weights exactly as the file holds them (float64 text of float32 values)
+    _, _, _, tensors = EX.read_mobius_txt(GOLDEN / f"export_{kind}.mobius.txt")
+    weights = {k: v for k, v in tensors.items() if not k.startswith("desc.")}
+    _assert_matches_oracle(out, weights, params, s, types)
 
 
 def _nep_variant(tmp_path, variant):
@@ -77,5 +103,8 @@ def test_nep_txt_loads_natively(variant, tmp_path):
     assert (max_r, max_a) == (100, 30)
     s = W.rocksalt(seed=42, reps=2, a=4.6)   # nearest neighbours 2.3 A: inside the ZBL taper
     types = np.array([0 if z == 82 else 1 for z in s.numbers], np.int32)
-    _assert_equal(_outputs(native, s, types, rc_r, rc_a, max_r, max_a),
-                  _outputs(ref, s, types, rc_r, rc_a, max_r, max_a))
+    out = _outputs(native, s, types, rc_r, rc_a, max_r, max_a)
+    _assert_equal(out, _outputs(ref, s, types, rc_r, rc_a, max_r, max_a))
+    weights = {k: v.detach().double() if v.is_floating_point() else v
+               for k, v in model.state_dict().items()}
+    _assert_matches_oracle(out, weights, model.params, s, types, nep=True)
