@@ -74,6 +74,27 @@ struct DeviceBuffer {
     T *as() const { return static_cast<T *>(ptr); }
 };
 
+// A few words of pinned host memory that kernels store into directly (small
+// readbacks need no copy then); allocated on first use.
+struct PinnedWords {
+    int32_t *ptr = nullptr;
+    PinnedWords() = default;
+    PinnedWords(const PinnedWords &) = delete;
+    PinnedWords &operator=(const PinnedWords &) = delete;
+    ~PinnedWords() {
+        if (ptr) (void)hipHostFree(ptr);
+    }
+    int32_t *get() {
+        if (!ptr) {
+            void *p = nullptr;
+            RUNE_HIP_CHECK(hipHostMalloc(&p, 64, hipHostMallocCoherent));
+            ptr = static_cast<int32_t *>(p);
+        }
+        return ptr;
+    }
+    int32_t read(int k) const { return static_cast<volatile int32_t *>(ptr)[k]; }
+};
+
 // Bump allocator over one DeviceBuffer: plan sizes first, then carve.
 struct Arena {
     std::vector<size_t> sizes;

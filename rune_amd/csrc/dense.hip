@@ -229,6 +229,110 @@ __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *
     tile_epilogue<WM, WN, WMW>(acc, smem, M, N, C, ldc, ep, m0, n0);
 }
 
+// One output element of the fused epilogue (the terms of tile_epilogue in the
+// same order); the element's loads precede its stores, so C may alias an
+// input element for element.
+__device__ inline void epilogue_one(const Epilogue &ep, float acc, int row, int col,
+                                    float *__restrict__ C, int ldc) {
+    float t = acc;
+    if (ep.row_scale) t *= ep.row_scale[row];
+    if (ep.bias) t += ep.bias[col];
+    if (ep.emb) t += ep.emb[size_t(ep.types[row]) * ep.ld_emb + col];
+    if (ep.residual) t += ep.residual[size_t(row) * ep.ldr + col];
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+        if (ep.gtab[k]) t += ep.gtab[k][size_t(ep.gidx[k][row]) * ep.gld[k] + col];
+    const float du = ep.dact_from ? ep.dact_from[size_t(row) * ep.ldu + col] : 0.0f;
+    if (ep.pre) ep.pre[size_t(row) * ep.ldp + col] = t;
+    if (ep.act_split >= 0 && col >= ep.act_split)
+        t = act_f(ep.act2, t);
+    else if (ep.act >= 0)
+        t = act_f(ep.act, t);
+    if (ep.dact_from) t *= act_d(ep.dact, du);
+    C[size_t(row) * ldc + col] = t;
+}
+
+// Four consecutive K values x[k..k+3] of one operand row, zero past K.
+template <bool kVec>
+__device__ inline float4 load_k4(const float *__restrict__ x, int k, int K) {
+    if (kVec && k + 3 < K) return *reinterpret_cast<const float4 *>(x + k);
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (k < K) v.x = x[k];
+    if (k + 1 < K) v.y = x[k + 1];
+    if (k + 2 < K) v.z = x[k + 2];
+    if (k + 3 < K) v.w = x[k + 3];
+    return v;
+}
+
+// GEMM for grids smaller than the chip (a few hundred rows, e.g. every dense
+// layer of a 512-atom cell): one 16 x (16*WN) output tile per 256-thread
+// block, so the launch has 4-16x more blocks than the 64-row tiles, and the
+// K range split over the block's 4 waves in 16-deep steps (step s to wave
+// s % 4).  Operands go straight from global memory into the MFMA layout
+// (lane l holds row l%16 at k = 16 s + 4 (l/16) + {0..3}; the next step's
+// operands are loaded before the current step's products); the 4 partial
+// tiles are summed through LDS in wave order and the epilogue runs per
+// element with consecutive threads on consecutive columns.
+template <int WN, bool kVec>
+__global__ void __launch_bounds__(256) k_gemm_small(int M, int N, int K,
+                                                    const float *__restrict__ A, int lda,
+                                                    const float *__restrict__ Bt, int ldb,
+                                                    float *__restrict__ C, int ldc, Epilogue ep,
+                                                    int nbn) {
+    constexpr int TN = 16 * WN;
+    __shared__ float part[4][16][TN + 1];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int m0 = (int(blockIdx.x) / nbn) * 16, n0 = (int(blockIdx.x) % nbn) * TN;
+    const int r = lane & 15, g = lane >> 4;
+    const float *a = A + size_t(min(m0 + r, M - 1)) * lda;
+    const float *b[WN];
+#pragma unroll
+    for (int j = 0; j < WN; ++j) b[j] = Bt + size_t(min(n0 + 16 * j + r, N - 1)) * ldb;
+    floatx4 acc[WN];
+#pragma unroll
+    for (int j = 0; j < WN; ++j) acc[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int steps = (K + 15) >> 4;
+    float4 fa = make_float4(0.0f, 0.0f, 0.0f, 0.0f), fb[WN];
+#pragma unroll
+    for (int j = 0; j < WN; ++j) fb[j] = fa;
+    if (wave < steps) {
+        fa = load_k4<kVec>(a, 16 * wave + 4 * g, K);
+#pragma unroll
+        for (int j = 0; j < WN; ++j) fb[j] = load_k4<kVec>(b[j], 16 * wave + 4 * g, K);
+    }
+    for (int st = wave; st < steps; st += 4) {
+        float4 na = fa, nb[WN];
+#pragma unroll
+        for (int j = 0; j < WN; ++j) nb[j] = fb[j];
+        if (st + 4 < steps) {
+            na = load_k4<kVec>(a, 16 * (st + 4) + 4 * g, K);
+#pragma unroll
+            for (int j = 0; j < WN; ++j) nb[j] = load_k4<kVec>(b[j], 16 * (st + 4) + 4 * g, K);
+        }
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa.x, fb[j].x, acc[j], 0, 0, 0);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa.y, fb[j].y, acc[j], 0, 0, 0);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa.z, fb[j].z, acc[j], 0, 0, 0);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa.w, fb[j].w, acc[j], 0, 0, 0);
+        }
+        fa = na;
+#pragma unroll
+        for (int j = 0; j < WN; ++j) fb[j] = nb[j];
+    }
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) part[wave][4 * g + v][16 * j + r] = acc[j][v];
+    __syncthreads();
+    for (int e = threadIdx.x; e < 16 * TN; e += 256) {
+        const int rr = e / TN, cc = e % TN, row = m0 + rr, col = n0 + cc;
+        if (row >= M || col >= N) continue;
+        const float v = ((part[0][rr][cc] + part[1][rr][cc]) + part[2][rr][cc]) + part[3][rr][cc];
+        epilogue_one(ep, v, row, col, C, ldc);
+    }
+}
+
 __device__ inline float wave_sum(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -343,6 +447,10 @@ __global__ void __launch_bounds__(256) k_nep_mlp(int M, int Q, int Hn, const flo
 // tile is taken when it pads N less.
 static bool narrow_tile(int N) { return ceil_div(N, 32) * 32 < ceil_div(N, 64) * 64; }
 
+// Below this many 64-row tiles (one per CU) a launch cannot fill the chip and
+// the small-grid kernel, with K split over the waves of a block, is used.
+constexpr int64_t kSmallGemmBlocks = 256;
+
 template <int WM, int WN, int WMW = 2>
 static void launch_gemm(bool vec, int M, int N, int K, const float *A, int lda, const float *Bt,
                         int ldb, float *C, int ldc, const Epilogue &ep, const GemmBatch &bt,
@@ -372,7 +480,25 @@ static void gemm_any(int M, int N, int K, const float *A, int lda, const float *
     if (M == 0 || N == 0 || bt.count == 0) return;
     bool vec = lda % 4 == 0 && ldb % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
                (reinterpret_cast<uintptr_t>(Bt) & 15) == 0 && bt.sa % 4 == 0 && bt.sb % 4 == 0;
-    if (narrow_tile(N))
+    const int64_t big_blocks = int64_t(ceil_div(M, 64)) * ceil_div(N, narrow_tile(N) ? 32 : 64);
+    if (big_blocks < kSmallGemmBlocks && bt.count == 1 && ep.a_act < 0) {
+        // 16 x 32 tiles, or 16 x 16 when that pads N less
+        const bool n16 = ceil_div(N, 16) * 16 < ceil_div(N, 32) * 32;
+        const int nbn = ceil_div(N, n16 ? 16 : 32);
+        const dim3 grid(unsigned(int64_t(ceil_div(M, 16)) * nbn));
+        if (n16 && vec)
+            hipLaunchKernelGGL((k_gemm_small<1, true>), grid, dim3(256), 0, s, M, N, K, A, lda, Bt,
+                               ldb, C, ldc, ep, nbn);
+        else if (n16)
+            hipLaunchKernelGGL((k_gemm_small<1, false>), grid, dim3(256), 0, s, M, N, K, A, lda,
+                               Bt, ldb, C, ldc, ep, nbn);
+        else if (vec)
+            hipLaunchKernelGGL((k_gemm_small<2, true>), grid, dim3(256), 0, s, M, N, K, A, lda, Bt,
+                               ldb, C, ldc, ep, nbn);
+        else
+            hipLaunchKernelGGL((k_gemm_small<2, false>), grid, dim3(256), 0, s, M, N, K, A, lda,
+                               Bt, ldb, C, ldc, ep, nbn);
+    } else if (narrow_tile(N))
         launch_gemm<1, 2, 4>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, bt, s);
     else
         launch_gemm<2, 2, 2>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, bt, s);

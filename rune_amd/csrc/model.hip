@@ -284,6 +284,13 @@ static void finalize(ModelImpl &m) {
     m.weights.reserve(pk.data.size() * sizeof(float));
     RUNE_HIP_CHECK(hipMemcpy(m.weights.ptr, pk.data.data(), pk.data.size() * sizeof(float),
                              hipMemcpyHostToDevice));
+    if (!m.type_flag_host) {
+        void *flag = nullptr;
+        RUNE_HIP_CHECK(hipHostMalloc(&flag, 64, hipHostMallocCoherent));
+        m.type_flag_host = static_cast<int32_t *>(flag);
+        *m.type_flag_host = 0;
+    }
+    if (!m.type_event) RUNE_HIP_CHECK(hipEventCreateWithFlags(&m.type_event, hipEventDisableTiming));
     const float *base = m.weights.as<float>();
     auto P = [&](const std::string &k) -> const float * {
         auto it = off.find(k);
@@ -334,10 +341,30 @@ static void finalize(ModelImpl &m) {
 // compute
 // ---------------------------------------------------------------------------
 
-__global__ void k_check_types(int n, const int32_t *types, int n_types, int32_t *flag) {
-    int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n && (types[i] < 0 || types[i] >= n_types)) atomicOr(flag, 1);
+// Range check of the atom types.  Writes a copy with every type clamped into
+// [0, n_types) -- the kernels after it read the copy, so a bad type never
+// indexes past a table -- and flags any type outside the range.  One block:
+// the flag is stored once, with no clearing launch before it; several
+// blocks: bit 0 is or-ed into a flag cleared beforehand.
+__global__ void __launch_bounds__(1024) k_check_types(int n, const int32_t *types, int n_types,
+                                                      int32_t *safe, int32_t *flag) {
+    int bad = 0;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const int t = types[i];
+        const bool out = t < 0 || t >= n_types;
+        safe[i] = out ? 0 : t;
+        bad |= out;
+    }
+    if (gridDim.x == 1) {
+        bad = __syncthreads_or(bad);
+        if (threadIdx.x == 0) *flag = bad;
+    } else if (bad) {
+        atomicOr(flag, 1);
+    }
 }
+
+// Largest atom count checked by one block of k_check_types.
+constexpr int kTypeCheckOneBlock = 1 << 16;
 
 static Records records_of(const rune_nlist *nl) {
     Records r;
@@ -383,6 +410,7 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     // ---- workspace plan ----
     Arena ar;
     size_t o_flag = ar.add(16);
+    size_t o_types = ar.add(4 * size_t(N));
     size_t o_q = ar.add(4 * size_t(N) * ldq);
     size_t o_dq = ar.add(4 * size_t(N) * ldq);
     size_t o_s = ar.add(4 * size_t(N) * nmom);
@@ -416,15 +444,25 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     float *forces = d_forces ? d_forces : reinterpret_cast<float *>(base + o_f);
     lp.bind(base);
     mp.bind(base);
-    // ---- type validation (one small readback) ----
-    RUNE_HIP_CHECK(hipMemsetAsync(flag, 0, 16, s));
-    if (N > 0)
-        hipLaunchKernelGGL(k_check_types, dim3(ceil_div(N, 256)), dim3(256), 0, s, N, types,
-                           m.cfg.n_types, flag);
-    int32_t hflag = 0;
-    RUNE_HIP_CHECK(hipMemcpyAsync(&hflag, flag, 4, hipMemcpyDeviceToHost, s));
-    RUNE_HIP_CHECK(hipStreamSynchronize(s));
-    RUNE_REQUIRE(hflag == 0, RUNE_ERR_TYPE, "atom type outside [0, n_types)");
+    // ---- type validation: the flag travels to pinned host memory behind the
+    // check kernel and is read once everything else is enqueued, so the
+    // host never waits on an idle device; the kernels read the clamped copy
+    if (N > 0) {
+        int32_t *safe = reinterpret_cast<int32_t *>(base + o_types);
+        if (N <= kTypeCheckOneBlock) {
+            // one block stores the verdict straight into the pinned word
+            hipLaunchKernelGGL(k_check_types, dim3(1), dim3(1024), 0, s, N, types, m.cfg.n_types,
+                               safe, m.type_flag_host);
+        } else {
+            RUNE_HIP_CHECK(hipMemsetAsync(flag, 0, 16, s));
+            hipLaunchKernelGGL(k_check_types, dim3(std::min(ceil_div(N, 1024), 1024)), dim3(1024),
+                               0, s, N, types, m.cfg.n_types, safe, flag);
+            RUNE_HIP_CHECK(hipMemcpyAsync(m.type_flag_host, flag, 4, hipMemcpyDeviceToHost, s));
+        }
+        RUNE_HIP_CHECK(hipGetLastError());
+        RUNE_HIP_CHECK(hipEventRecord(m.type_event, s));
+        types = safe;
+    }
     if (N == 0) {
         // no atoms: every structure's energy and virial is zero (the sums
         // over empty ranges read nothing)
@@ -487,9 +525,15 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
         if (want_w && d_virial) structure_sum(r, atom_virial, 9, d_virial, sums, s);
     }
     mark(8);
+    // the type verdict (on a bad type the outputs written above are unspecified)
+    RUNE_HIP_CHECK(hipEventSynchronize(m.type_event));
+    RUNE_REQUIRE(*static_cast<volatile int32_t *>(m.type_flag_host) == 0, RUNE_ERR_TYPE,
+                 "atom type outside [0, n_types)");
 }
 
 ModelImpl::~ModelImpl() {
+    if (type_event) (void)hipEventDestroy(type_event);
+    if (type_flag_host) (void)hipHostFree(type_flag_host);
     for (auto &e : events) (void)hipEventDestroy(e);
     for (auto &e : span_ev) (void)hipEventDestroy(e);
 }
@@ -863,6 +907,7 @@ extern "C" int rune_model_descriptor_extrema(rune_model *model, const rune_nlist
         const int ldq = (m.Q + 3) & ~3;
         Arena ar;
         const size_t o_flag = ar.add(16);
+        const size_t o_types = ar.add(4 * size_t(std::max(N, 1)));
         const size_t o_q = ar.add(4 * size_t(std::max(N, 1)) * ldq);
         const size_t o_s = ar.add(4 * size_t(std::max(N, 1)) * d.na * d.nlm);
         m.work.reserve(ar.total);
@@ -870,8 +915,9 @@ extern "C" int rune_model_descriptor_extrema(rune_model *model, const rune_nlist
         int32_t *flag = reinterpret_cast<int32_t *>(base + o_flag);
         RUNE_HIP_CHECK(hipMemsetAsync(flag, 0, 16, s));
         if (N > 0)
-            hipLaunchKernelGGL(k_check_types, dim3(ceil_div(N, 256)), dim3(256), 0, s, N,
-                               d_types, m.cfg.n_types, flag);
+            hipLaunchKernelGGL(k_check_types, dim3(std::min(ceil_div(N, 1024), 1024)), dim3(1024),
+                               0, s, N, d_types, m.cfg.n_types,
+                               reinterpret_cast<int32_t *>(base + o_types), flag);
         int32_t hflag = 0;
         RUNE_HIP_CHECK(hipMemcpyAsync(&hflag, flag, 4, hipMemcpyDeviceToHost, s));
         RUNE_HIP_CHECK(hipStreamSynchronize(s));

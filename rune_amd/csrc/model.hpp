@@ -121,6 +121,10 @@ struct ModelImpl {
     // NEP
     const float *nep_w0 = nullptr, *nep_b0 = nullptr, *nep_w1 = nullptr;
     float nep_bias = 0.0f;
+    // type-check verdict: pinned host word written behind the check kernel,
+    // and the event that marks its arrival (created by rune_model_finalize)
+    int32_t *type_flag_host = nullptr;
+    hipEvent_t type_event = nullptr;
     // phase timing ring (events recorded on the launch stream)
     bool timing = false;
     std::vector<hipEvent_t> events;       // kTimingRing x (RUNE_N_PHASES + 1)

@@ -413,7 +413,7 @@ __global__ void __launch_bounds__(256) decode_wave(int n, const double *pos, con
                                                    const int32_t *ptr, const int32_t *cnt_r,
                                                    const int32_t *cnt_a, const uint64_t *keys,
                                                    int32_t *view, int32_t *nbr, int32_t *shift,
-                                                   float4 *vec, int32_t *ctr) {
+                                                   float4 *vec, int32_t *ctr, int32_t *indeg) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int i = blockIdx.x * 4 + wave;
     if (i >= n) return;
@@ -443,6 +443,7 @@ __global__ void __launch_bounds__(256) decode_wave(int n, const double *pos, con
         }
         nbr[r] = j;
         ctr[r] = i;
+        atomicAdd(indeg + j, 1);   // in-degree of the transpose
         shift[3 * r + 0] = S[0];
         shift[3 * r + 1] = S[1];
         shift[3 * r + 2] = S[2];
@@ -521,23 +522,19 @@ __global__ void fill_in(int64_t e, const int32_t *nbr, const int32_t *tptr, int3
     tidx[tptr[a] + slot] = int(r);
 }
 
-// Centre of each transposed record (tctr[t] = ctr[tidx[t]]).
-__global__ void transpose_centres(int64_t e, const int32_t *tidx, const int32_t *ctr,
-                                  int32_t *tctr) {
-    int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (t < e) tctr[t] = ctr[tidx[t]];
-}
-
-// Each atom's transposed records in ascending record order: one atom per
-// wave, ranked in LDS (record ids are distinct, so each value's rank is the
-// number of smaller ones); an atom with more than kWaveKeys falls back to
-// lane 0's insertion sort in global memory.
-__global__ void __launch_bounds__(256) sort_in(int n, const int32_t *tptr, int32_t *tidx) {
+// Each atom's transposed records in ascending record order, and the centre
+// of each (tctr[t] = ctr[tidx[t]]): one atom per wave, ranked in LDS (record
+// ids are distinct, so each value's rank is the number of smaller ones); an
+// atom with more than kWaveKeys falls back to lane 0's insertion sort in
+// global memory.
+__global__ void __launch_bounds__(256) sort_in(int n, const int32_t *tptr, int32_t *tidx,
+                                               const int32_t *ctr, int32_t *tctr) {
     __shared__ int32_t kl[4][kWaveKeys];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int a = blockIdx.x * 4 + wave;
     if (a >= n) return;
     int32_t *k = tidx + tptr[a];
+    int32_t *kc = tctr + tptr[a];
     const int c = tptr[a + 1] - tptr[a];
     if (c <= kWaveKeys) {
         for (int p = lane; p < c; p += kWave) kl[wave][p] = k[p];
@@ -547,6 +544,7 @@ __global__ void __launch_bounds__(256) sort_in(int n, const int32_t *tptr, int32
             int rank = 0;
             for (int b = 0; b < c; ++b) rank += kl[wave][b] < x ? 1 : 0;
             k[rank] = x;
+            kc[rank] = ctr[x];
         }
         return;
     }
@@ -559,6 +557,16 @@ __global__ void __launch_bounds__(256) sort_in(int n, const int32_t *tptr, int32
             --q;
         }
         k[q + 1] = x;
+    }
+    for (int p = 0; p < c; ++p) kc[p] = ctr[k[p]];
+}
+
+// The record total ptr[n] and the builder's flag word, stored straight into
+// pinned host memory (read after one stream synchronisation).
+__global__ void publish_counts(const int32_t *total, const int32_t *flag, int32_t *host) {
+    if (threadIdx.x == 0) {
+        host[0] = *total;
+        host[1] = *flag;
     }
 }
 
@@ -712,35 +720,55 @@ static double from_ordered_bits(uint64_t k) {
     return x;
 }
 
+// Upload of a small host array to `dev`, skipped when the device copy
+// already holds these bytes (`shadow` keeps what was last uploaded; a
+// reallocation of `dev` forces the upload).  Repeated builds of one system
+// then issue no host-to-device copies.
+void upload_cached(rune::DeviceBuffer &dev, std::vector<char> &shadow, const void *src,
+                   size_t bytes, hipStream_t s) {
+    void *before = dev.ptr;
+    dev.reserve(std::max<size_t>(bytes, 1));
+    if (dev.ptr == before && shadow.size() == bytes &&
+        (bytes == 0 || std::memcmp(shadow.data(), src, bytes) == 0))
+        return;
+    shadow.assign(static_cast<const char *>(src), static_cast<const char *>(src) + bytes);
+    if (bytes)
+        RUNE_HIP_CHECK(hipMemcpyAsync(dev.ptr, shadow.data(), bytes, hipMemcpyHostToDevice, s));
+}
+
+// Atom count from which the builder computes the Morton processing order.
+constexpr int kOrderMinAtoms = 4096;
+
 struct Work {
     int32_t *atom_bin, *atom_wrap, *atom_cell, *bin_count, *bin_start, *bin_cursor, *bin_atoms;
     int32_t *cnt_union, *cnt_r, *cnt_a, *flag, *scan_tmp, *indeg;
     Geo *geo;
 };
 
-void build_transpose(rune_nlist *nl, int32_t *indeg, int32_t *scan_tmp, hipStream_t s) {
+// indeg and cursor: n + 1 counters each, cleared by the caller (inside its
+// one clearing of the builder's counters); `counted`: indeg already holds
+// the in-degrees (counted while the records were written).
+void build_transpose(rune_nlist *nl, int32_t *indeg, int32_t *cursor, int32_t *scan_tmp,
+                     bool counted, hipStream_t s) {
     int n = int(nl->n_atoms);
     int64_t e = nl->n_records;
     nl->tptr.reserve(sizeof(int32_t) * (n + 1));
     nl->tidx.reserve(sizeof(int32_t) * std::max<int64_t>(e, 1));
-    RUNE_HIP_CHECK(hipMemsetAsync(indeg, 0, sizeof(int32_t) * (n + 1), s));
-    if (e > 0)
+    if (e > 0 && !counted)
         hipLaunchKernelGGL(count_in, dim3(ceil_div(e, kThreads)), dim3(kThreads), 0, s, e,
                            nl->nbr.as<int32_t>(), indeg);
     exclusive_scan(indeg, nl->tptr.as<int32_t>(), n, scan_tmp, s);
-    RUNE_HIP_CHECK(hipMemsetAsync(indeg, 0, sizeof(int32_t) * (n + 1), s));
     if (e > 0) {
         hipLaunchKernelGGL(fill_in, dim3(ceil_div(e, kThreads)), dim3(kThreads), 0, s, e,
-                           nl->nbr.as<int32_t>(), nl->tptr.as<int32_t>(), indeg,
+                           nl->nbr.as<int32_t>(), nl->tptr.as<int32_t>(), cursor,
                            nl->tidx.as<int32_t>());
+        nl->tctr.reserve(sizeof(int32_t) * std::max<int64_t>(e, 1));
         hipLaunchKernelGGL(sort_in, dim3(ceil_div(n, 4)), dim3(256), 0, s, n,
-                           nl->tptr.as<int32_t>(), nl->tidx.as<int32_t>());
+                           nl->tptr.as<int32_t>(), nl->tidx.as<int32_t>(),
+                           nl->ctr.as<int32_t>(), nl->tctr.as<int32_t>());
+    } else {
+        nl->tctr.reserve(sizeof(int32_t));
     }
-    nl->tctr.reserve(sizeof(int32_t) * std::max<int64_t>(e, 1));
-    if (e > 0)
-        hipLaunchKernelGGL(transpose_centres, dim3(ceil_div(e, kThreads)), dim3(kThreads), 0, s,
-                           e, nl->tidx.as<int32_t>(), nl->ctr.as<int32_t>(),
-                           nl->tctr.as<int32_t>());
     RUNE_HIP_CHECK(hipGetLastError());
 }
 
@@ -796,9 +824,7 @@ static void set_structures(rune_nlist *nl, int64_t n_atoms, int32_t nstruct,
     nl->h_struct_ptr.assign(h_sptr, h_sptr + nstruct + 1);
     std::vector<int32_t> sp(nstruct + 1);
     for (int b = 0; b <= nstruct; ++b) sp[b] = int32_t(h_sptr[b]);
-    nl->sptr.reserve(sizeof(int32_t) * (nstruct + 1));
-    RUNE_HIP_CHECK(hipMemcpyAsync(nl->sptr.ptr, sp.data(), sizeof(int32_t) * (nstruct + 1),
-                                  hipMemcpyHostToDevice, s));
+    upload_cached(nl->sptr, nl->sptr_shadow, sp.data(), sizeof(int32_t) * (nstruct + 1), s);
     nl->n_structures = nstruct;
     nl->n_atoms = n_atoms;
 }
@@ -868,28 +894,30 @@ static void build_lists(rune_nlist *nl, int64_t n_atoms, const double *d_positio
         total_bins += geo[b].nbin[0] * geo[b].nbin[1] * geo[b].nbin[2];
     }
     // working memory
+    // (the counters that start at zero come first, so one fill clears them)
     Arena ar;
-    size_t o_geo = ar.add(sizeof(Geo) * n_structures);
+    size_t o_flag = ar.add(16);
+    size_t o_bcnt = ar.add(4 * size_t(total_bins + 1));
+    size_t o_bcur = ar.add(4 * size_t(total_bins + 1));
+    size_t o_indeg = ar.add(4 * size_t(n + 1));
+    size_t o_tcur = ar.add(4 * size_t(n + 1));
+    const size_t zero_bytes = ar.total;
     size_t o_abin = ar.add(4 * size_t(n + 1));
     size_t o_wrap = ar.add(12 * size_t(n + 1));
     size_t o_cell = ar.add(12 * size_t(n + 1));
-    size_t o_bcnt = ar.add(4 * size_t(total_bins + 1));
     size_t o_bst = ar.add(4 * size_t(total_bins + 2));
-    size_t o_bcur = ar.add(4 * size_t(total_bins + 1));
     size_t o_batm = ar.add(4 * size_t(n + 1));
     size_t o_cu = ar.add(4 * size_t(n + 1));
     size_t o_cr = ar.add(4 * size_t(n + 1));
     size_t o_ca = ar.add(4 * size_t(n + 1));
-    size_t o_flag = ar.add(16);
     size_t o_scan = ar.add(4 * scan_tmp_ints(std::max(n, total_bins) + 1));
-    size_t o_indeg = ar.add(4 * size_t(n + 1));
-    size_t o_perm = ar.add(4 * size_t(total_bins + 1));
     size_t o_rcnt = ar.add(4 * size_t(total_bins + 1));
     size_t o_rst = ar.add(4 * size_t(total_bins + 2));
     nl->work.reserve(ar.total);
     char *base = nl->work.as<char>();
     Work w;
-    w.geo = reinterpret_cast<Geo *>(base + o_geo);
+    upload_cached(nl->geo, nl->geo_shadow, geo.data(), sizeof(Geo) * n_structures, s);
+    w.geo = nl->geo.as<Geo>();
     w.atom_bin = reinterpret_cast<int32_t *>(base + o_abin);
     w.atom_wrap = reinterpret_cast<int32_t *>(base + o_wrap);
     w.atom_cell = reinterpret_cast<int32_t *>(base + o_cell);
@@ -903,9 +931,8 @@ static void build_lists(rune_nlist *nl, int64_t n_atoms, const double *d_positio
     w.flag = reinterpret_cast<int32_t *>(base + o_flag);
     w.scan_tmp = reinterpret_cast<int32_t *>(base + o_scan);
     w.indeg = reinterpret_cast<int32_t *>(base + o_indeg);
-    RUNE_HIP_CHECK(hipMemcpyAsync(w.geo, geo.data(), sizeof(Geo) * n_structures,
-                                  hipMemcpyHostToDevice, s));
-    RUNE_HIP_CHECK(hipMemsetAsync(w.flag, 0, 16, s));
+    int32_t *tcur = reinterpret_cast<int32_t *>(base + o_tcur);
+    RUNE_HIP_CHECK(hipMemsetAsync(base, 0, zero_bytes, s));
     nl->ptr.reserve(4 * size_t(n + 1));
     nl->view.reserve(16 * size_t(n + 1));
     int gb = ceil_div(std::max(n, 1), kThreads);
@@ -915,8 +942,6 @@ static void build_lists(rune_nlist *nl, int64_t n_atoms, const double *d_positio
     nl->keys.reserve(8 * size_t(std::max(n, 1)) * size_t(cap));
     const double rc2_r = rc_radial * rc_radial, rc2_a = rc_angular * rc_angular, rc2 = rc * rc;
     if (binned) {
-        RUNE_HIP_CHECK(hipMemsetAsync(w.bin_count, 0, 4 * size_t(total_bins + 1), s));
-        RUNE_HIP_CHECK(hipMemsetAsync(w.bin_cursor, 0, 4 * size_t(total_bins + 1), s));
         if (n > 0)
             hipLaunchKernelGGL(bin_atoms, dim3(gb), dim3(kThreads), 0, s, n, d_positions, sptr,
                                n_structures, w.geo, w.atom_bin, w.atom_wrap, w.atom_cell,
@@ -976,12 +1001,12 @@ static void build_lists(rune_nlist *nl, int64_t n_atoms, const double *d_positio
                                nl->keys.as<uint64_t>());
     }
     exclusive_scan(w.cnt_union, nl->ptr.as<int32_t>(), n, w.scan_tmp, s);
+    int32_t *words = nl->readback.get();
+    hipLaunchKernelGGL(publish_counts, dim3(1), dim3(64), 0, s, nl->ptr.as<int32_t>() + n, w.flag,
+                       words);
     RUNE_HIP_CHECK(hipGetLastError());
-    int32_t host[2] = {0, 0};
-    RUNE_HIP_CHECK(hipMemcpyAsync(&host[0], nl->ptr.as<int32_t>() + n, 4,
-                                  hipMemcpyDeviceToHost, s));
-    RUNE_HIP_CHECK(hipMemcpyAsync(&host[1], w.flag, 4, hipMemcpyDeviceToHost, s));
     RUNE_HIP_CHECK(hipStreamSynchronize(s));
+    const int32_t host[2] = {nl->readback.read(0), nl->readback.read(1)};
     RUNE_REQUIRE(!(host[1] & 2), RUNE_ERR_ARGUMENT, kShiftMessage);
     if (host[1]) {
         std::vector<int32_t> cr(n), ca(n);
@@ -1002,25 +1027,36 @@ static void build_lists(rune_nlist *nl, int64_t n_atoms, const double *d_positio
                            sptr, n_structures, w.geo, cap, nl->ptr.as<int32_t>(), w.cnt_r,
                            w.cnt_a, nl->keys.as<uint64_t>(), nl->view.as<int32_t>(),
                            nl->nbr.as<int32_t>(), nl->shift.as<int32_t>(), nl->vec.as<float4>(),
-                           nl->ctr.as<int32_t>());
+                           nl->ctr.as<int32_t>(), w.indeg);
     }
     RUNE_HIP_CHECK(hipGetLastError());
-    build_transpose(nl, w.indeg, w.scan_tmp, s);
+    build_transpose(nl, w.indeg, tcur, w.scan_tmp, true, s);
     // processing order: atoms bin by bin, bins in Morton order (kept from the
-    // last binning when the candidates are reused; it only orders the work)
-    if (binned) {
+    // last binning when the candidates are reused; it only orders the work,
+    // so a list of fewer than kOrderMinAtoms atoms, which fits in L2 either
+    // way, keeps the index order and saves the launches)
+    if (binned && n < kOrderMinAtoms) {
+        nl->has_order = false;
+    } else if (binned) {
         nl->order.reserve(4 * size_t(std::max(n, 1)));
         if (n > 0) {
-            std::vector<int32_t> &perm = nl->h_perm;   // outlives the asynchronous upload
-            perm.clear();
-            perm.reserve(total_bins);
-            for (int b = 0; b < n_structures; ++b)
-                morton_bins(geo[b].nbin, geo[b].bin_offset, perm);
-            int32_t *d_perm = reinterpret_cast<int32_t *>(base + o_perm);
+            // the bin ranks depend only on the bin grids: recomputed and
+            // uploaded when those changed
+            const size_t gbytes = sizeof(Geo) * n_structures;
+            if (nl->perm_geo.size() != gbytes ||
+                std::memcmp(nl->perm_geo.data(), geo.data(), gbytes) != 0) {
+                nl->h_perm.clear();
+                nl->h_perm.reserve(total_bins);
+                for (int b = 0; b < n_structures; ++b)
+                    morton_bins(geo[b].nbin, geo[b].bin_offset, nl->h_perm);
+                nl->perm_geo.assign(reinterpret_cast<const char *>(geo.data()),
+                                    reinterpret_cast<const char *>(geo.data()) + gbytes);
+            }
+            upload_cached(nl->perm, nl->perm_shadow, nl->h_perm.data(),
+                          4 * nl->h_perm.size(), s);
+            int32_t *d_perm = nl->perm.as<int32_t>();
             int32_t *rcnt = reinterpret_cast<int32_t *>(base + o_rcnt);
             int32_t *rst = reinterpret_cast<int32_t *>(base + o_rst);
-            RUNE_HIP_CHECK(hipMemcpyAsync(d_perm, perm.data(), 4 * perm.size(),
-                                          hipMemcpyHostToDevice, s));
             const int bg = ceil_div(total_bins, kThreads);
             hipLaunchKernelGGL(rank_counts, dim3(bg), dim3(kThreads), 0, s, total_bins, d_perm,
                                w.bin_count, rcnt);
@@ -1123,12 +1159,14 @@ extern "C" int rune_nlist_from_padded(rune_nlist *nl, int64_t n_atoms, const flo
         nl->has_order = false;
         const int n = int(n_atoms);
         Arena ar;
+        size_t o_flag = ar.add(16);
+        size_t o_indeg = ar.add(4 * size_t(n + 1));
+        size_t o_tcur = ar.add(4 * size_t(n + 1));
+        const size_t zero_bytes = ar.total;
         size_t o_cu = ar.add(4 * size_t(n + 1));
         size_t o_cr = ar.add(4 * size_t(n + 1));
         size_t o_ca = ar.add(4 * size_t(n + 1));
-        size_t o_flag = ar.add(16);
         size_t o_scan = ar.add(4 * scan_tmp_ints(n + 1));
-        size_t o_indeg = ar.add(4 * size_t(n + 1));
         nl->work.reserve(ar.total);
         char *base = nl->work.as<char>();
         int32_t *cu = reinterpret_cast<int32_t *>(base + o_cu);
@@ -1137,7 +1175,8 @@ extern "C" int rune_nlist_from_padded(rune_nlist *nl, int64_t n_atoms, const flo
         int32_t *flag = reinterpret_cast<int32_t *>(base + o_flag);
         int32_t *scan_tmp = reinterpret_cast<int32_t *>(base + o_scan);
         int32_t *indeg = reinterpret_cast<int32_t *>(base + o_indeg);
-        RUNE_HIP_CHECK(hipMemsetAsync(flag, 0, 16, s));
+        int32_t *tcur = reinterpret_cast<int32_t *>(base + o_tcur);
+        RUNE_HIP_CHECK(hipMemsetAsync(base, 0, zero_bytes, s));
         nl->ptr.reserve(4 * size_t(n + 1));
         nl->view.reserve(16 * size_t(n + 1));
         int gb = ceil_div(std::max(n, 1), kThreads);
@@ -1172,7 +1211,7 @@ extern "C" int rune_nlist_from_padded(rune_nlist *nl, int64_t n_atoms, const flo
                                nl->shift.as<int32_t>(), nl->vec.as<float4>(),
                                nl->ctr.as<int32_t>());
         RUNE_HIP_CHECK(hipGetLastError());
-        build_transpose(nl, indeg, scan_tmp, s);
+        build_transpose(nl, indeg, tcur, scan_tmp, false, s);
         if (n_records) *n_records = e;
     });
 }

@@ -23,11 +23,16 @@ struct rune_nlist {
     rune::DeviceBuffer tidx;     // int32 [E]
     rune::DeviceBuffer tctr;     // int32 [E] centre of each transposed record
     rune::DeviceBuffer sptr;     // int32 [B+1] device copy of structure ranges
+    rune::DeviceBuffer geo;      // bin frames of the structures
+    rune::DeviceBuffer perm;     // int32 Morton rank of every bin
+    // host copies of what sptr, geo and perm last received (repeated builds of
+    // one system upload nothing), and the bin grids behind h_perm
+    std::vector<char> sptr_shadow, geo_shadow, perm_shadow, perm_geo;
     // atoms in cell-bin order (spatially coherent processing order); empty
     // for lists made from padded tensors
     rune::DeviceBuffer order;    // int32 [N]
     bool has_order = false;
-    std::vector<int32_t> h_perm; // host bin ranks behind the last order upload
+    std::vector<int32_t> h_perm; // host Morton ranks of the bins
     // skin reuse (rune_nlist_update): candidates within max(rc) + skin of the
     // last search, the positions it saw, and what else it depended on
     rune::DeviceBuffer cand_keys;   // uint64 [N, cand_cap], sorted per centre
@@ -42,6 +47,7 @@ struct rune_nlist {
     rune::DeviceBuffer extent;   // bin frames and atom extents of open directions
     rune::DeviceBuffer keys;     // uint64 [N, max(max_radial, max_angular)] sorted per centre
     rune::DeviceBuffer pinned_dummy;
+    rune::PinnedWords readback;  // record total and flags of the last build
 };
 
 namespace rune {

@@ -5,14 +5,16 @@ an MI355X; run with ``-m gpu``).
 The reference's GPUMD evaluator keeps a candidate list at rc + 1 A and reuses
 it while every atom moved less than skin / 2 (rune/mobius/src/mobius.cu:241-271,
 :334-402).  Here reuse must be invisible: the records of every call are
-compared bit for bit with a fresh build on the same positions, and the model
-outputs through both lists must be identical.
+compared bit for bit with a fresh build on the same positions and with the
+oracle's canonical lists (``oracle/neighbors.py``), and the model outputs
+through both lists must be identical.
 """
 
 import numpy as np
 import pytest
 import torch
 
+from oracle import neighbors as ONB
 from rune_amd import workloads as W
 from tests.helpers import load_weights
 
@@ -45,6 +47,19 @@ def _assert_same_records(upd, ref):
     assert torch.equal(a["vec"].view(torch.int32), b["vec"].view(torch.int32))
 
 
+def _assert_matches_oracle(upd, pos, sp, cells, pbc):
+    """Records of every structure against the oracle's list, bit for bit."""
+    out = {k: v.cpu().numpy() for k, v in upd.export().items()}
+    for k in range(len(sp) - 1):
+        a, b = int(sp[k]), int(sp[k + 1])
+        ref = ONB.build(pos[a:b], cells[k], tuple(bool(x) for x in pbc[k]), RC_R, RC_A)
+        lo, hi = out["ptr"][a], out["ptr"][b]
+        np.testing.assert_array_equal(out["ptr"][a:b + 1] - lo, ref["ptr"])
+        np.testing.assert_array_equal(out["nbr"][lo:hi] - a, ref["neighbor"])
+        np.testing.assert_array_equal(out["shift"][lo:hi], ref["shift"])
+        np.testing.assert_array_equal(out["vec"][lo:hi, :3], ref["vec32"])
+
+
 @pytest.mark.parametrize("case", ["amorphous", "small_cells", "cluster"])
 def test_skin_reuse_matches_fresh_build(case):
     from rune_amd import _native as N
@@ -59,6 +74,7 @@ def test_skin_reuse_matches_fresh_build(case):
         searched.append(upd.update(t, sp, cells, pbc, RC_R, RC_A, LIMIT, LIMIT, SKIN))
         ref.build(t, sp, cells, pbc, RC_R, RC_A, LIMIT, LIMIT)
         _assert_same_records(upd, ref)
+        _assert_matches_oracle(upd, pos, sp, cells, pbc)
     print(case, "searched at steps", [k for k, s in enumerate(searched) if s], flush=True)
     # the first call searches; small moves reuse; the walk outgrows skin / 2
     assert searched[0] and not searched[1] and any(searched[2:])
@@ -67,6 +83,7 @@ def test_skin_reuse_matches_fresh_build(case):
     assert upd.update(t, sp, cells * 1.01, pbc, RC_R, RC_A, LIMIT, LIMIT, SKIN)
     ref.build(t, sp, cells * 1.01, pbc, RC_R, RC_A, LIMIT, LIMIT)
     _assert_same_records(upd, ref)
+    _assert_matches_oracle(upd, pos * 1.01, sp, cells * 1.01, pbc)
 
 
 def test_skin_reuse_reports_overflow_like_build():
