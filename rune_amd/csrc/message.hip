@@ -11,6 +11,7 @@
 #include <cmath>
 
 #include "message.hpp"
+#include "wave.hpp"
 
 namespace rune {
 namespace {
@@ -168,68 +169,123 @@ struct MpArgs {
     float cutoff;          // message_cutoff
 };
 
-__global__ void __launch_bounds__(kWave) k_mp_aggregate(MpArgs a) {
-    __shared__ float vsL[3 * 64];
-    const int i = blockIdx.x, lane = threadIdx.x;
+// Lane layout of the MP record loops: a wave walks one atom's records S at a
+// time, one record per slot of W = 64 / S lanes; lane sl of a slot owns the
+// hidden columns sl, sl + W, sl + 2W, ... (HM of them for H <= 256) and the
+// vector channels sl and sl + W.  Record metadata is read 64 records at a
+// time lane-parallel and handed to the slots by shuffles; the slots' partial
+// sums are folded in a fixed order at the end, so every output has one
+// writer and a fixed summation order.
+constexpr int kMpSlots = 4, kMpW = kWave / kMpSlots, kMpHM = 256 / kMpW;
+
+// Sigmoid of the group gate of hidden column c (fc folded in).  G <= W: lane
+// sl of the slot holds group sl's value and the column reads it by a shuffle
+// (executed by every lane); otherwise each column evaluates its own.
+__device__ inline float group_gate(float sg, const float *gl, int c, int gw, int G, int slot,
+                                   float fc) {
+    const float s = bcast(sg, slot * kMpW + min(c / gw, kMpW - 1));
+    return G <= kMpW ? s : sigm(gl[c / gw]) * fc;
+}
+
+// Scalar and vector messages of centre i (message.py:160-190): msg_i =
+// sum_e sig(g_e) fc_e V_j, vsum_i = sum_e sig(v_e) fc_e src_j u_e, then the
+// message RMS, the vector mix and its invariants.
+__global__ void __launch_bounds__(256) k_mp_aggregate(MpArgs a) {
+    __shared__ float vsL[4][64];
+    const int i = wave_atom(a.r);
+    if (i < 0) return;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+    const int slot = lane / kMpW, sl = lane - slot * kMpW;
     const int H = a.H, G = a.G, vc = a.vc, NG = a.NG, NP = a.NP, gw = H / G;
-    float acc[4] = {0, 0, 0, 0};      // channels lane + 64*k, H <= 256
-    float vsl = 0.0f;                 // lane = 3*k + x < 3*vc
+    float acc[kMpHM], vx[2], vy[2], vz[2];
+    zero(acc);
+    zero(vx);
+    zero(vy);
+    zero(vz);
     const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
-    for (int e = rb; e < re; ++e) {
-        float fc = a.fc[e];
-        if (fc == 0.0f) continue;
-        int j = a.r.nbr[e];
-        const float *gl = a.gv + size_t(e) * NG;
-        const float *vj = a.vs + size_t(j) * NP;
+    for (int b0 = rb; b0 < re; b0 += kWave) {
+        const int cnt = min(kWave, re - b0);
+        const int ml = min(lane, cnt - 1);
+        const float mf = lane < cnt ? a.fc[b0 + ml] : 0.0f;
+        const int mj = a.r.nbr[b0 + ml];
+        const float4 mv = a.r.vec[b0 + ml];
+        for (int q0 = 0; q0 < cnt; q0 += kMpSlots) {
+            const int q = min(q0 + slot, cnt - 1);
+            const float fq = bcast(mf, q);   // every lane joins the shuffle
+            const float fc = q0 + slot < cnt ? fq : 0.0f;
+            const int j = bcast(mj, q), e = b0 + q;
+            const float *gl = a.gv + size_t(e) * NG;
+            const float *vj = a.vs + size_t(j) * NP;
+            const float sg = sl < G ? sigm(gl[sl]) * fc : 0.0f;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            int c = lane + kWave * k;
-            if (c < H) acc[k] += sigm(gl[c / gw]) * fc * vj[c];
-        }
-        if (lane < 3 * vc) {
-            int k = lane / 3, x = lane - 3 * k;
-            float4 v = a.r.vec[e];
-            float inv = 1.0f / fmaxf(v.w, 1.0e-12f);
-            float u = (x == 0 ? v.x : (x == 1 ? v.y : v.z)) * inv;
-            vsl += sigm(gl[G + k]) * fc * vj[H + k] * u;
+            for (int u = 0; u < kMpHM; ++u) {
+                const int c = sl + kMpW * u;
+                const float gate = group_gate(sg, gl, min(c, H - 1), gw, G, slot, fc);
+                if (c < H) acc[u] += gate * vj[c];
+            }
+            const float ux = bcast(mv.x, q), uy = bcast(mv.y, q), uz = bcast(mv.z, q);
+            const float inv = 1.0f / fmaxf(bcast(mv.w, q), 1.0e-12f);
+#pragma unroll
+            for (int v = 0; v < 2; ++v) {
+                const int k = sl + kMpW * v;
+                if (k < vc) {
+                    const float w = sigm(gl[G + k]) * fc * vj[H + k];
+                    vx[v] += w * (ux * inv);
+                    vy[v] += w * (uy * inv);
+                    vz[v] += w * (uz * inv);
+                }
+            }
         }
     }
+    fold_slots<kMpSlots>(acc);
+    fold_slots<kMpSlots>(vx);
+    fold_slots<kMpSlots>(vy);
+    fold_slots<kMpSlots>(vz);
     float ss = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        int c = lane + kWave * k;
-        if (c < H) {
-            a.msg[size_t(i) * H + c] = acc[k];
-            ss += acc[k] * acc[k];
+    for (int u = 0; u < kMpHM; ++u)
+        if (sl + kMpW * u < H) ss += acc[u] * acc[u];
+    ss = group_sum(ss, kMpW);
+    const float r = 1.0f / sqrtf(ss / float(H) + a.eps);
+    const int ldu = H + vc;
+    if (slot == 0) {
+        if (sl == 0) a.rm[i] = r;
+#pragma unroll
+        for (int u = 0; u < kMpHM; ++u) {
+            const int c = sl + kMpW * u;
+            if (c < H) {
+                a.msg[size_t(i) * H + c] = acc[u];
+                a.uin[size_t(i) * ldu + c] = acc[u] * r;
+            }
         }
     }
-    ss = wave_sum(ss);
-    float r = 1.0f / sqrtf(ss / float(H) + a.eps);
-    if (lane == 0) a.rm[i] = r;
-    const int ldu = H + vc;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        int c = lane + kWave * k;
-        if (c < H) a.uin[size_t(i) * ldu + c] = acc[k] * r;
-    }
     if (vc == 0) return;
-    if (lane < 3 * vc) {
-        vsL[lane] = vsl;
-        a.vsum[size_t(i) * 3 * vc + lane] = vsl;
+    float *vs = vsL[wave];
+    if (slot == 0) {
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+            const int k = sl + kMpW * v;
+            if (k < vc) {
+                vs[3 * k] = vx[v];
+                vs[3 * k + 1] = vy[v];
+                vs[3 * k + 2] = vz[v];
+            }
+        }
     }
-    __syncthreads();
+    wave_sync();
     float mx = 0.0f;
     if (lane < 3 * vc) {
-        int k = lane / 3, x = lane - 3 * k;
-        for (int kk = 0; kk < vc; ++kk) mx += a.vmix[k * vc + kk] * vsL[3 * kk + x];
+        a.vsum[size_t(i) * 3 * vc + lane] = vs[lane];
+        const int k = lane / 3, x = lane - 3 * k;
+        for (int kk = 0; kk < vc; ++kk) mx += a.vmix[k * vc + kk] * vs[3 * kk + x];
         a.mixed[size_t(i) * 3 * vc + lane] = mx;
     }
-    __syncthreads();
-    if (lane < 3 * vc) vsL[lane] = mx;
-    __syncthreads();
+    wave_sync();
+    if (lane < 3 * vc) vs[lane] = mx;
+    wave_sync();
     if (lane < vc) {
-        float t = vsL[3 * lane] * vsL[3 * lane] + vsL[3 * lane + 1] * vsL[3 * lane + 1] +
-                  vsL[3 * lane + 2] * vsL[3 * lane + 2];
+        const float t = vs[3 * lane] * vs[3 * lane] + vs[3 * lane + 1] * vs[3 * lane + 1] +
+                        vs[3 * lane + 2] * vs[3 * lane + 2];
         a.uin[size_t(i) * ldu + H + lane] = t;
     }
 }
@@ -260,109 +316,444 @@ __global__ void __launch_bounds__(kWave) k_mp_node_backward(MpArgs a) {
     }
 }
 
-// Adjoint of the gates, fc and the unit vector for the records of centre i.
-__global__ void __launch_bounds__(kWave) k_mp_edge_backward(MpArgs a) {
+// Adjoint of the gates, fc and the unit vector for the records of centre i
+// (slot layout of k_mp_aggregate; the centre's dE/dmsg row and dE/dvsum stay
+// in registers).  Group sums P_g = sum_{c in g} dmsg_i[c] V_j[c] go through
+// the slot's LDS row.
+__global__ void __launch_bounds__(256) k_mp_edge_backward(MpArgs a) {
     extern __shared__ float lds[];
-    float *pL = lds;                 // [H]
-    float *dvsL = pL + a.H;          // [3*vc]
-    const int i = blockIdx.x, lane = threadIdx.x;
+    const int i = wave_atom(a.r);
+    if (i < 0) return;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+    const int slot = lane / kMpW, sl = lane - slot * kMpW;
     const int H = a.H, G = a.G, vc = a.vc, NG = a.NG, NP = a.NP, gw = H / G;
-    float dm[4];
+    float *pL = lds + (wave * kMpSlots + slot) * (H + 1);   // this slot's products
+    float dm[kMpHM], dvx[2], dvy[2], dvz[2];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        int c = lane + kWave * k;
-        dm[k] = c < H ? a.dmsg[size_t(i) * H + c] : 0.0f;
+    for (int u = 0; u < kMpHM; ++u) {
+        const int c = sl + kMpW * u;
+        dm[u] = c < H ? a.dmsg[size_t(i) * H + c] : 0.0f;
     }
-    if (lane < 3 * vc) dvsL[lane] = a.dvsum[size_t(i) * 3 * vc + lane];
-    __syncthreads();
-    const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
-    for (int e = rb; e < re; ++e) {
-        float fc = a.fc[e];
-        float *dg = a.dgv + size_t(e) * NG;
-        if (fc == 0.0f) {
-            for (int c = lane; c < NG; c += kWave) dg[c] = 0.0f;
-            continue;
-        }
-        int j = a.r.nbr[e];
-        const float *gl = a.gv + size_t(e) * NG;
-        const float *vj = a.vs + size_t(j) * NP;
+    zero(dvx);
+    zero(dvy);
+    zero(dvz);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            int c = lane + kWave * k;
-            if (c < H) pL[c] = dm[k] * vj[c];
+    for (int v = 0; v < 2; ++v) {
+        const int k = sl + kMpW * v;
+        if (k < vc) {
+            const float *d = a.dvsum + size_t(i) * 3 * vc + 3 * k;
+            dvx[v] = d[0];
+            dvy[v] = d[1];
+            dvz[v] = d[2];
         }
-        __syncthreads();
-        float4 v = a.r.vec[e];
-        float d = v.w;
-        float inv = 1.0f / fmaxf(d, 1.0e-12f);
-        float u[3] = {v.x * inv, v.y * inv, v.z * inv};
-        float contrib = 0.0f, dux = 0.0f, duy = 0.0f, duz = 0.0f;
-        if (lane < G) {
-            float P = 0.0f;
-            for (int c = lane * gw; c < (lane + 1) * gw; ++c) P += pL[c];
-            float s = sigm(gl[lane]);
-            dg[lane] = P * fc * s * (1.0f - s);
-            contrib = P * s;
-        } else if (lane < G + vc) {
-            int k = lane - G;
-            float ak = dvsL[3 * k] * u[0] + dvsL[3 * k + 1] * u[1] + dvsL[3 * k + 2] * u[2];
-            float src = vj[H + k];
-            float vg = sigm(gl[G + k]);
-            dg[G + k] = ak * src * fc * vg * (1.0f - vg);
-            contrib = ak * src * vg;
-            float w = vg * fc * src;
-            dux = w * dvsL[3 * k];
-            duy = w * dvsL[3 * k + 1];
-            duz = w * dvsL[3 * k + 2];
+    }
+    const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
+    for (int b0 = rb; b0 < re; b0 += kWave) {
+        const int cnt = min(kWave, re - b0);
+        const int ml = min(lane, cnt - 1);
+        const float mf = a.fc[b0 + ml];
+        const int mj = a.r.nbr[b0 + ml];
+        const float4 mv = a.r.vec[b0 + ml];
+        for (int q0 = 0; q0 < cnt; q0 += kMpSlots) {
+            const bool live = q0 + slot < cnt;
+            const int q = min(q0 + slot, cnt - 1);
+            const float fc = bcast(mf, q);
+            const int j = bcast(mj, q), e = b0 + q;
+            const float4 v = make_float4(bcast(mv.x, q), bcast(mv.y, q), bcast(mv.z, q),
+                                         bcast(mv.w, q));
+            const float *gl = a.gv + size_t(e) * NG;
+            const float *vj = a.vs + size_t(j) * NP;
+            const bool on = live && fc != 0.0f;
+            if (on) {
+#pragma unroll
+                for (int u = 0; u < kMpHM; ++u) {
+                    const int c = sl + kMpW * u;
+                    if (c < H) pL[c] = dm[u] * vj[c];
+                }
+            }
+            wave_sync();
+            const float inv = 1.0f / fmaxf(v.w, 1.0e-12f);
+            const float u0 = v.x * inv, u1 = v.y * inv, u2 = v.z * inv;
+            float contrib = 0.0f, dux = 0.0f, duy = 0.0f, duz = 0.0f;
+            float *dg = a.dgv + size_t(e) * NG;
+            for (int g = sl; g < G; g += kMpW) {
+                float P = 0.0f;
+                for (int c = g * gw; c < (g + 1) * gw; ++c) P += pL[c];
+                const float sg = sigm(gl[g]);
+                if (live) dg[g] = on ? P * fc * sg * (1.0f - sg) : 0.0f;
+                contrib += on ? P * sg : 0.0f;
+            }
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                const int k = sl + kMpW * w;
+                if (k < vc) {
+                    const float ak = dvx[w] * u0 + dvy[w] * u1 + dvz[w] * u2;
+                    const float src = vj[H + k];
+                    const float vg = sigm(gl[G + k]);
+                    if (live) dg[G + k] = on ? ak * src * fc * vg * (1.0f - vg) : 0.0f;
+                    if (on) {
+                        contrib += ak * src * vg;
+                        const float wt = vg * fc * src;
+                        dux += wt * dvx[w];
+                        duy += wt * dvy[w];
+                        duz += wt * dvz[w];
+                    }
+                }
+            }
+            contrib = group_sum(contrib, kMpW);
+            dux = group_sum(dux, kMpW);
+            duy = group_sum(duy, kMpW);
+            duz = group_sum(duz, kMpW);
+            if (on && sl == 0) {
+                const float fcp = -0.5f * kPi / a.cutoff * sinf(kPi * v.w / a.cutoff);
+                float4 acc = a.dv[e];
+                acc.x += dux;
+                acc.y += duy;
+                acc.z += duz;
+                acc.w += contrib * fcp;
+                a.dv[e] = acc;
+            }
+            wave_sync();
         }
-        contrib = wave_sum(contrib);
-        dux = wave_sum(dux);
-        duy = wave_sum(duy);
-        duz = wave_sum(duz);
-        if (lane == 0) {
-            float fcp = -0.5f * kPi / a.cutoff * sinf(kPi * d / a.cutoff);
-            float4 acc = a.dv[e];
-            acc.x += dux;
-            acc.y += duy;
-            acc.z += duz;
-            acc.w += contrib * fcp;
-            a.dv[e] = acc;
-        }
-        __syncthreads();
     }
 }
 
-// Adjoint of the gathered neighbour rows (values | vector source) of atom j.
-__global__ void __launch_bounds__(kWave) k_mp_neighbor_backward(MpArgs a) {
-    const int j = blockIdx.x, lane = threadIdx.x;
+// Adjoint of the gathered neighbour rows (values | vector source) of atom j,
+// walking the records whose neighbour is j (slot layout of k_mp_aggregate).
+__global__ void __launch_bounds__(256) k_mp_neighbor_backward(MpArgs a) {
+    const int j = wave_atom(a.r);
+    if (j < 0) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int slot = lane / kMpW, sl = lane - slot * kMpW;
     const int H = a.H, G = a.G, vc = a.vc, NG = a.NG, NP = a.NP, gw = H / G;
-    float acc[4] = {0, 0, 0, 0};
-    float av = 0.0f;
-    for (int t = a.r.tptr[j]; t < a.r.tptr[j + 1]; ++t) {
-        int e = a.r.tidx[t];
-        float fc = a.fc[e];
-        if (fc == 0.0f) continue;
-        int i = a.r.ctr[e];
-        const float *gl = a.gv + size_t(e) * NG;
+    float acc[kMpHM], av[2];
+    zero(acc);
+    zero(av);
+    const int tb = a.r.tptr[j], te = a.r.tptr[j + 1];
+    for (int t0 = tb; t0 < te; t0 += kWave) {
+        const int cnt = min(kWave, te - t0);
+        const int ml = min(lane, cnt - 1);
+        const int me = a.r.tidx[t0 + ml];
+        const int mi = a.r.tctr[t0 + ml];
+        const float mf = lane < cnt ? a.fc[me] : 0.0f;
+        const float4 mv = a.r.vec[me];
+        for (int q0 = 0; q0 < cnt; q0 += kMpSlots) {
+            const int q = min(q0 + slot, cnt - 1);
+            const float fq = bcast(mf, q);   // every lane joins the shuffle
+            const float fc = q0 + slot < cnt ? fq : 0.0f;
+            const int e = bcast(me, q), i = bcast(mi, q);
+            const float *gl = a.gv + size_t(e) * NG;
+            const float *dmi = a.dmsg + size_t(i) * H;
+            const float sg = sl < G ? sigm(gl[sl]) * fc : 0.0f;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            int c = lane + kWave * k;
-            if (c < H) acc[k] += sigm(gl[c / gw]) * fc * a.dmsg[size_t(i) * H + c];
-        }
-        if (lane < vc) {
-            float4 v = a.r.vec[e];
-            float inv = 1.0f / fmaxf(v.w, 1.0e-12f);
-            const float *dvs = a.dvsum + size_t(i) * 3 * vc + 3 * lane;
-            float ak = (dvs[0] * v.x + dvs[1] * v.y + dvs[2] * v.z) * inv;
-            av += sigm(gl[G + lane]) * fc * ak;
+            for (int u = 0; u < kMpHM; ++u) {
+                const int c = sl + kMpW * u;
+                const float gate = group_gate(sg, gl, min(c, H - 1), gw, G, slot, fc);
+                if (c < H) acc[u] += gate * dmi[c];
+            }
+            const float inv = 1.0f / fmaxf(bcast(mv.w, q), 1.0e-12f);
+            const float vx = bcast(mv.x, q), vy = bcast(mv.y, q), vz = bcast(mv.z, q);
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                const int k = sl + kMpW * w;
+                if (k < vc) {
+                    const float *dvs = a.dvsum + size_t(i) * 3 * vc + 3 * k;
+                    const float ak = (dvs[0] * vx + dvs[1] * vy + dvs[2] * vz) * inv;
+                    av[w] += sigm(gl[G + k]) * fc * ak;
+                }
+            }
         }
     }
+    fold_slots<kMpSlots>(acc);
+    fold_slots<kMpSlots>(av);
+    if (slot != 0) return;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        int c = lane + kWave * k;
-        if (c < H) a.dvs[size_t(j) * NP + c] = acc[k];
+    for (int u = 0; u < kMpHM; ++u) {
+        const int c = sl + kMpW * u;
+        if (c < H) a.dvs[size_t(j) * NP + c] = acc[u];
     }
-    if (lane < vc) a.dvs[size_t(j) * NP + H + lane] = av;
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        const int k = sl + kMpW * w;
+        if (k < vc) a.dvs[size_t(j) * NP + H + k] = av[w];
+    }
+}
+
+// ---- MP record kernels, contiguous-column layout ----
+// Same slots as above, but lane sl of a slot owns the CH = H / 16 contiguous
+// hidden columns sl*CH .. sl*CH + CH - 1, all inside one message group (taken
+// when the group width is a multiple of CH, CH divides the rows' 16-byte
+// alignment and gw / CH is a power of two): each record then costs a lane one
+// gate load and sigmoid and CH/4 vector loads, and the group sums of the
+// reverse pass are lane-group sums with no LDS.
+
+template <int CH>
+__device__ inline void load_cols(float (&v)[CH], const float *__restrict__ p) {
+#pragma unroll
+    for (int q = 0; q < CH / 4; ++q) {
+        const float4 t = reinterpret_cast<const float4 *>(p)[q];
+        v[4 * q] = t.x;
+        v[4 * q + 1] = t.y;
+        v[4 * q + 2] = t.z;
+        v[4 * q + 3] = t.w;
+    }
+}
+
+template <int CH>
+__device__ inline void store_cols(const float (&v)[CH], float *__restrict__ p) {
+#pragma unroll
+    for (int q = 0; q < CH / 4; ++q)
+        reinterpret_cast<float4 *>(p)[q] =
+            make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+}
+
+template <int CH>
+__global__ void __launch_bounds__(256) k_mp_aggregate_c(MpArgs a) {
+    __shared__ float vsL[4][64];
+    const int i = wave_atom(a.r);
+    if (i < 0) return;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+    const int slot = lane / kMpW, sl = lane - slot * kMpW;
+    const int H = a.H, G = a.G, vc = a.vc, NG = a.NG, NP = a.NP, gw = H / G;
+    const int c0 = sl * CH, g = c0 / gw;
+    float acc[CH], vx[2], vy[2], vz[2];
+    zero(acc);
+    zero(vx);
+    zero(vy);
+    zero(vz);
+    const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
+    for (int b0 = rb; b0 < re; b0 += kWave) {
+        const int cnt = min(kWave, re - b0);
+        const int ml = min(lane, cnt - 1);
+        const float mf = lane < cnt ? a.fc[b0 + ml] : 0.0f;
+        const int mj = a.r.nbr[b0 + ml];
+        const float4 mv = a.r.vec[b0 + ml];
+#pragma unroll 2
+        for (int q0 = 0; q0 < cnt; q0 += kMpSlots) {
+            const int q = min(q0 + slot, cnt - 1);
+            const float fq = bcast(mf, q);   // every lane joins the shuffle
+            const float fc = q0 + slot < cnt ? fq : 0.0f;
+            const int j = bcast(mj, q), e = b0 + q;
+            const float *gl = a.gv + size_t(e) * NG;
+            const float *vj = a.vs + size_t(j) * NP;
+            float val[CH];
+            load_cols(val, vj + c0);
+            const float sg = sigm(gl[g]) * fc;
+#pragma unroll
+            for (int t = 0; t < CH; ++t) acc[t] += sg * val[t];
+            const float ux = bcast(mv.x, q), uy = bcast(mv.y, q), uz = bcast(mv.z, q);
+            const float inv = 1.0f / fmaxf(bcast(mv.w, q), 1.0e-12f);
+#pragma unroll
+            for (int v = 0; v < 2; ++v) {
+                const int k = sl + kMpW * v;
+                if (k < vc) {
+                    const float w = sigm(gl[G + k]) * fc * vj[H + k];
+                    vx[v] += w * (ux * inv);
+                    vy[v] += w * (uy * inv);
+                    vz[v] += w * (uz * inv);
+                }
+            }
+        }
+    }
+    fold_slots<kMpSlots>(acc);
+    fold_slots<kMpSlots>(vx);
+    fold_slots<kMpSlots>(vy);
+    fold_slots<kMpSlots>(vz);
+    float ss = 0.0f;
+#pragma unroll
+    for (int t = 0; t < CH; ++t) ss += acc[t] * acc[t];
+    ss = group_sum(ss, kMpW);
+    const float r = 1.0f / sqrtf(ss / float(H) + a.eps);
+    const int ldu = H + vc;
+    if (slot == 0) {
+        if (sl == 0) a.rm[i] = r;
+        store_cols(acc, a.msg + size_t(i) * H + c0);
+#pragma unroll
+        for (int t = 0; t < CH; ++t) a.uin[size_t(i) * ldu + c0 + t] = acc[t] * r;
+    }
+    if (vc == 0) return;
+    float *vs = vsL[wave];
+    if (slot == 0) {
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+            const int k = sl + kMpW * v;
+            if (k < vc) {
+                vs[3 * k] = vx[v];
+                vs[3 * k + 1] = vy[v];
+                vs[3 * k + 2] = vz[v];
+            }
+        }
+    }
+    wave_sync();
+    float mx = 0.0f;
+    if (lane < 3 * vc) {
+        a.vsum[size_t(i) * 3 * vc + lane] = vs[lane];
+        const int k = lane / 3, x = lane - 3 * k;
+        for (int kk = 0; kk < vc; ++kk) mx += a.vmix[k * vc + kk] * vs[3 * kk + x];
+        a.mixed[size_t(i) * 3 * vc + lane] = mx;
+    }
+    wave_sync();
+    if (lane < 3 * vc) vs[lane] = mx;
+    wave_sync();
+    if (lane < vc) {
+        const float t = vs[3 * lane] * vs[3 * lane] + vs[3 * lane + 1] * vs[3 * lane + 1] +
+                        vs[3 * lane + 2] * vs[3 * lane + 2];
+        a.uin[size_t(i) * ldu + H + lane] = t;
+    }
+}
+
+template <int CH>
+__global__ void __launch_bounds__(256) k_mp_edge_backward_c(MpArgs a) {
+    const int i = wave_atom(a.r);
+    if (i < 0) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int slot = lane / kMpW, sl = lane - slot * kMpW;
+    const int H = a.H, G = a.G, vc = a.vc, NG = a.NG, NP = a.NP, gw = H / G;
+    const int c0 = sl * CH, g = c0 / gw, lg = gw / CH;   // lg lanes per group
+    const bool lead = sl % lg == 0;
+    float dm[CH], dvx[2], dvy[2], dvz[2];
+    load_cols(dm, a.dmsg + size_t(i) * H + c0);
+    zero(dvx);
+    zero(dvy);
+    zero(dvz);
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+        const int k = sl + kMpW * v;
+        if (k < vc) {
+            const float *d = a.dvsum + size_t(i) * 3 * vc + 3 * k;
+            dvx[v] = d[0];
+            dvy[v] = d[1];
+            dvz[v] = d[2];
+        }
+    }
+    const int rb = a.r.view[4 * i], re = a.r.view[4 * i + 1];
+    for (int b0 = rb; b0 < re; b0 += kWave) {
+        const int cnt = min(kWave, re - b0);
+        const int ml = min(lane, cnt - 1);
+        const float mf = a.fc[b0 + ml];
+        const int mj = a.r.nbr[b0 + ml];
+        const float4 mv = a.r.vec[b0 + ml];
+#pragma unroll 2
+        for (int q0 = 0; q0 < cnt; q0 += kMpSlots) {
+            const bool live = q0 + slot < cnt;
+            const int q = min(q0 + slot, cnt - 1);
+            const float fc = bcast(mf, q);
+            const int j = bcast(mj, q), e = b0 + q;
+            const float4 v = make_float4(bcast(mv.x, q), bcast(mv.y, q), bcast(mv.z, q),
+                                         bcast(mv.w, q));
+            const float *gl = a.gv + size_t(e) * NG;
+            const float *vj = a.vs + size_t(j) * NP;
+            const bool on = live && fc != 0.0f;
+            float val[CH];
+            load_cols(val, vj + c0);
+            float P = 0.0f;
+#pragma unroll
+            for (int t = 0; t < CH; ++t) P += dm[t] * val[t];
+            P = group_sum(P, lg);
+            const float sg = sigm(gl[g]);
+            float *dg = a.dgv + size_t(e) * NG;
+            if (live && lead) dg[g] = on ? P * fc * sg * (1.0f - sg) : 0.0f;
+            float contrib = on && lead ? P * sg : 0.0f;
+            const float inv = 1.0f / fmaxf(v.w, 1.0e-12f);
+            const float u0 = v.x * inv, u1 = v.y * inv, u2 = v.z * inv;
+            float dux = 0.0f, duy = 0.0f, duz = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                const int k = sl + kMpW * w;
+                if (k < vc) {
+                    const float ak = dvx[w] * u0 + dvy[w] * u1 + dvz[w] * u2;
+                    const float src = vj[H + k];
+                    const float vg = sigm(gl[G + k]);
+                    if (live) dg[G + k] = on ? ak * src * fc * vg * (1.0f - vg) : 0.0f;
+                    if (on) {
+                        contrib += ak * src * vg;
+                        const float wt = vg * fc * src;
+                        dux += wt * dvx[w];
+                        duy += wt * dvy[w];
+                        duz += wt * dvz[w];
+                    }
+                }
+            }
+            contrib = group_sum(contrib, kMpW);
+            dux = group_sum(dux, kMpW);
+            duy = group_sum(duy, kMpW);
+            duz = group_sum(duz, kMpW);
+            if (on && sl == 0) {
+                const float fcp = -0.5f * kPi / a.cutoff * sinf(kPi * v.w / a.cutoff);
+                float4 acc = a.dv[e];
+                acc.x += dux;
+                acc.y += duy;
+                acc.z += duz;
+                acc.w += contrib * fcp;
+                a.dv[e] = acc;
+            }
+        }
+    }
+}
+
+template <int CH>
+__global__ void __launch_bounds__(256) k_mp_neighbor_backward_c(MpArgs a) {
+    const int j = wave_atom(a.r);
+    if (j < 0) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int slot = lane / kMpW, sl = lane - slot * kMpW;
+    const int H = a.H, G = a.G, vc = a.vc, NG = a.NG, NP = a.NP, gw = H / G;
+    const int c0 = sl * CH, g = c0 / gw;
+    float acc[CH], av[2];
+    zero(acc);
+    zero(av);
+    const int tb = a.r.tptr[j], te = a.r.tptr[j + 1];
+    for (int t0 = tb; t0 < te; t0 += kWave) {
+        const int cnt = min(kWave, te - t0);
+        const int ml = min(lane, cnt - 1);
+        const int me = a.r.tidx[t0 + ml];
+        const int mi = a.r.tctr[t0 + ml];
+        const float mf = lane < cnt ? a.fc[me] : 0.0f;
+        const float4 mv = a.r.vec[me];
+#pragma unroll 2
+        for (int q0 = 0; q0 < cnt; q0 += kMpSlots) {
+            const int q = min(q0 + slot, cnt - 1);
+            const float fq = bcast(mf, q);   // every lane joins the shuffle
+            const float fc = q0 + slot < cnt ? fq : 0.0f;
+            const int e = bcast(me, q), i = bcast(mi, q);
+            const float *gl = a.gv + size_t(e) * NG;
+            float dmi[CH];
+            load_cols(dmi, a.dmsg + size_t(i) * H + c0);
+            const float sg = sigm(gl[g]) * fc;
+#pragma unroll
+            for (int t = 0; t < CH; ++t) acc[t] += sg * dmi[t];
+            const float inv = 1.0f / fmaxf(bcast(mv.w, q), 1.0e-12f);
+            const float vx = bcast(mv.x, q), vy = bcast(mv.y, q), vz = bcast(mv.z, q);
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                const int k = sl + kMpW * w;
+                if (k < vc) {
+                    const float *dvs = a.dvsum + size_t(i) * 3 * vc + 3 * k;
+                    const float ak = (dvs[0] * vx + dvs[1] * vy + dvs[2] * vz) * inv;
+                    av[w] += sigm(gl[G + k]) * fc * ak;
+                }
+            }
+        }
+    }
+    fold_slots<kMpSlots>(acc);
+    fold_slots<kMpSlots>(av);
+    if (slot != 0) return;
+    store_cols(acc, a.dvs + size_t(j) * NP + c0);
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        const int k = sl + kMpW * w;
+        if (k < vc) a.dvs[size_t(j) * NP + H + k] = av[w];
+    }
+}
+
+// Columns per lane of the contiguous-column kernels for this model, or 0 when
+// the strided kernels are used.
+int mp_columns(int H, int G, int NP) {
+    if (H != 64 && H != 128 && H != 256) return 0;
+    const int ch = H / kMpW, gw = H / G;
+    if (gw % ch != 0 || NP % 4 != 0) return 0;
+    const int lg = gw / ch;
+    return (lg & (lg - 1)) == 0 ? ch : 0;
 }
 
 }  // namespace
@@ -729,7 +1120,13 @@ float *messages_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Recor
         MpArgs a = mp_args(m, p, r, b);
         {
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
-            hipLaunchKernelGGL(k_mp_aggregate, dim3(N), dim3(kWave), 0, s, a);
+            const dim3 grid(ceil_div(N, 4)), block(256);
+            switch (mp_columns(H, c.message_groups, w.NP)) {
+            case 4: hipLaunchKernelGGL(k_mp_aggregate_c<4>, grid, block, 0, s, a); break;
+            case 8: hipLaunchKernelGGL(k_mp_aggregate_c<8>, grid, block, 0, s, a); break;
+            case 16: hipLaunchKernelGGL(k_mp_aggregate_c<16>, grid, block, 0, s, a); break;
+            default: hipLaunchKernelGGL(k_mp_aggregate, grid, block, 0, s, a);
+            }
         }
         RUNE_HIP_CHECK(hipGetLastError());
         Epilogue e3;
@@ -771,14 +1168,28 @@ float *messages_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Reco
         gemm(N, w.NP, D, p.at(p.t_dz1), D, w.up1_fT, D, p.at(p.t_duin), w.NP, e1, s);
         MpArgs a = mp_args(m, p, r, b);
         hipLaunchKernelGGL(k_mp_node_backward, dim3(N), dim3(kWave), 0, s, a);
-        size_t lds = sizeof(float) * (H + 3 * std::max(c.vector_channels, 1));
+        const size_t lds = sizeof(float) * 4 * kMpSlots * (H + 1);
+        const dim3 grid(ceil_div(N, 4)), block(256);
+        const int ch = mp_columns(H, c.message_groups, w.NP);
         {
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
-            hipLaunchKernelGGL(k_mp_edge_backward, dim3(N), dim3(kWave), lds, s, a);
+            switch (ch) {
+            case 4: hipLaunchKernelGGL(k_mp_edge_backward_c<4>, grid, block, 0, s, a); break;
+            case 8: hipLaunchKernelGGL(k_mp_edge_backward_c<8>, grid, block, 0, s, a); break;
+            case 16: hipLaunchKernelGGL(k_mp_edge_backward_c<16>, grid, block, 0, s, a); break;
+            default: hipLaunchKernelGGL(k_mp_edge_backward, grid, block, lds, s, a);
+            }
         }
         {
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
-            hipLaunchKernelGGL(k_mp_neighbor_backward, dim3(N), dim3(kWave), 0, s, a);
+            switch (ch) {
+            case 4: hipLaunchKernelGGL(k_mp_neighbor_backward_c<4>, grid, block, 0, s, a); break;
+            case 8: hipLaunchKernelGGL(k_mp_neighbor_backward_c<8>, grid, block, 0, s, a); break;
+            case 16:
+                hipLaunchKernelGGL(k_mp_neighbor_backward_c<16>, grid, block, 0, s, a);
+                break;
+            default: hipLaunchKernelGGL(k_mp_neighbor_backward, grid, block, 0, s, a);
+            }
         }
         RUNE_HIP_CHECK(hipGetLastError());
         if (E > 0) {
