@@ -10,6 +10,7 @@
 // in a fixed order, so nothing uses floating-point atomics.
 #include <cmath>
 
+#include "activation.hpp"
 #include "message.hpp"
 #include "wave.hpp"
 
@@ -18,6 +19,7 @@ namespace {
 
 constexpr int kWave = 64;
 constexpr float kPi = 3.14159265358979323846f;
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
 __device__ inline float wave_sum(float v) {
 #pragma unroll
@@ -746,6 +748,291 @@ __global__ void __launch_bounds__(256) k_mp_neighbor_backward_c(MpArgs a) {
     }
 }
 
+// ---- MP edge MLP on the matrix cores, nothing per record but the gates ----
+// Forward, per 16-record tile and wave: u^T = W_rb rb^T + pair row (edge_mlp.0
+// with its bias folded into the pair table), h = act(u), gate logits
+// g^T = W_g h^T + b (message.py:108-111, :160, :178).  Reverse: u is formed
+// again, due^T = (W_g^T dgv^T) * act'(u^T) and drb^T = W_rb^T due^T.  With
+// v_mfma_f32_16x16x4f32 (lane l supplies A[l%16][k], B[k][l%16] for the k
+// its lane group l/16 feeds; accumulator v of lane l is C[4(l/16)+v][l%16])
+// the transposed products keep record r = l%16 in every lane's columns, so
+// the accumulator of one product is the B operand of the next (dimension
+// d = 16q + 4(l/16) + v of record r) and u, h and due never leave
+// registers.  Weights sit in LDS for the whole launch; waves stride over
+// the tiles.  This replaces the [E, D] pre-activation array and the three
+// per-record GEMMs that wrote and read it.
+struct MpEdgeArgs {
+    int64_t E;
+    const float *rb;       // [E, ldrb]
+    int ldrb, kb, KP;      // basis size, row stride of W_rb (= kb rounded to 4)
+    const int32_t *pair;   // [E]
+    const float *Wx;       // [D, KP]  edge_mlp.0 radial columns
+    const float *P;        // [T*T, D] pair rows (+ bias)
+    const float *Wg;       // [NG, D]  gate rows
+    const float *gb;       // [NG]
+    int D, NG, act;
+    float *gv;             // forward out [E, NG]
+    const float *dgv;      // reverse in  [E, NG]
+    float *drb;            // reverse out [E, ldrb], or null when dv takes its contraction
+    const float *fc;       // [E] cosine cutoff (0: record outside the message list)
+    const float4 *vec;     // [E] record vectors
+    float4 *dv;            // [E] dE/dd accumulated in .w (dv.w += sum_k drb_k f_k'(d))
+    float cutoff;          // message_cutoff
+};
+
+// Operands of one tile that come from memory, loaded one tile ahead: the
+// radial basis values this lane feeds (k = 4s + g) and the record's pair.
+constexpr int kMpKS = 8;   // KP <= 32
+struct MpTileIn {
+    float rb[kMpKS];
+    int pair;
+};
+
+__device__ inline void mp_tile_load(const MpEdgeArgs &a, int64_t e, int g, MpTileIn &in) {
+    const float *rbr = a.rb + size_t(e) * a.ldrb;
+#pragma unroll
+    for (int s = 0; s < kMpKS; ++s) in.rb[s] = 4 * s < a.KP ? rbr[4 * s + g] : 0.0f;
+    in.pair = a.pair[e];
+}
+
+// u^T of one tile: acc[q][v] = u[r][16q + 4g + v] (pair row and bias added).
+template <int DB>
+__device__ inline void mp_edge_u(const MpEdgeArgs &a, const float *Wx, const MpTileIn &in, int r,
+                                 int g, float (&acc)[DB][4]) {
+    const float *pr = a.P + size_t(in.pair) * a.D + 4 * g;
+    float4 pv[DB];
+#pragma unroll
+    for (int q = 0; q < DB; ++q) pv[q] = *reinterpret_cast<const float4 *>(pr + 16 * q);
+    floatx4_t m[DB];
+#pragma unroll
+    for (int q = 0; q < DB; ++q) m[q] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    // k-step s feeds k = 4s + g from every lane group
+#pragma unroll
+    for (int s = 0; s < kMpKS; ++s) {
+        if (4 * s >= a.KP) break;
+#pragma unroll
+        for (int q = 0; q < DB; ++q)
+            m[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(Wx[(16 * q + r) * a.KP + 4 * s + g],
+                                                        in.rb[s], m[q], 0, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < DB; ++q) {
+        acc[q][0] = m[q][0] + pv[q].x;
+        acc[q][1] = m[q][1] + pv[q].y;
+        acc[q][2] = m[q][2] + pv[q].z;
+        acc[q][3] = m[q][3] + pv[q].w;
+    }
+}
+
+template <int DB, int GB, int ACT>
+__global__ void __launch_bounds__(256) k_mp_edge_forward(MpEdgeArgs a) {
+    extern __shared__ float lds[];
+    float *Wx = lds;                      // [D][KP]
+    float *Wg = Wx + a.D * a.KP;          // [16 GB][D], zero rows past NG
+    for (int o = threadIdx.x; o < a.D * a.KP; o += 256) Wx[o] = a.Wx[o];
+    for (int o = threadIdx.x; o < 16 * GB * a.D; o += 256)
+        Wg[o] = o < a.NG * a.D ? a.Wg[o] : 0.0f;
+    __syncthreads();
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const int64_t tiles = (a.E + 15) / 16;
+    const int64_t waves = int64_t(gridDim.x) * 4;
+    int64_t t = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    MpTileIn in;
+    if (t < tiles) mp_tile_load(a, min(16 * t + r, a.E - 1), g, in);
+    for (; t < tiles; t += waves) {
+        const int64_t e = min(16 * t + r, a.E - 1);
+        float u[DB][4];
+        mp_edge_u<DB>(a, Wx, in, r, g, u);
+        if (t + waves < tiles) mp_tile_load(a, min(16 * (t + waves) + r, a.E - 1), g, in);
+#pragma unroll
+        for (int q = 0; q < DB; ++q)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) u[q][v] = act_f(ACT, u[q][v]);
+        // g^T[16 gb + 4g + v][r]: k-step (q, v) feeds d = 16q + 4g + v
+#pragma unroll
+        for (int b = 0; b < GB; ++b) {
+            floatx4_t m = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            const float *wr = Wg + (16 * b + r) * a.D + 4 * g;
+#pragma unroll
+            for (int q = 0; q < DB; ++q) {
+                const float4 w = *reinterpret_cast<const float4 *>(wr + 16 * q);
+                m = __builtin_amdgcn_mfma_f32_16x16x4f32(w.x, u[q][0], m, 0, 0, 0);
+                m = __builtin_amdgcn_mfma_f32_16x16x4f32(w.y, u[q][1], m, 0, 0, 0);
+                m = __builtin_amdgcn_mfma_f32_16x16x4f32(w.z, u[q][2], m, 0, 0, 0);
+                m = __builtin_amdgcn_mfma_f32_16x16x4f32(w.w, u[q][3], m, 0, 0, 0);
+            }
+            if (16 * t + r < a.E) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int o = 16 * b + 4 * g + v;
+                    if (o < a.NG) a.gv[size_t(e) * a.NG + o] = m[v] + a.gb[o];
+                }
+            }
+        }
+    }
+}
+
+template <int DB, int GB, int ACT>
+__global__ void __launch_bounds__(256) k_mp_edge_reverse(MpEdgeArgs a) {
+    extern __shared__ float lds[];
+    float *Wx = lds;                      // [D][KP]
+    float *WgT = Wx + a.D * a.KP;         // [D][16 GB], zero columns past NG
+    const int ng16 = 16 * GB;
+    for (int o = threadIdx.x; o < a.D * a.KP; o += 256) Wx[o] = a.Wx[o];
+    for (int o = threadIdx.x; o < a.D * ng16; o += 256) {
+        const int d = o / ng16, k = o - d * ng16;
+        WgT[o] = k < a.NG ? a.Wg[size_t(k) * a.D + d] : 0.0f;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const int64_t tiles = (a.E + 15) / 16;
+    const int64_t waves = int64_t(gridDim.x) * 4;
+    const int KBF = a.kb / 16, tail = a.kb - 16 * KBF;   // MFMA rows of drb, VALU rows
+    int64_t t = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    MpTileIn in;
+    float dgn[GB][4];
+    auto load_dg = [&](int64_t e) {
+        const float *dg = a.dgv + size_t(e) * a.NG;
+#pragma unroll
+        for (int b = 0; b < GB; ++b)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int o = 16 * b + 4 * s + g;
+                dgn[b][s] = o < a.NG ? dg[o] : 0.0f;
+            }
+    };
+    if (t < tiles) {
+        mp_tile_load(a, min(16 * t + r, a.E - 1), g, in);
+        load_dg(min(16 * t + r, a.E - 1));
+    }
+    for (; t < tiles; t += waves) {
+        const int64_t e = min(16 * t + r, a.E - 1);
+        float u[DB][4];
+        mp_edge_u<DB>(a, Wx, in, r, g, u);
+        float dgc[GB][4];
+#pragma unroll
+        for (int b = 0; b < GB; ++b)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) dgc[b][s] = dgn[b][s];
+        if (t + waves < tiles) {
+            const int64_t en = min(16 * (t + waves) + r, a.E - 1);
+            mp_tile_load(a, en, g, in);
+            load_dg(en);
+        }
+        // due^T[d][r] = sum_o W_g[o][d] dgv[r][o]: k-step s of block b feeds
+        // o = 16b + 4s + g
+        floatx4_t m[DB];
+#pragma unroll
+        for (int q = 0; q < DB; ++q) m[q] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int b = 0; b < GB; ++b)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int o = 16 * b + 4 * s + g;
+#pragma unroll
+                for (int q = 0; q < DB; ++q)
+                    m[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(WgT[(16 * q + r) * ng16 + o],
+                                                                dgc[b][s], m[q], 0, 0, 0);
+            }
+#pragma unroll
+        for (int q = 0; q < DB; ++q)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) u[q][v] = m[q][v] * act_d(ACT, u[q][v]);   // due
+        const bool live = 16 * t + r < a.E;
+        // drb^T[16p + 4g + v][r] = sum_d W_rb[d][k] due^T[d][r] for the full
+        // 16-row blocks (k-step (q, v), two accumulators), then the last
+        // kb % 16 rows as lane dot products summed over the four lane groups
+        float w[2][4];
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+            floatx4_t acc0 = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+            if (pb < KBF) {
+                const int k = 16 * pb + r;
+#pragma unroll
+                for (int q = 0; q < DB; ++q)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const float wa = Wx[(16 * q + 4 * g + v) * a.KP + k];
+                        if (q & 1)
+                            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(wa, u[q][v], acc1, 0, 0, 0);
+                        else
+                            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(wa, u[q][v], acc0, 0, 0, 0);
+                    }
+            }
+#pragma unroll
+            for (int v = 0; v < 4; ++v) w[pb][v] = acc0[v] + acc1[v];
+        }
+        float wt[4];   // tail rows k = 16 KBF + j, this lane's share over its d
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float sum = 0.0f;
+            if (j < tail) {
+#pragma unroll
+                for (int q = 0; q < DB; ++q)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        sum += Wx[(16 * q + 4 * g + v) * a.KP + 16 * KBF + j] * u[q][v];
+            }
+            sum += __shfl_xor(sum, 16, 64);
+            sum += __shfl_xor(sum, 32, 64);
+            wt[j] = sum;
+        }
+        if (!a.dv) {
+            if (live) {
+#pragma unroll
+                for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        if (pb < KBF) a.drb[size_t(e) * a.ldrb + 16 * pb + 4 * g + v] = w[pb][v];
+                if (g == 0)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (j < tail) a.drb[size_t(e) * a.ldrb + 16 * KBF + j] = wt[j];
+            }
+            continue;
+        }
+        // dE/dd += sum_k drb_k f_k'(d) (masked Chebyshev basis, message.py:108-110):
+        // each lane group adds its own k of the full blocks, lane group 0 the
+        // tail rows, then the four groups of record r are summed
+        const float d = a.vec[e].w, rc = a.cutoff;
+        const float f = 0.5f * cosf(kPi * d / rc) + 0.5f;
+        const float fp = -0.5f * kPi / rc * sinf(kPi * d / rc);
+        const float rs = d / rc - 1.0f;
+        const float x = 2.0f * rs * rs - 1.0f, dxdr = 4.0f * rs / rc;
+        float t2 = 1.0f, t1 = x, u2 = 1.0f, u1 = 2.0f * x;
+        float part = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 36; ++k) {   // 2 full blocks + 4 tail rows
+            if (k >= a.kb) continue;
+            float dk;
+            if (k == 0) {
+                dk = fp;
+            } else if (k == 1) {
+                dk = 0.5f * dxdr * f + 0.5f * (x + 1.0f) * fp;
+            } else {
+                const float tn = 2.0f * x * t1 - t2, un = 2.0f * x * u1 - u2;
+                dk = 0.5f * float(k) * u1 * dxdr * f + 0.5f * (tn + 1.0f) * fp;
+                t2 = t1;
+                t1 = tn;
+                u2 = u1;
+                u1 = un;
+            }
+            if (k < 32) {
+                const int pb = k >> 4;
+                if (pb < KBF && ((k >> 2) & 3) == g) part += w[pb][k & 3] * dk;
+            }
+            if (k >= 16 * KBF && k < 16 * KBF + 4 && g == 0) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (k == 16 * KBF + j) part += wt[j] * dk;
+            }
+        }
+        part += __shfl_xor(part, 16, 64);
+        part += __shfl_xor(part, 32, 64);
+        if (live && g == 0 && a.fc[e] != 0.0f) a.dv[e].w += part;
+    }
+}
+
 // Columns per lane of the contiguous-column kernels for this model, or 0 when
 // the strided kernels are used.
 int mp_columns(int H, int G, int NP) {
@@ -754,6 +1041,40 @@ int mp_columns(int H, int G, int NP) {
     if (gw % ch != 0 || NP % 4 != 0) return 0;
     const int lg = gw / ch;
     return (lg & (lg - 1)) == 0 ? ch : 0;
+}
+
+// Launch of the fused MP edge MLP (forward or reverse), or false when the
+// model's widths have no instantiation (the per-record GEMMs are used then).
+bool mp_edge_fused(const MpEdgeArgs &a, bool reverse, hipStream_t s) {
+    const int DB = a.D / 16, GB = (a.NG + 15) / 16;
+    // drb rows: up to two 16-row blocks on the matrix cores plus four more
+    if (a.D % 16 != 0 || (DB != 2 && DB != 4 && DB != 6 && DB != 8) || GB > 2 || a.KP > 32 ||
+        a.kb - 16 * (a.kb / 16) > 4)
+        return false;
+    if (a.E == 0) return true;
+    const size_t lds = sizeof(float) * (size_t(a.D) * a.KP + size_t(16) * GB * a.D);
+    const int64_t tiles = (a.E + 15) / 16;
+    const dim3 grid(unsigned(std::min<int64_t>((tiles + 3) / 4, 2048))), block(256);
+#define MP_EDGE_ACT(K, D_, G_, A_)                                                   \
+    if (DB == D_ && GB == G_ && a.act == A_) {                                       \
+        hipLaunchKernelGGL((K<D_, G_, A_>), grid, block, lds, s, a);                 \
+        return true;                                                                 \
+    }
+#define MP_EDGE(K, D_, G_)                                                           \
+    MP_EDGE_ACT(K, D_, G_, RUNE_ACT_TANH)                                            \
+    MP_EDGE_ACT(K, D_, G_, RUNE_ACT_SILU) MP_EDGE_ACT(K, D_, G_, RUNE_ACT_GELU)
+#define MP_EDGE_ALL(K)                                                               \
+    MP_EDGE(K, 2, 1) MP_EDGE(K, 4, 1) MP_EDGE(K, 6, 1) MP_EDGE(K, 8, 1)              \
+    MP_EDGE(K, 2, 2) MP_EDGE(K, 4, 2) MP_EDGE(K, 6, 2) MP_EDGE(K, 8, 2)
+    if (reverse) {
+        MP_EDGE_ALL(k_mp_edge_reverse)
+    } else {
+        MP_EDGE_ALL(k_mp_edge_forward)
+    }
+#undef MP_EDGE_ALL
+#undef MP_EDGE
+#undef MP_EDGE_ACT
+    return false;
 }
 
 }  // namespace
@@ -1076,6 +1397,26 @@ static MpArgs mp_args(ModelImpl &m, MessagePlan &p, const Records &r, int b) {
     return a;
 }
 
+static MpEdgeArgs mp_edge_args(ModelImpl &m, MessagePlan &p, const MessageWeights &w,
+                               int64_t E) {
+    const rune_model_config &c = m.cfg;
+    MpEdgeArgs a{};
+    a.E = E;
+    a.rb = p.at(p.i_rb);
+    a.ldrb = p.ldrb;
+    a.kb = c.message_basis_size;
+    a.KP = w.ld_edge_x;
+    a.pair = reinterpret_cast<const int32_t *>(p.at(p.i_pair));
+    a.Wx = w.edge_x;
+    a.P = w.pair_proj;
+    a.Wg = w.gate;
+    a.gb = w.gate_b;
+    a.D = c.message_dim;
+    a.NG = w.NG;
+    a.act = c.activation;
+    return a;
+}
+
 float *messages_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Records &r,
                         const int32_t *types, const float *moments, float *h, hipStream_t s,
                         bool keep) {
@@ -1098,7 +1439,14 @@ float *messages_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Recor
         Epilogue e0;
         e0.row_scale = p.at(bb.rin);
         gemm(N, w.NP, H, cur, H, w.node_f, H, p.at(bb.vs), w.NP, e0, s);
+        bool fused = false;
         if (E > 0) {
+            Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
+            MpEdgeArgs ea = mp_edge_args(m, p, w, E);
+            ea.gv = p.at(bb.gv);
+            fused = mp_edge_fused(ea, false, s);
+        }
+        if (E > 0 && !fused) {
             Epilogue e1;
             e1.gtab[0] = w.pair_proj;
             e1.gidx[0] = reinterpret_cast<const int32_t *>(p.at(p.i_pair));
@@ -1193,20 +1541,35 @@ float *messages_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Reco
         }
         RUNE_HIP_CHECK(hipGetLastError());
         if (E > 0) {
-            Epilogue e2;
-            e2.dact_from = p.at(bb.ue);
-            e2.ldu = D;
-            e2.dact = act;
+            bool fused = false;
             {
                 Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
-                gemm(int(E), D, w.NG, p.at(p.t_dgv), w.NG, w.gate_T, w.NG, p.at(p.t_due), D, e2, s);
+                MpEdgeArgs ea = mp_edge_args(m, p, w, E);
+                ea.dgv = p.at(p.t_dgv);
+                ea.fc = p.at(p.i_fc);
+                ea.vec = r.vec;
+                ea.dv = reinterpret_cast<float4 *>(p.at(p.i_dv));
+                ea.cutoff = float(c.message_cutoff);
+                fused = mp_edge_fused(ea, true, s);
             }
-            Epilogue e3;
-            {
-                Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
-                gemm(int(E), w.KX, D, p.at(p.t_due), D, w.edge_xT, D, p.at(p.t_drb), p.ldrb, e3, s);
+            if (!fused) {
+                Epilogue e2;
+                e2.dact_from = p.at(bb.ue);
+                e2.ldu = D;
+                e2.dact = act;
+                {
+                    Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
+                    gemm(int(E), D, w.NG, p.at(p.t_dgv), w.NG, w.gate_T, w.NG, p.at(p.t_due), D,
+                         e2, s);
+                }
+                Epilogue e3;
+                {
+                    Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
+                    gemm(int(E), w.KX, D, p.at(p.t_due), D, w.edge_xT, D, p.at(p.t_drb), p.ldrb,
+                         e3, s);
+                }
             }
-            {
+            if (!fused) {   // the fused reverse adds this contraction itself
                 Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
                 edge_rb_backward(m, p, r, p.at(p.t_drb), p.ldrb, s);
             }
