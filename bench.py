@@ -149,8 +149,15 @@ def group_model(ev, prep, n_records, params):
             # edge reverse: gates, vec, fc, nbr, dv r/w; dgv out; dmsg, dvsum, values
             + E * (8 * NG + 16 + 8 + 32) + N * (4 * H + 12 * vc + 4 * NP)
             # neighbour reverse: gates, transpose, fc, vec; dmsg, dvsum; dvs out
-            + E * (4 * NG + 8 + 4 + 16) + N * (4 * H + 12 * vc + 4 * NP)
-            + rb_bwd)
+            + E * (4 * NG + 8 + 4 + 16) + N * (4 * H + 12 * vc + 4 * NP))
+        # the radial-basis reverse runs inside the fused edge-MLP reverse when
+        # the widths have an instantiation (D/16 in {2, 4, 6, 8}, <= 32 gates,
+        # basis rows <= 32, <= 4 rows past the last 16-row block)
+        kp = (kb + 3) // 4 * 4
+        fused = D % 16 == 0 and D // 16 in (2, 4, 6, 8) and NG <= 32 and kp <= 32 and \
+            kb - 16 * (kb // 16) <= 4
+        if not fused:
+            per_block += rb_bwd
         once = prep_bytes + direct
     return {"edge_gemm": ("mfma", flops), "edge_kernels": ("hbm", B * per_block + once)}
 

@@ -1045,12 +1045,18 @@ int mp_columns(int H, int G, int NP) {
 
 // Launch of the fused MP edge MLP (forward or reverse), or false when the
 // model's widths have no instantiation (the per-record GEMMs are used then).
+// Widths the fused kernels are instantiated for: D in {32, 64, 96, 128},
+// at most 32 gates, basis rows padded to at most 32 and at most four rows past
+// the last full 16-row block of drb.
+bool mp_edge_fusable(int D, int NG, int kb) {
+    const int DB = D / 16, KP = (kb + 3) & ~3;
+    return D % 16 == 0 && (DB == 2 || DB == 4 || DB == 6 || DB == 8) && NG <= 32 && KP <= 32 &&
+           kb - 16 * (kb / 16) <= 4;
+}
+
 bool mp_edge_fused(const MpEdgeArgs &a, bool reverse, hipStream_t s) {
     const int DB = a.D / 16, GB = (a.NG + 15) / 16;
-    // drb rows: up to two 16-row blocks on the matrix cores plus four more
-    if (a.D % 16 != 0 || (DB != 2 && DB != 4 && DB != 6 && DB != 8) || GB > 2 || a.KP > 32 ||
-        a.kb - 16 * (a.kb / 16) > 4)
-        return false;
+    if (!mp_edge_fusable(a.D, a.NG, a.kb)) return false;
     if (a.E == 0) return true;
     const size_t lds = sizeof(float) * (size_t(a.D) * a.KP + size_t(16) * GB * a.D);
     const int64_t tiles = (a.E + 15) / 16;
@@ -1285,12 +1291,14 @@ MessagePlan plan_messages(ModelImpl &m, Arena &ar, int N, int64_t E) {
     p.i_fc = p.add(ar, 4 * e);
     p.i_pair = p.add(ar, 4 * e);
     p.i_dv = p.add(ar, 16 * e);
+    // the fused edge MLP keeps pre-activations and their adjoints in registers
+    const size_t ed = mp_edge_fusable(D, NG, c.message_basis_size) ? 1 : e;
     for (int b = 0; b < L; ++b) {
         BlockBuffers bb;
         bb.h_out = p.add(ar, 4 * n * H);
         bb.rin = p.add(ar, 4 * n);
         bb.vs = p.add(ar, 4 * n * NP);
-        bb.ue = p.add(ar, 4 * e * D);
+        bb.ue = p.add(ar, 4 * ed * D);
         bb.gv = p.add(ar, 4 * e * NG);
         bb.msg = p.add(ar, 4 * n * H);
         bb.rm = p.add(ar, 4 * n);
@@ -1306,8 +1314,8 @@ MessagePlan plan_messages(ModelImpl &m, Arena &ar, int N, int64_t E) {
     p.t_dmsg = p.add(ar, 4 * n * H);
     p.t_dvsum = p.add(ar, 4 * n * 3 * std::max(vc, 1));
     p.t_dgv = p.add(ar, 4 * e * NG);
-    p.t_due = p.add(ar, 4 * e * D);
-    p.t_drb = p.add(ar, 4 * e * p.ldrb);
+    p.t_due = p.add(ar, 4 * ed * D);
+    p.t_drb = p.add(ar, 4 * ed * p.ldrb);
     p.t_dvs = p.add(ar, 4 * n * NP);
     p.t_dz = p.add(ar, 4 * n * H);
     p.t_dh0 = p.add(ar, 4 * n * H);

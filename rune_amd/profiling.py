@@ -30,7 +30,10 @@ COPY_KERNEL = "__amd_rocclr_copyBuffer"
 EDGE_KERNELS = ("k_eq_edge_nbr", "k_eq_edge_centre", "k_eq_aggregate", "k_eq_pair_dir",
                 "k_eq_pair_grp", "k_eq_pair_grp_c", "k_eq_edge_adj", "k_eq_harmonic_backward", "k_edge_prep",
                 "k_gather_f", "k_edge_rb_backward", "k_edge_direct", "k_mp_aggregate",
-                "k_mp_edge_backward", "k_mp_neighbor_backward")
+                "k_mp_edge_backward", "k_mp_neighbor_backward", "k_mp_aggregate_c",
+                "k_mp_edge_backward_c", "k_mp_neighbor_backward_c")
+# fused per-record MLP kernels (bench.py "edge_gemm", with the per-record GEMMs)
+EDGE_GEMM_KERNELS = ("k_mp_edge_forward", "k_mp_edge_reverse")
 
 
 def short_name(name):
@@ -45,6 +48,8 @@ def group_of(name, grid_threads, records):
     """bench.py group of one dispatch: GEMMs over at least `records` rows
     (64-row tiles of 256 threads) are per-record GEMMs."""
     base = short_name(name)
+    if any(base == k or base.startswith(k + "<") for k in EDGE_GEMM_KERNELS):
+        return "edge_gemm"
     if base.startswith("k_gemm<"):
         return "edge_gemm" if grid_threads >= 256 * math.ceil(records / 64) else None
     for k in EDGE_KERNELS:
@@ -112,11 +117,16 @@ def traffic(fetch_dir, write_dir, records):
 
     ff, fw = calibration(fetch), calibration(write)
     groups = collections.defaultdict(lambda: [0.0, 0.0, 0])
+    kernels = collections.defaultdict(lambda: [0.0, 0.0, 0])
     for counts, slot in ((fetch, 0), (write, 1)):
         for name, grid, v in counts.values():
+            b = v * 1024.0 * (ff if slot == 0 else fw)
+            k = kernels[short_name(name)]
+            k[slot] += b
+            k[2] += slot == 0
             g = group_of(name, grid, records)
             if g:
-                groups[g][slot] += v * 1024.0 * (ff if slot == 0 else fw)
+                groups[g][slot] += b
                 if slot == 0:
                     groups[g][2] += 1
     out = {"copy_calibration": {"fetch_factor": round(ff, 4), "write_factor": round(fw, 4),
@@ -126,6 +136,12 @@ def traffic(fetch_dir, write_dir, records):
         out["groups"][g] = {"launches": n, "fetch_bytes_per_launch": int(fb / n),
                             "write_bytes_per_launch": int(wb / n),
                             "bytes_per_launch": int((fb + wb) / n)}
+    # every kernel moving at least 1 MB per launch, largest first
+    out["kernels"] = {}
+    for name, (fb, wb, n) in sorted(kernels.items(), key=lambda kv: -(kv[1][0] + kv[1][1])):
+        if n and (fb + wb) / n >= 1e6 and name != COPY_KERNEL:
+            out["kernels"][name] = {"launches": n, "fetch_bytes_per_launch": int(fb / n),
+                                    "write_bytes_per_launch": int(wb / n)}
     return out
 
 
