@@ -364,7 +364,7 @@ __global__ void __launch_bounds__(1024) k_check_types(int n, const int32_t *type
 }
 
 // Largest atom count checked by one block of k_check_types.
-constexpr int kTypeCheckOneBlock = 1 << 16;
+constexpr int kTypeCheckOneBlock = 8192;
 
 static Records records_of(const rune_nlist *nl) {
     Records r;
