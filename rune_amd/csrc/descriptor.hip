@@ -226,6 +226,10 @@ __device__ void invariant_gradient(const DescTables &t, const float *s, const fl
     }
 }
 
+// KR / KA: basis values of a lane's record, NR: radial channels, NO: moment
+// outputs per lane (register arrays sized for the model, so the compact
+// instantiation keeps occupancy up).
+template <int KR, int KA, int NR, int NO>
 __global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Records r,
                                                               const int32_t *types, float *q,
                                                               int ldq, float *moments) {
@@ -241,33 +245,32 @@ __global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Reco
     const int ab = r.view[4 * i + 2], ae = r.view[4 * i + 3];
 
     // radial channels
-    float qr[kMaxNr];
+    float qr[NR];
 #pragma unroll
-    for (int n = 0; n < kMaxNr; ++n) qr[n] = 0.0f;
+    for (int n = 0; n < NR; ++n) qr[n] = 0.0f;
     for (int e = rb + lane; e < re; e += kWave) {
         float4 v = r.vec[e];
         int tj = types[r.nbr[e]];
-        float f[kMaxKr] = {};
-        chebyshev<kMaxKr>(v.w, t.rc_r, t.kr, f);
+        float f[KR] = {};
+        chebyshev<KR>(v.w, t.rc_r, t.kr, f);
         const float *row = t.c_radial + size_t(ti * t.n_types + tj) * t.nr * t.kr4;
 #pragma unroll
-        for (int n = 0; n < kMaxNr; ++n) {
+        for (int n = 0; n < NR; ++n) {
             if (n >= t.nr) break;
-            qr[n] += row_dot<kMaxKr>(row + n * t.kr4, t.kr4, f);
+            qr[n] += row_dot<KR>(row + n * t.kr4, t.kr4, f);
         }
     }
 #pragma unroll
-    for (int n = 0; n < kMaxNr; ++n) {
+    for (int n = 0; n < NR; ++n) {
         if (n >= t.nr) break;
         float v = wave_sum(qr[n]);
         if (lane == 0) q[size_t(i) * ldq + n] = v;
     }
 
     // angular moments s[n][lm] = sum_e gn[e][n] b[e][lm]
-    constexpr int kMaxOut = (kMaxNa * kMaxLm + kWave - 1) / kWave;
-    float acc[kMaxOut];
+    float acc[NO];
 #pragma unroll
-    for (int j = 0; j < kMaxOut; ++j) acc[j] = 0.0f;
+    for (int j = 0; j < NO; ++j) acc[j] = 0.0f;
     for (int base = ab; base < ae; base += kWave) {
         int e = base + lane;
         float *gl = gnL + lane * (na + 1);
@@ -275,10 +278,10 @@ __global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Reco
         if (e < ae) {
             float4 v = r.vec[e];
             int tj = types[r.nbr[e]];
-            float f[kMaxKa] = {};
-            chebyshev<kMaxKa>(v.w, t.rc_a, t.ka, f);
+            float f[KA] = {};
+            chebyshev<KA>(v.w, t.rc_a, t.ka, f);
             const float *row = t.c_angular + size_t(ti * t.n_types + tj) * t.na * t.ka4;
-            for (int n = 0; n < na; ++n) gl[n] = row_dot<kMaxKa>(row + n * t.ka4, t.ka4, f);
+            for (int n = 0; n < na; ++n) gl[n] = row_dot<KA>(row + n * t.ka4, t.ka4, f);
             float inv = 1.0f / fmaxf(v.w, 1.0e-12f);
             const float ux = v.x * inv, uy = v.y * inv, uz = v.z * inv;
             int idx = 0;
@@ -303,7 +306,7 @@ __global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Reco
         __syncthreads();
         int cnt = min(kWave, ae - base);
 #pragma unroll
-        for (int j = 0; j < kMaxOut; ++j) {
+        for (int j = 0; j < NO; ++j) {
             int o = lane + kWave * j;
             if (o >= nout) break;
             int n = o / nlm, c = o - n * nlm;
@@ -314,7 +317,7 @@ __global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Reco
         __syncthreads();
     }
 #pragma unroll
-    for (int j = 0; j < kMaxOut; ++j) {
+    for (int j = 0; j < NO; ++j) {
         int o = lane + kWave * j;
         if (o >= nout) break;
         sL[o] = acc[j];
@@ -367,6 +370,7 @@ __device__ inline void zbl_pair(const ZblTables &z, int ti, int tj, float d, flo
     de = 0.5f * (dscr * cut + scr * dcut);
 }
 
+template <int KR, int KA, int NA>
 __global__ void __launch_bounds__(kWave) k_descriptor_reverse(
     DescTables t, ZblTables z, Records r, const int32_t *types, const float *dq, int ldq,
     const float *moments, const float *dmom, const float4 *g_direct, float *energies,
@@ -404,27 +408,27 @@ __global__ void __launch_bounds__(kWave) k_descriptor_reverse(
         bool in_r = e >= rb && e < re;
         bool in_a = e >= ab && e < ae;
         if (want_grad && in_r) {
-            float f[kMaxKr] = {}, fp[kMaxKr] = {};
-            chebyshev_d<kMaxKr>(d, t.rc_r, t.kr, f, fp);
+            float f[KR] = {}, fp[KR] = {};
+            chebyshev_d<KR>(d, t.rc_r, t.kr, f, fp);
             const float *row = t.c_radial + size_t(ti * t.n_types + tj) * t.nr * t.kr4;
             float gs = 0.0f;
-            for (int n = 0; n < t.nr; ++n) gs += dqL[n] * row_dot<kMaxKr>(row + n * t.kr4, t.kr4, fp);
+            for (int n = 0; n < t.nr; ++n) gs += dqL[n] * row_dot<KR>(row + n * t.kr4, t.kr4, fp);
             gx += gs * ux;
             gy += gs * uy;
             gz += gs * uz;
         }
         if (want_grad && in_a) {
-            float f[kMaxKa] = {}, fp[kMaxKa] = {};
-            chebyshev_d<kMaxKa>(d, t.rc_a, t.ka, f, fp);
+            float f[KA] = {}, fp[KA] = {};
+            chebyshev_d<KA>(d, t.rc_a, t.ka, f, fp);
             const float *row = t.c_angular + size_t(ti * t.n_types + tj) * t.na * t.ka4;
-            float gn[kMaxNa], gnp[kMaxNa];
+            float gn[NA], gnp[NA];
 #pragma unroll
-            for (int n = 0; n < kMaxNa; ++n) {
+            for (int n = 0; n < NA; ++n) {
                 float a = 0.0f, b = 0.0f;
                 if (n < na) {
                     const float4 *r4 = reinterpret_cast<const float4 *>(row + n * t.ka4);
 #pragma unroll
-                    for (int q = 0; q < kMaxKa / 4; ++q) {
+                    for (int q = 0; q < KA / 4; ++q) {
                         if (4 * q >= t.ka4) break;
                         const float4 c = r4[q];
                         a += c.x * f[4 * q];
@@ -446,7 +450,7 @@ __global__ void __launch_bounds__(kWave) k_descriptor_reverse(
             auto channel = [&](float b, float bx, float by, float bz) {
                 float wsum = 0.0f, wsump = 0.0f;
 #pragma unroll
-                for (int n = 0; n < kMaxNa; ++n) {
+                for (int n = 0; n < NA; ++n) {
                     if (n >= na) break;
                     float w = WL[n * nlm + c];
                     wsum += w * gn[n];
@@ -785,6 +789,16 @@ bool descriptor_fits_registers(const DescTables &t) {
     return t.nr <= kMaxNr && t.na <= kMaxNa && t.kr <= kMaxKr && t.ka <= kMaxKa;
 }
 
+// Compact register arrays (basis 20 / 16, 12 angular channels, 5 moment
+// outputs per lane: 67 / 90 VGPRs for the forward / reverse kernel instead
+// of 140 / 145, so 7 / 5 waves per SIMD instead of 3) for the models that
+// fit them, the OAM and NEP models among them.
+constexpr int kCompactKr = 20, kCompactKa = 16, kCompactNa = 12, kCompactOut = 5;
+bool descriptor_compact(const DescTables &t) {
+    return t.nr <= kMaxNr && t.kr <= kCompactKr && t.ka <= kCompactKa && t.na <= kCompactNa &&
+           t.na * t.nlm <= kCompactOut * kWave;
+}
+
 }  // namespace
 
 static void allow_lds(const void *kernel, size_t lds) {
@@ -807,8 +821,13 @@ void descriptor_forward(const DescTables &t, const Records &r, const int32_t *ty
         return;
     }
     size_t lds = sizeof(float) * (kWave * (t.na + 1) + kWave * (t.nlm + 1) + t.na * t.nlm);
-    hipLaunchKernelGGL(k_descriptor_forward, dim3(r.n_atoms), dim3(kWave), lds, s, t, r, types,
-                       q, ldq, moments);
+    if (descriptor_compact(t))
+        hipLaunchKernelGGL((k_descriptor_forward<kCompactKr, kCompactKa, kMaxNr, kCompactOut>),
+                           dim3(r.n_atoms), dim3(kWave), lds, s, t, r, types, q, ldq, moments);
+    else
+        hipLaunchKernelGGL((k_descriptor_forward<kMaxKr, kMaxKa, kMaxNr,
+                                                 (kMaxNa * kMaxLm + kWave - 1) / kWave>),
+                           dim3(r.n_atoms), dim3(kWave), lds, s, t, r, types, q, ldq, moments);
     RUNE_HIP_CHECK(hipGetLastError());
 }
 
@@ -829,8 +848,14 @@ void descriptor_reverse(const DescTables &t, const ZblTables &z, const Records &
         return;
     }
     size_t lds = sizeof(float) * (t.Q + 2 * t.na * t.nlm);
-    hipLaunchKernelGGL(k_descriptor_reverse, dim3(r.n_atoms), dim3(kWave), lds, s, t, z, r,
-                       types, dq, ldq, moments, dmom, g_direct, energies, g, want_grad);
+    if (descriptor_compact(t))
+        hipLaunchKernelGGL((k_descriptor_reverse<kCompactKr, kCompactKa, kCompactNa>),
+                           dim3(r.n_atoms), dim3(kWave), lds, s, t, z, r, types, dq, ldq, moments,
+                           dmom, g_direct, energies, g, want_grad);
+    else
+        hipLaunchKernelGGL((k_descriptor_reverse<kMaxKr, kMaxKa, kMaxNa>), dim3(r.n_atoms),
+                           dim3(kWave), lds, s, t, z, r, types, dq, ldq, moments, dmom, g_direct,
+                           energies, g, want_grad);
     RUNE_HIP_CHECK(hipGetLastError());
 }
 
