@@ -243,6 +243,19 @@ def _small_model(seed, **changes):
     {}, {"vector_channels": 0}, {"activation": "tanh"}, {"activation": "gelu"},
     {"message_cutoff": 3.9, "message_basis_size": 4},
     {"rcut_angular": 5.2, "zbl": [0.8, 1.6]},
+    # widths of the fused edge-MLP kernels and the contiguous-column record
+    # kernels: D 32 / 64 / 128, one or two gate blocks, basis 4 / 17 / 20
+    # (drb tail rows 4 / 1 / 4), hidden 64 / 128 / 256
+    {"hidden_dim": 64, "message_dim": 32, "message_groups": 4, "vector_channels": 4,
+     "message_basis_size": 4},
+    {"hidden_dim": 128, "message_dim": 64, "message_groups": 8, "vector_channels": 20,
+     "message_basis_size": 20, "activation": "tanh"},
+    {"hidden_dim": 256, "message_dim": 128, "message_groups": 16, "vector_channels": 8,
+     "message_basis_size": 17, "activation": "gelu"},
+    # fallbacks: basis 5 (drb tail of 5 rows), 34 gates, groups narrower than a lane's columns
+    {"hidden_dim": 64, "message_dim": 32, "message_groups": 4, "vector_channels": 4,
+     "message_basis_size": 5},
+    {"hidden_dim": 64, "message_dim": 96, "message_groups": 32, "vector_channels": 2},
 ])
 def test_small_mp_variants_match_oracle(changes):
     from rune_amd import _native as N
