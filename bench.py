@@ -180,7 +180,8 @@ def algorithmic_model(ev, params, n_atoms, e_radial, e_angular):
     E_a) + 4QN + 96 n_a N (x2 with EQ moment adjoints) + 12E_r, forces and
     virials 16N + 32E_r.  Per-edge dense FLOPs of an EQ block count the
     factored edge MLP (K = kb + 2 ec l), the group gate and the direction
-    gates; of an MP block its edge MLP and gates."""
+    gates; of an MP block its edge MLP (radial-basis columns; the pair columns
+    are a table lookup) and gates."""
     p = params
     N, Er, Ea = n_atoms, e_radial, e_angular
     nr, na = p["n_desc_radial"], p["n_desc_angular"]
@@ -205,13 +206,32 @@ def algorithmic_model(ev, params, n_atoms, e_radial, e_angular):
             bwd = 8 * N + 16 * Er + 12 * H * N + 16 * md * N + 5 * S * N + 24 * Er
             per_edge = 2 * (kb + 2 * ec * lq) * md + 2 * md * G + 2 * md * 2 * ec * lq
         else:
-            vc, pd = p["vector_channels"], p["pair_dim"]
+            vc = p["vector_channels"]
             fwd = 8 * N + 16 * Er + 8 * H * N + 16 * vc * N
             bwd = 8 * N + 16 * Er + 12 * H * N + 20 * vc * N + 24 * Er
-            per_edge = 2 * (kb + pd) * md + 2 * md * (G + vc)
+            # the pair-embedding columns of edge_mlp.0 are a table lookup
+            per_edge = 2 * kb * md + 2 * md * (G + vc)
         out["message_bytes"] = nb * (fwd + bwd)
         out["message_flops"] = nb * 2 * per_edge * Er
     return out
+
+
+def per_atom_message_flops(ev, params, n_atoms):
+    """Forward FLOPs of the per-atom GEMMs of the message blocks: node
+    projections of RMSNorm(h) and the update MLP (message.py:69-99,
+    equivariant.py:98-121)."""
+    p = params
+    nb = int(p.get("message_layers", 0)) if ev.family == 0 else 0
+    if not nb:
+        return 0
+    H, md = p["hidden_dim"], p["message_dim"]
+    if p.get("message_mode", "scalar") == "equivariant":
+        lc = p["equivariant_l_max"] * p["equivariant_channels"]
+        node, upd = H * (2 * md + H), (H + lc) * md + md * H
+    else:
+        vc = p["vector_channels"]
+        node, upd = H * (H + vc), (H + vc) * md + md * H
+    return nb * 2 * n_atoms * (node + upd)
 
 
 def measured_traffic(workload, group):
@@ -361,6 +381,19 @@ def run_gpu(args):
     edge_ms += per_group.get("edge_kernels", {}).get("ms_per_step", 0.0)
     edge_bytes = algo["neighbors"] + algo["descriptor"] + algo["reverse"] + algo["forces"] + \
         algo["message_bytes"]
+    # whole-step matrix work: the dense FLOPs of SURVEY 8(d) (per-atom layers and
+    # per-edge MLPs, forward + input-gradient backward) against the step time;
+    # ideal_ms is the time they take at the fp32 MFMA peak (the survey's
+    # ideal-ceiling basis)
+    if ev.family == 0:
+        dense = 2 * model["dense_fwd"][1] + 2 * per_atom_message_flops(ev, params, n_atoms)
+    else:   # the NEP network's work (forward and input gradient) is its readout phase
+        dense = model["readout"][1]
+    total_flops = dense + algo["message_flops"]
+    mfma_step = {"dense_flops_per_step": int(total_flops),
+                 "ideal_ms": round(total_flops / FP32_PEAK * 1e3, 3),
+                 "achieved_TFs": round(total_flops / (ms_per_step / 1e3) / 1e12, 2),
+                 "frac": round(total_flops / (ms_per_step / 1e3) / FP32_PEAK, 4)}
     edge_summary = {"bytes_per_step": int(edge_bytes), "ms_per_step": round(edge_ms, 4),
                     "frac": round(edge_bytes / (edge_ms / 1e3) / HBM_PEAK, 4) if edge_ms else None,
                     "kernels": "neighbour build, descriptor forward / reverse, forces, "
@@ -368,6 +401,7 @@ def run_gpu(args):
     return {
         "value": value, "ms_per_step": ms_per_step, "n_atoms": n_atoms, "n_records": n_records,
         "e_radial": e_radial, "e_angular": e_angular, "edge_kernels_hbm": edge_summary,
+        "mfma_whole_step": mfma_step,
         "roofline": roof, "phases": per_phase, "groups": per_group,
         "energy": float(out["energy"].double().sum().cpu()),
     }
@@ -484,6 +518,7 @@ def main():
                    "radial_edges": res["e_radial"], "angular_edges": res["e_angular"]},
         "roofline": res["roofline"], "cpu_baseline": cpu, "phases": res["phases"],
         "groups": res["groups"], "edge_kernels_hbm": res["edge_kernels_hbm"],
+        "mfma_whole_step": res["mfma_whole_step"],
     }
     print(json.dumps(line), flush=True)
 
