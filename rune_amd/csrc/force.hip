@@ -66,16 +66,19 @@ __global__ void __launch_bounds__(256) k_forces(Records r, const float4 *g, floa
 
 // One workgroup per structure; thread t sums atoms t, t+256, ... then a tree.
 // Column sums of x [atoms, ncol] over the atoms of each structure, in fp64.
-// Block (p, b) takes part p of structure b's atoms (one part unless the
-// structure is large) and reads them as one flat coalesced range; the
-// threads in use are a multiple of ncol, so thread t always meets column
-// t % ncol.  The per-thread partials of each column are combined by a fixed
-// tree.  With one part the result goes to out, else to part[b, p, :].
-__global__ void __launch_bounds__(1024) k_structure_sum(const int32_t *sptr, const float *x,
-                                                        int ncol, int parts, double *part,
-                                                        float *out) {
+// Block (p, b, z) takes part p of structure b's atoms for output z (z = 0:
+// energies, one column; z = 1: virials, nine columns) and reads them as one
+// flat coalesced range; the threads in use are a multiple of the column
+// count, so thread t always meets column t % ncol.  The per-thread partials
+// of each column are combined by a fixed tree.  With one part the result
+// goes to the output, else to part[z][b, p, :].
+__global__ void __launch_bounds__(1024) k_structure_sum(const int32_t *sptr, SumArgs a) {
     __shared__ double lds[1024];
-    const int b = blockIdx.y, p = blockIdx.x, t = threadIdx.x;
+    const int b = blockIdx.y, p = blockIdx.x, t = threadIdx.x, z = blockIdx.z;
+    const float *x = z ? a.virial : a.energies;
+    float *out = z ? a.d_virial : a.d_energy;
+    if (!out) return;   // uniform per block
+    const int ncol = z ? 9 : 1, parts = a.parts;
     const int per = 1024 / ncol, lanes = per * ncol;
     const int a0 = sptr[b], n = sptr[b + 1] - a0, chunk = (n + parts - 1) / parts;
     const int lo = a0 + min(n, p * chunk), hi = a0 + min(n, (p + 1) * chunk);
@@ -96,23 +99,28 @@ __global__ void __launch_bounds__(1024) k_structure_sum(const int32_t *sptr, con
         if (parts == 1)
             out[size_t(b) * ncol + t] = float(lds[t]);
         else
-            part[(size_t(b) * parts + p) * ncol + t] = lds[t];
+            a.part[size_t(z) * a.part_stride + (size_t(b) * parts + p) * ncol + t] = lds[t];
     }
 }
 
-// out[b, c] = sum of the parts of structure b in part order.
-__global__ void k_structure_sum_parts(int n_structures, int ncol, int parts, const double *part,
-                                      float *out) {
+// Output q of the energies (q < n_structures) and virials: the sum of its
+// parts in part order.
+__global__ void k_structure_sum_parts(int n_structures, SumArgs a) {
     const int q = blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= n_structures * ncol) return;
-    const int b = q / ncol, c = q - b * ncol;
+    if (q >= n_structures * 10) return;
+    const int z = q < n_structures ? 0 : 1, ncol = z ? 9 : 1;
+    const int o = z ? q - n_structures : q;
+    float *out = z ? a.d_virial : a.d_energy;
+    if (!out) return;
+    const int b = o / ncol, c = o - b * ncol;
+    const double *part = a.part + size_t(z) * a.part_stride;
     double s = 0.0;
-    for (int p = 0; p < parts; ++p) s += part[(size_t(b) * parts + p) * ncol + c];
-    out[q] = float(s);
+    for (int p = 0; p < a.parts; ++p) s += part[(size_t(b) * a.parts + p) * ncol + c];
+    out[o] = float(s);
 }
 
 static int sum_parts(const Records &r) {
-    return std::max(1, std::min(64, ceil_div(r.max_struct_atoms, kSumChunk)));
+    return std::max(1, std::min(kMaxSumParts, ceil_div(r.max_struct_atoms, kSumChunk)));
 }
 
 }  // namespace
@@ -126,22 +134,28 @@ void forces_and_virial(const Records &r, const float4 *g, float *forces, float *
     RUNE_HIP_CHECK(hipGetLastError());
 }
 
-size_t structure_sum_scratch(const Records &r, int ncol) {
+size_t structure_sum_scratch(const Records &r) {
     const int parts = sum_parts(r);
-    return parts == 1 ? 0 : size_t(r.n_structures) * parts * ncol;
+    return parts == 1 ? 0 : size_t(r.n_structures) * parts * 10;
 }
 
-void structure_sum(const Records &r, const float *x, int ncol, float *out, double *scratch,
-                   hipStream_t s) {
-    if (r.n_structures == 0) return;
-    if (ncol < 1 || ncol > 1024) throw Error(RUNE_ERR_ARGUMENT, "structure_sum: bad column count");
-    const int parts = sum_parts(r);
-    if (parts > 1 && !scratch) throw Error(RUNE_ERR_STATE, "structure_sum: no scratch");
-    hipLaunchKernelGGL(k_structure_sum, dim3(parts, r.n_structures), dim3(1024), 0, s, r.sptr, x,
-                       ncol, parts, scratch, out);
-    if (parts > 1)
-        hipLaunchKernelGGL(k_structure_sum_parts, dim3(ceil_div(r.n_structures * ncol, 256)),
-                           dim3(256), 0, s, r.n_structures, ncol, parts, scratch, out);
+void structure_sums(const Records &r, const float *energies, float *d_energy,
+                    const float *atom_virial, float *d_virial, double *scratch, hipStream_t s) {
+    if (r.n_structures == 0 || (!d_energy && !d_virial)) return;
+    SumArgs a;
+    a.energies = energies;
+    a.virial = atom_virial;
+    a.d_energy = d_energy;
+    a.d_virial = d_virial;
+    a.parts = sum_parts(r);
+    a.part = scratch;
+    a.part_stride = size_t(r.n_structures) * a.parts;
+    if (a.parts > 1 && !scratch) throw Error(RUNE_ERR_STATE, "structure_sums: no scratch");
+    hipLaunchKernelGGL(k_structure_sum, dim3(a.parts, r.n_structures, 2), dim3(1024), 0, s,
+                       r.sptr, a);
+    if (a.parts > 1)
+        hipLaunchKernelGGL(k_structure_sum_parts, dim3(ceil_div(r.n_structures * 10, 256)),
+                           dim3(256), 0, s, r.n_structures, a);
     RUNE_HIP_CHECK(hipGetLastError());
 }
 

@@ -130,13 +130,22 @@ void nep_mlp(int M, int Q, int Hn, const float *q, int ldq, const int32_t *types
 // ---- forces (force.hip) ----
 void forces_and_virial(const Records &r, const float4 *g, float *forces, float *atom_virial,
                        hipStream_t s);
-// out[b, c] = sum over atoms of structure b of x[m, c] (fixed order, fp64 accumulation)
-// (fixed order for a given structure layout).  Structures larger than
-// kSumChunk atoms are split over several blocks whose fp64 partials go to
-// scratch; structure_sum_scratch(r, ncol) doubles are needed (0: none).
-constexpr int kSumChunk = 8192;
-size_t structure_sum_scratch(const Records &r, int ncol);
-void structure_sum(const Records &r, const float *x, int ncol, float *out, double *scratch,
-                   hipStream_t s);
+// Per-structure sums of the per-atom energies (one column) and virials
+// (nine columns): d_energy[b] and d_virial[b, c] over the atoms of structure
+// b, fp64 accumulation in a fixed order for a given structure layout; a null
+// output is skipped.  Structures larger than kSumChunk atoms are split over
+// up to kMaxSumParts blocks whose fp64 partials go to scratch, combined in
+// part order; structure_sum_scratch(r) doubles are needed (0: none).
+constexpr int kSumChunk = 1024, kMaxSumParts = 256;
+struct SumArgs {
+    const float *energies = nullptr, *virial = nullptr;
+    float *d_energy = nullptr, *d_virial = nullptr;
+    int parts = 1;
+    double *part = nullptr;
+    size_t part_stride = 0;   // doubles per output's partials (n_structures * parts)
+};
+size_t structure_sum_scratch(const Records &r);
+void structure_sums(const Records &r, const float *energies, float *d_energy,
+                    const float *atom_virial, float *d_virial, double *scratch, hipStream_t s);
 
 }  // namespace rune

@@ -343,9 +343,9 @@ static void finalize(ModelImpl &m) {
 
 // Range check of the atom types.  Writes a copy with every type clamped into
 // [0, n_types) -- the kernels after it read the copy, so a bad type never
-// indexes past a table -- and flags any type outside the range.  One block:
-// the flag is stored once, with no clearing launch before it; several
-// blocks: bit 0 is or-ed into a flag cleared beforehand.
+// indexes past a table -- and flags any type outside the range: a block
+// that meets one stores 1 into the flag word (pinned host memory the host
+// cleared before the launch), so no clearing launch or copy is needed.
 __global__ void __launch_bounds__(1024) k_check_types(int n, const int32_t *types, int n_types,
                                                       int32_t *safe, int32_t *flag) {
     int bad = 0;
@@ -355,12 +355,8 @@ __global__ void __launch_bounds__(1024) k_check_types(int n, const int32_t *type
         safe[i] = out ? 0 : t;
         bad |= out;
     }
-    if (gridDim.x == 1) {
-        bad = __syncthreads_or(bad);
-        if (threadIdx.x == 0) *flag = bad;
-    } else if (bad) {
-        atomicOr(flag, 1);
-    }
+    bad = __syncthreads_or(bad);
+    if (threadIdx.x == 0 && bad) *flag = 1;
 }
 
 // Largest atom count checked by one block of k_check_types.
@@ -409,7 +405,6 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     const int nmom = d.na * d.nlm;
     // ---- workspace plan ----
     Arena ar;
-    size_t o_flag = ar.add(16);
     size_t o_types = ar.add(4 * size_t(N));
     size_t o_q = ar.add(4 * size_t(N) * ldq);
     size_t o_dq = ar.add(4 * size_t(N) * ldq);
@@ -420,7 +415,7 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     size_t o_f = ar.add(4 * size_t(N) * 3);
     LocalPlan lp = plan_local(m, ar, N);
     MessagePlan mp = plan_messages(m, ar, N, E);
-    const size_t o_sums = ar.add(sizeof(double) * std::max<size_t>(1, structure_sum_scratch(r, 9)));
+    const size_t o_sums = ar.add(sizeof(double) * std::max<size_t>(1, structure_sum_scratch(r)));
     char *base = fixed;
     if (fixed) {
         if (ar.total > fixed_bytes) {
@@ -434,7 +429,6 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
         base = m.work.as<char>();
     }
     double *sums = reinterpret_cast<double *>(base + o_sums);
-    int32_t *flag = reinterpret_cast<int32_t *>(base + o_flag);
     float *q = reinterpret_cast<float *>(base + o_q);
     float *dq = reinterpret_cast<float *>(base + o_dq);
     float *mom = reinterpret_cast<float *>(base + o_s);
@@ -449,25 +443,23 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     // host never waits on an idle device; the kernels read the clamped copy
     if (N > 0) {
         int32_t *safe = reinterpret_cast<int32_t *>(base + o_types);
-        if (N <= kTypeCheckOneBlock) {
-            // one block stores the verdict straight into the pinned word
-            hipLaunchKernelGGL(k_check_types, dim3(1), dim3(1024), 0, s, N, types, m.cfg.n_types,
-                               safe, m.type_flag_host);
-        } else {
-            RUNE_HIP_CHECK(hipMemsetAsync(flag, 0, 16, s));
-            hipLaunchKernelGGL(k_check_types, dim3(std::min(ceil_div(N, 1024), 1024)), dim3(1024),
-                               0, s, N, types, m.cfg.n_types, safe, flag);
-            RUNE_HIP_CHECK(hipMemcpyAsync(m.type_flag_host, flag, 4, hipMemcpyDeviceToHost, s));
-        }
+        // a check left in flight by a call that failed part-way must end
+        // before the word is cleared
+        if (m.type_pending) RUNE_HIP_CHECK(hipEventSynchronize(m.type_event));
+        *static_cast<volatile int32_t *>(m.type_flag_host) = 0;
+        const int blocks = N <= kTypeCheckOneBlock ? 1 : std::min(ceil_div(N, 1024), 1024);
+        hipLaunchKernelGGL(k_check_types, dim3(blocks), dim3(1024), 0, s, N, types, m.cfg.n_types,
+                           safe, m.type_flag_host);
         RUNE_HIP_CHECK(hipGetLastError());
         RUNE_HIP_CHECK(hipEventRecord(m.type_event, s));
+        m.type_pending = true;
         types = safe;
     }
     if (N == 0) {
         // no atoms: every structure's energy and virial is zero (the sums
         // over empty ranges read nothing)
-        if (d_energy) structure_sum(r, energies, 1, d_energy, nullptr, s);
-        if (want_w && d_virial) structure_sum(r, atom_virial, 9, d_virial, nullptr, s);
+        structure_sums(r, energies, d_energy, atom_virial, want_w ? d_virial : nullptr, nullptr,
+                       s);
         return;
     }
     hipEvent_t *ev = nullptr;
@@ -519,14 +511,13 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     descriptor_reverse(d, m.zbl, r, types, dq, ldq, mom, dmom, g_direct, energies, g,
                        grad ? 1 : 0, s);
     mark(7);
-    if (d_energy) structure_sum(r, energies, 1, d_energy, sums, s);
-    if (grad) {
-        forces_and_virial(r, g, forces, atom_virial, s);
-        if (want_w && d_virial) structure_sum(r, atom_virial, 9, d_virial, sums, s);
-    }
+    if (grad) forces_and_virial(r, g, forces, atom_virial, s);
+    structure_sums(r, energies, d_energy, atom_virial, grad && want_w ? d_virial : nullptr, sums,
+                   s);
     mark(8);
     // the type verdict (on a bad type the outputs written above are unspecified)
     RUNE_HIP_CHECK(hipEventSynchronize(m.type_event));
+    m.type_pending = false;
     RUNE_REQUIRE(*static_cast<volatile int32_t *>(m.type_flag_host) == 0, RUNE_ERR_TYPE,
                  "atom type outside [0, n_types)");
 }

@@ -125,6 +125,7 @@ struct ModelImpl {
     // and the event that marks its arrival (created by rune_model_finalize)
     int32_t *type_flag_host = nullptr;
     hipEvent_t type_event = nullptr;
+    bool type_pending = false;   // type_event recorded, verdict not yet read
     // phase timing ring (events recorded on the launch stream)
     bool timing = false;
     std::vector<hipEvent_t> events;       // kTimingRing x (RUNE_N_PHASES + 1)

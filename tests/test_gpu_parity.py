@@ -216,6 +216,30 @@ def test_errors_are_reported():
                  6.0, 5.0, 10, 100)
 
 
+@pytest.mark.parametrize("reps", [2, 11])   # 64 atoms: one checking block; 10,648: a grid
+def test_out_of_range_type_is_reported_and_cleared(reps):
+    """A type outside [0, n_types) is reported by the device check (the kernels
+    read a clamped copy meanwhile), and the next call with valid types is
+    unaffected: bitwise equal to the call before."""
+    from rune_amd import _native as N
+    ev, p = _evaluator("loc")
+    s = W.si_diamond(seed=3, reps=reps)
+    types = torch.as_tensor(ev.types_of(s.numbers), device="cuda")
+    nl = N.NeighborList().build(torch.as_tensor(s.positions, device="cuda"), [0, len(s)],
+                                [s.cell], [np.ones(3, np.int32)], p["rcut_radial"],
+                                p["rcut_angular"], p["max_neighbors_radial"],
+                                p["max_neighbors_angular"])
+    good = ev.native.compute(nl, types, 1, True, True)
+    for bad in (-1, 1 << 20):
+        t = types.clone()
+        t[len(s) // 2] = bad
+        with pytest.raises(ValueError, match="outside"):
+            ev.native.compute(nl, t, 1, True, True)
+    again = ev.native.compute(nl, types, 1, True, True)
+    for k in ("energies", "energy", "forces", "virial"):
+        assert torch.equal(good[k], again[k]), k
+
+
 @pytest.mark.parametrize("name", ["fec4", "fcc108", "amo200"])
 def test_mp_model_matches_oracle(name):
     ev, p = _evaluator("mp")
