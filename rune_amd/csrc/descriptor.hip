@@ -134,37 +134,113 @@ __device__ inline float dot_cubic(const DescTables &t, int which, const float *s
     return r;
 }
 
-// q of one angular channel from its moments s[0..nlm) (descriptor.py:650-725).
-__device__ void invariants_of(const DescTables &t, const float *s, float *out, int stride) {
-    int idx = 0;
-    for (int L = 1; L <= t.l_max; ++L) {
-        int st = L * L - 1;
-        float q = t.c3b[st] * s[st] * s[st];
+// Invariant idx of the q layout (L = 1..l_max, then q222, q1111, q112, q123,
+// q233, q134 as enabled; descriptor.py:650-725) of one channel's moments s.
+__device__ float invariant_one(const DescTables &t, const float *s, int idx) {
+    if (idx < t.l_max) {
+        const int L = idx + 1, st = L * L - 1;
+        const float q = t.c3b[st] * s[st] * s[st];
         float acc = 0.0f;
         for (int c = 1; c <= 2 * L; ++c) acc += t.c3b[st + c] * s[st + c] * s[st + c];
-        out[stride * idx++] = q + 2.0f * acc;
+        return q + 2.0f * acc;
     }
-    if (t.has_q[0]) {
+    int kind = 0;
+    for (int k = idx - t.l_max; kind < 6; ++kind)
+        if (t.has_q[kind] && k-- == 0) break;
+    if (kind == 0) {
         const float *c = t.c4b;
-        float s3 = s[3], s4 = s[4], s5 = s[5], s6 = s[6], s7 = s[7];
-        out[stride * idx++] = c[0] * s3 * s3 * s3 + c[1] * s3 * (s4 * s4 + s5 * s5) +
-                              c[2] * s3 * (s6 * s6 + s7 * s7) + c[3] * s6 * (s5 * s5 - s4 * s4) +
-                              c[4] * s4 * s5 * s7;
+        const float s3 = s[3], s4 = s[4], s5 = s[5], s6 = s[6], s7 = s[7];
+        return c[0] * s3 * s3 * s3 + c[1] * s3 * (s4 * s4 + s5 * s5) +
+               c[2] * s3 * (s6 * s6 + s7 * s7) + c[3] * s6 * (s5 * s5 - s4 * s4) +
+               c[4] * s4 * s5 * s7;
+    }
+    if (kind == 1) {
+        const float *c = t.c5b;
+        const float a = s[0] * s[0], b = s[1] * s[1] + s[2] * s[2];
+        return c[0] * a * a + c[1] * a * b + c[2] * b * b;
+    }
+    if (kind == 2) {
+        const float *c = t.c4b2;
+        const float a = s[0], b = s[1], cc = s[2], d = s[3], e = s[4], f = s[5], g = s[6],
+                    h = s[7];
+        return c[0] * a * a * d + c[1] * a * (b * e + cc * f) + c[2] * d * (b * b + cc * cc) +
+               c[3] * g * (b * b - cc * cc) + c[4] * b * cc * h;
+    }
+    return dot_cubic(t, kind - 3, s);
+}
+
+// q of every angular channel (moments sL[n * nlm + c]): one output per lane,
+// out[idx * na + n] for invariant idx of channel n.
+__device__ void invariants_all(const DescTables &t, const float *sL, float *out, int lane) {
+    const int na = t.na, nlm = t.nlm;
+    for (int o = lane; o < na * t.num_L; o += kWave) {
+        const int idx = o / na, n = o - idx * na;
+        out[o] = invariant_one(t, sL + n * nlm, idx);
+    }
+}
+
+// dE/ds_c of one channel: sum over its invariants idx of dq[idx * stride] *
+// d q_idx / d s_c (force.py:28-133), for models without the cubic invariants.
+__device__ float invariant_grad_one(const DescTables &t, const float *s, const float *dq,
+                                    int stride, int c) {
+    float w = 0.0f;
+    int L = 1;
+    while ((L + 1) * (L + 1) - 1 <= c) ++L;   // c in [L^2 - 1, (L + 1)^2 - 1)
+    const int st = L * L - 1;
+    if (L <= t.l_max) w += dq[stride * (L - 1)] * ((c == st ? 2.0f : 4.0f) * t.c3b[c] * s[c]);
+    int idx = t.l_max;
+    if (t.has_q[0]) {
+        const float *k = t.c4b;
+        const float g = dq[stride * idx++];
+        const float s20 = s[3], s21r = s[4], s21i = s[5], s22r = s[6], s22i = s[7];
+        if (c == 3)
+            w += g * (3.0f * k[0] * s20 * s20 + k[1] * (s21r * s21r + s21i * s21i) +
+                      k[2] * (s22r * s22r + s22i * s22i));
+        else if (c == 4)
+            w += g * (2.0f * k[1] * s20 * s21r - 2.0f * k[3] * s22r * s21r + k[4] * s21i * s22i);
+        else if (c == 5)
+            w += g * (2.0f * k[1] * s20 * s21i + 2.0f * k[3] * s22r * s21i + k[4] * s21r * s22i);
+        else if (c == 6)
+            w += g * (2.0f * k[2] * s20 * s22r + k[3] * (s21i * s21i - s21r * s21r));
+        else if (c == 7)
+            w += g * (2.0f * k[2] * s20 * s22i + k[4] * s21r * s21i);
     }
     if (t.has_q[1]) {
-        const float *c = t.c5b;
-        float a = s[0] * s[0], b = s[1] * s[1] + s[2] * s[2];
-        out[stride * idx++] = c[0] * a * a + c[1] * a * b + c[2] * b * b;
+        const float *k = t.c5b;
+        const float g = dq[stride * idx++];
+        if (c <= 2) {
+            const float s0 = s[0], s1 = s[1], s2 = s[2];
+            const float a = s0 * s0, b = s1 * s1 + s2 * s2;
+            const float factor = k[1] * a + 2.0f * k[2] * b;
+            if (c == 0)
+                w += g * (2.0f * s0 * (2.0f * k[0] * a + k[1] * b));
+            else
+                w += g * 2.0f * s[c] * factor;
+        }
     }
     if (t.has_q[2]) {
-        const float *c = t.c4b2;
-        float a = s[0], b = s[1], cc = s[2], d = s[3], e = s[4], f = s[5], g = s[6], h = s[7];
-        out[stride * idx++] = c[0] * a * a * d + c[1] * a * (b * e + cc * f) +
-                              c[2] * d * (b * b + cc * cc) + c[3] * g * (b * b - cc * cc) +
-                              c[4] * b * cc * h;
+        const float *k = t.c4b2;
+        const float g = dq[stride * idx++];
+        const float a = s[0], b = s[1], cc = s[2], d = s[3], e = s[4], f = s[5], gg = s[6],
+                    h = s[7];
+        if (c == 0)
+            w += g * (2.0f * k[0] * a * d + k[1] * (b * e + cc * f));
+        else if (c == 1)
+            w += g * (k[1] * a * e + 2.0f * k[2] * d * b + 2.0f * k[3] * gg * b + k[4] * cc * h);
+        else if (c == 2)
+            w += g * (k[1] * a * f + 2.0f * k[2] * d * cc - 2.0f * k[3] * gg * cc + k[4] * b * h);
+        else if (c == 3)
+            w += g * (k[0] * a * a + k[2] * (b * b + cc * cc));
+        else if (c == 4)
+            w += g * k[1] * a * b;
+        else if (c == 5)
+            w += g * k[1] * a * cc;
+        else if (c == 6)
+            w += g * k[3] * (b * b - cc * cc);
+        else if (c == 7)
+            w += g * k[4] * b * cc;
     }
-    for (int w = 0; w < 3; ++w)
-        if (t.has_q[3 + w]) out[stride * idx++] = dot_cubic(t, w, s);
+    return w;
 }
 
 // dE/ds of one channel: W[c] += sum_L dq_L * dq_L/ds_c  (force.py:28-133).
@@ -223,6 +299,24 @@ __device__ void invariant_gradient(const DescTables &t, const float *s, const fl
             W[b] += gc * (s[a] * s[c]);
             W[c] += gc * (s[a] * s[b]);
         }
+    }
+}
+
+// WL[n * nlm + c] += dE/ds_c of channel n for every (n, c).  Without the
+// cubic invariants one lane forms one output; with them one lane takes a
+// channel and scatters each term's three partial derivatives (the per-output
+// form would walk a long derivative list per lane).
+__device__ void invariant_gradient_all(const DescTables &t, const float *sL, const float *dq,
+                                       float *WL, int lane) {
+    const int na = t.na, nlm = t.nlm;
+    if (t.has_q[3] || t.has_q[4] || t.has_q[5]) {
+        for (int n = lane; n < na; n += kWave)
+            invariant_gradient(t, sL + n * nlm, dq + n, na, WL + n * nlm);
+        return;
+    }
+    for (int o = lane; o < na * nlm; o += kWave) {
+        const int n = o / nlm, c = o - n * nlm;
+        WL[o] += invariant_grad_one(t, sL + n * nlm, dq + n, na, c);
     }
 }
 
@@ -324,7 +418,7 @@ __global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Reco
         moments[size_t(i) * nout + o] = acc[j];
     }
     __syncthreads();
-    if (lane < na) invariants_of(t, sL + lane * nlm, q + size_t(i) * ldq + t.nr + lane, na);
+    invariants_all(t, sL, q + size_t(i) * ldq + t.nr, lane);
 }
 
 __device__ inline void zbl_pair(const ZblTables &z, int ti, int tj, float d, float &e,
@@ -393,8 +487,7 @@ __global__ void __launch_bounds__(kWave) k_descriptor_reverse(
             WL[o] = dmom ? dmom[size_t(i) * nout + o] : 0.0f;
         }
         __syncthreads();
-        if (lane < na)
-            invariant_gradient(t, sL + lane * nlm, dqL + t.nr + lane, na, WL + lane * nlm);
+        invariant_gradient_all(t, sL, dqL + t.nr, WL, lane);
         __syncthreads();
     }
     float zsum = 0.0f;
@@ -651,8 +744,7 @@ __global__ void __launch_bounds__(kWave) k_descriptor_forward_wide(DescTables t,
         }
     }
     __syncthreads();
-    for (int n = lane; n < na; n += kWave)
-        invariants_of(t, sL + n * nlm, q + size_t(i) * ldq + t.nr + n, na);
+    invariants_all(t, sL, q + size_t(i) * ldq + t.nr, lane);
 }
 
 __global__ void __launch_bounds__(kWave) k_descriptor_reverse_wide(
@@ -680,8 +772,7 @@ __global__ void __launch_bounds__(kWave) k_descriptor_reverse_wide(
             WL[o] = dmom ? dmom[size_t(i) * nout + o] : 0.0f;
         }
         __syncthreads();
-        for (int n = lane; n < na; n += kWave)
-            invariant_gradient(t, sL + n * nlm, dqL + t.nr + n, na, WL + n * nlm);
+        invariant_gradient_all(t, sL, dqL + t.nr, WL, lane);
         __syncthreads();
     }
     float *f = fL + lane * (kmax + 1), *fp = fpL + lane * (kmax + 1);
