@@ -81,7 +81,7 @@ __device__ inline void store_stage(const float4 (&r)[kRows * 8 / 256], float *S,
 // activation (act2 from column act_split on) and the activation derivative.
 // Out-of-range elements load from clamped indices and store nothing.
 template <int WM, int WN, int WMW>
-__device__ inline void tile_epilogue(floatx4 (&acc)[WM][WN], float *, int M, int N,
+__device__ inline void tile_epilogue(floatx4 (&acc)[WM][WN], int M, int N,
                                      float *__restrict__ C, int ldc, const Epilogue &ep,
                                      int m0, int n0) {
     constexpr int WNW = 4 / WMW;
@@ -226,16 +226,19 @@ __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *
         }
         __syncthreads();
     }
-    tile_epilogue<WM, WN, WMW>(acc, smem, M, N, C, ldc, ep, m0, n0);
+    tile_epilogue<WM, WN, WMW>(acc, M, N, C, ldc, ep, m0, n0);
 }
 
 // One output element of the fused epilogue (the terms of tile_epilogue in the
 // same order); the element's loads precede its stores, so C may alias an
 // input element for element.
 __device__ inline void epilogue_one(const Epilogue &ep, float acc, int row, int col,
-                                    float *__restrict__ C, int ldc) {
+                                    float *__restrict__ C, int ldc, float rms) {
     float t = acc;
-    if (ep.row_scale) t *= ep.row_scale[row];
+    if (ep.rms_out)
+        t *= rms;
+    else if (ep.row_scale)
+        t *= ep.row_scale[row];
     if (ep.bias) t += ep.bias[col];
     if (ep.emb) t += ep.emb[size_t(ep.types[row]) * ep.ld_emb + col];
     if (ep.residual) t += ep.residual[size_t(row) * ep.ldr + col];
@@ -273,7 +276,7 @@ __device__ inline float4 load_k4(const float *__restrict__ x, int k, int K) {
 // operands are loaded before the current step's products); the 4 partial
 // tiles are summed through LDS in wave order and the epilogue runs per
 // element with consecutive threads on consecutive columns.
-template <int WN, bool kVec>
+template <int WN, bool kVec, bool kRms = false>
 __global__ void __launch_bounds__(256) k_gemm_small(int M, int N, int K,
                                                     const float *__restrict__ A, int lda,
                                                     const float *__restrict__ Bt, int ldb,
@@ -300,7 +303,9 @@ __global__ void __launch_bounds__(256) k_gemm_small(int M, int N, int K,
 #pragma unroll
         for (int j = 0; j < WN; ++j) fb[j] = load_k4<kVec>(b[j], 16 * wave + 4 * g, K);
     }
+    float ss = 0.0f;   // sum of squares of the A values this lane loads (rms epilogue)
     for (int st = wave; st < steps; st += 4) {
+        if constexpr (kRms) ss += ((fa.x * fa.x + fa.y * fa.y) + fa.z * fa.z) + fa.w * fa.w;
         float4 na = fa, nb[WN];
 #pragma unroll
         for (int j = 0; j < WN; ++j) nb[j] = fb[j];
@@ -324,12 +329,29 @@ __global__ void __launch_bounds__(256) k_gemm_small(int M, int N, int K,
     for (int j = 0; j < WN; ++j)
 #pragma unroll
         for (int v = 0; v < 4; ++v) part[wave][4 * g + v][16 * j + r] = acc[j][v];
+    // lanes r, r + 16, r + 32, r + 48 of every wave load row r
+    __shared__ float rsum[4][16];
+    if constexpr (kRms) {
+        ss += __shfl_xor(ss, 16, 64);
+        ss += __shfl_xor(ss, 32, 64);
+        if (lane < 16) rsum[wave][lane] = ss;
+    }
     __syncthreads();
+    __shared__ float rms[16];
+    if constexpr (kRms) {
+        if (threadIdx.x < 16) {
+            const int rr = threadIdx.x;
+            const float v = ((rsum[0][rr] + rsum[1][rr]) + rsum[2][rr]) + rsum[3][rr];
+            rms[rr] = 1.0f / sqrtf(v / float(K) + ep.rms_eps);
+            if (n0 == 0 && m0 + rr < M) ep.rms_out[m0 + rr] = rms[rr];
+        }
+        __syncthreads();
+    }
     for (int e = threadIdx.x; e < 16 * TN; e += 256) {
         const int rr = e / TN, cc = e % TN, row = m0 + rr, col = n0 + cc;
         if (row >= M || col >= N) continue;
         const float v = ((part[0][rr][cc] + part[1][rr][cc]) + part[2][rr][cc]) + part[3][rr][cc];
-        epilogue_one(ep, v, row, col, C, ldc);
+        epilogue_one(ep, v, row, col, C, ldc, kRms ? rms[rr] : 1.0f);
     }
 }
 
@@ -478,6 +500,8 @@ static void launch_gemm(bool vec, int M, int N, int K, const float *A, int lda, 
 static void gemm_any(int M, int N, int K, const float *A, int lda, const float *Bt, int ldb,
                      float *C, int ldc, const Epilogue &ep, const GemmBatch &bt, hipStream_t s) {
     if (M == 0 || N == 0 || bt.count == 0) return;
+    if (ep.rms_out && (ep.a_act >= 0 || bt.count != 1 || ep.row_scale))
+        throw Error(RUNE_ERR_ARGUMENT, "gemm: the rms epilogue takes a plain single product");
     bool vec = lda % 4 == 0 && ldb % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
                (reinterpret_cast<uintptr_t>(Bt) & 15) == 0 && bt.sa % 4 == 0 && bt.sb % 4 == 0;
     const int64_t big_blocks = int64_t(ceil_div(M, 64)) * ceil_div(N, narrow_tile(N) ? 32 : 64);
@@ -486,7 +510,19 @@ static void gemm_any(int M, int N, int K, const float *A, int lda, const float *
         const bool n16 = ceil_div(N, 16) * 16 < ceil_div(N, 32) * 32;
         const int nbn = ceil_div(N, n16 ? 16 : 32);
         const dim3 grid(unsigned(int64_t(ceil_div(M, 16)) * nbn));
-        if (n16 && vec)
+        if (ep.rms_out && n16 && vec)
+            hipLaunchKernelGGL((k_gemm_small<1, true, true>), grid, dim3(256), 0, s, M, N, K, A,
+                               lda, Bt, ldb, C, ldc, ep, nbn);
+        else if (ep.rms_out && n16)
+            hipLaunchKernelGGL((k_gemm_small<1, false, true>), grid, dim3(256), 0, s, M, N, K, A,
+                               lda, Bt, ldb, C, ldc, ep, nbn);
+        else if (ep.rms_out && vec)
+            hipLaunchKernelGGL((k_gemm_small<2, true, true>), grid, dim3(256), 0, s, M, N, K, A,
+                               lda, Bt, ldb, C, ldc, ep, nbn);
+        else if (ep.rms_out)
+            hipLaunchKernelGGL((k_gemm_small<2, false, true>), grid, dim3(256), 0, s, M, N, K, A,
+                               lda, Bt, ldb, C, ldc, ep, nbn);
+        else if (n16 && vec)
             hipLaunchKernelGGL((k_gemm_small<1, true>), grid, dim3(256), 0, s, M, N, K, A, lda, Bt,
                                ldb, C, ldc, ep, nbn);
         else if (n16)
@@ -498,10 +534,21 @@ static void gemm_any(int M, int N, int K, const float *A, int lda, const float *
         else
             hipLaunchKernelGGL((k_gemm_small<2, false>), grid, dim3(256), 0, s, M, N, K, A, lda,
                                Bt, ldb, C, ldc, ep, nbn);
-    } else if (narrow_tile(N))
-        launch_gemm<1, 2, 4>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, bt, s);
-    else
-        launch_gemm<2, 2, 2>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, ep, bt, s);
+    } else {
+        // the row scales of the rms epilogue come from a row kernel here: the
+        // 64-row tile kernels run slower with them folded in (more registers)
+        Epilogue e = ep;
+        if (ep.rms_out) {
+            hipLaunchKernelGGL(k_row_inv_rms, dim3(ceil_div(M, 4)), dim3(256), 0, s, M, K, A, lda,
+                               ep.rms_eps, ep.rms_out);
+            e.row_scale = ep.rms_out;
+            e.rms_out = nullptr;
+        }
+        if (narrow_tile(N))
+            launch_gemm<1, 2, 4>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, e, bt, s);
+        else
+            launch_gemm<2, 2, 2>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, e, bt, s);
+    }
     RUNE_HIP_CHECK(hipGetLastError());
 }
 
@@ -513,13 +560,6 @@ void gemm(int M, int N, int K, const float *A, int lda, const float *Bt, int ldb
 void gemm_batched(const GemmBatch &bt, int M, int N, int K, const float *A, int lda,
                   const float *Bt, int ldb, float *C, int ldc, hipStream_t s) {
     gemm_any(M, N, K, A, lda, Bt, ldb, C, ldc, Epilogue{}, bt, s);
-}
-
-void row_inv_rms(int M, int N, const float *x, int ldx, float eps, float *inv_rms, hipStream_t s) {
-    if (M == 0) return;
-    hipLaunchKernelGGL(k_row_inv_rms, dim3(ceil_div(M, 4)), dim3(256), 0, s, M, N, x, ldx, eps,
-                       inv_rms);
-    RUNE_HIP_CHECK(hipGetLastError());
 }
 
 void rms_backward(int M, int N, const float *h, int ldh, const float *inv_rms, const float *dz,

@@ -2023,9 +2023,9 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
         const MessageWeights &w = m.msg[b];
         const BlockBuffers &bb = p.blocks[b];
         EqArgs a = eq_args(m, p, r, b);
-        row_inv_rms(N, H, cur, H, float(c.norm_eps), p.at(bb.rin), s);
         Epilogue e0;
-        e0.row_scale = p.at(bb.rin);
+        e0.rms_out = p.at(bb.rin);   // input RMSNorm, formed by the GEMM
+        e0.rms_eps = float(c.norm_eps);
         gemm(N, w.NP, H, cur, H, w.node_f, H, p.at(bb.vs), w.NP, e0, s);
         launch_mix(lq, C, N, w.mix, p.at(bb.dir_in), 0, nullptr, nullptr, p.at(bb.mixstate), s);
         if (E > 0) {

@@ -100,6 +100,12 @@ struct Epilogue {
     // pre-activations), -1 none; the padding of a partial K stage is
     // multiplied by zero B columns, so act(0) there does not matter
     int a_act = -1;
+    // RMSNorm of the A rows folded in: when set, v = r[m] * acc with
+    // r[m] = 1 / sqrt(mean_k A[m, k]^2 + rms_eps) formed from the rows the
+    // GEMM reads (K is the norm width), and r stored to rms_out[m]; used
+    // instead of row_scale, not with a_act or batches
+    float *rms_out = nullptr;
+    float rms_eps = 0.0f;
 };
 // C[M,N] = A[M,K] Bt[N,K]^T (+ epilogue); row-major with leading dimensions.
 void gemm(int M, int N, int K, const float *A, int lda, const float *Bt, int ldb, float *C,
@@ -114,8 +120,6 @@ struct GemmBatch {
 };
 void gemm_batched(const GemmBatch &bt, int M, int N, int K, const float *A, int lda,
                   const float *Bt, int ldb, float *C, int ldc, hipStream_t s);
-// inv_rms[m] = rsqrt(mean_n x[m,n]^2 + eps)
-void row_inv_rms(int M, int N, const float *x, int ldx, float eps, float *inv_rms, hipStream_t s);
 // dh[m] = base[m] + r*dz[m] - r^3/N (dz[m].h[m]) h[m]   (RMSNorm backward + residual)
 void rms_backward(int M, int N, const float *h, int ldh, const float *inv_rms, const float *dz,
                   int ldz, const float *base, int ldb, float *dh, int ldd, hipStream_t s);

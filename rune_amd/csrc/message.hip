@@ -1443,9 +1443,9 @@ float *messages_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Recor
     for (int b = 0; b < c.message_layers; ++b) {
         const MessageWeights &w = m.msg[b];
         const BlockBuffers &bb = p.blocks[b];
-        row_inv_rms(N, H, cur, H, float(c.norm_eps), p.at(bb.rin), s);
         Epilogue e0;
-        e0.row_scale = p.at(bb.rin);
+        e0.rms_out = p.at(bb.rin);   // input RMSNorm, formed by the GEMM
+        e0.rms_eps = float(c.norm_eps);
         gemm(N, w.NP, H, cur, H, w.node_f, H, p.at(bb.vs), w.NP, e0, s);
         bool fused = false;
         if (E > 0) {

@@ -590,9 +590,9 @@ float *local_forward(ModelImpl &m, LocalPlan &p, int N, const float *q, int ldq,
         float *hn = p.h + size_t(b + 1) * N * H;
         float *rb = p.r + size_t(b) * N;
         float *ub = p.u + size_t(b) * N * F;
-        row_inv_rms(N, H, hb, H, float(m.cfg.norm_eps), rb, s);
         Epilogue e1;
-        e1.row_scale = rb;
+        e1.rms_out = rb;   // RMSNorm of hb, formed by the GEMM from the rows it reads
+        e1.rms_eps = float(m.cfg.norm_eps);
         e1.bias = m.res[b].b1;
         e1.pre = ub;
         e1.ldp = F;
