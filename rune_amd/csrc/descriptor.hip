@@ -8,6 +8,7 @@
 // term (zbl.py:92-141).  No atomics: every output has one writer.
 #include <cmath>
 
+#include "cubic.hpp"
 #include "kernels.hpp"
 
 namespace rune {
@@ -125,13 +126,10 @@ __device__ inline void zpoly(const DescTables &t, int L, int n1, float z, float 
     }
 }
 
-__device__ inline float dot_cubic(const DescTables &t, int which, const float *s) {
-    float r = 0.0f;
-    const float *co = t.cubic_coef + which * kMaxCubic;
-    const int *ix = t.cubic_idx + which * kMaxCubic * 3;
-    for (int k = 0; k < t.cubic_n[which]; ++k)
-        r = r + co[k] * ((s[ix[3 * k]] * s[ix[3 * k + 1]]) * s[ix[3 * k + 2]]);
-    return r;
+// One channel's moments s[0..kCubicComps) in registers (zero past nlm).
+__device__ inline void cubic_moments(const float *s, int nlm, float (&sr)[kCubicComps]) {
+#pragma unroll
+    for (int c = 0; c < kCubicComps; ++c) sr[c] = c < nlm ? s[c] : 0.0f;
 }
 
 // Invariant idx of the q layout (L = 1..l_max, then q222, q1111, q112, q123,
@@ -166,7 +164,9 @@ __device__ float invariant_one(const DescTables &t, const float *s, int idx) {
         return c[0] * a * a * d + c[1] * a * (b * e + cc * f) + c[2] * d * (b * b + cc * cc) +
                c[3] * g * (b * b - cc * cc) + c[4] * b * cc * h;
     }
-    return dot_cubic(t, kind - 3, s);
+    float sr[kCubicComps];
+    cubic_moments(s, t.nlm, sr);
+    return kind == 3 ? cubic_value<0>(sr) : kind == 4 ? cubic_value<1>(sr) : cubic_value<2>(sr);
 }
 
 // q of every angular channel (moments sL[n * nlm + c]): one output per lane,
@@ -179,8 +179,8 @@ __device__ void invariants_all(const DescTables &t, const float *sL, float *out,
     }
 }
 
-// dE/ds_c of one channel: sum over its invariants idx of dq[idx * stride] *
-// d q_idx / d s_c (force.py:28-133), for models without the cubic invariants.
+// dE/ds_c of one channel from its order and four/five-body invariants: sum
+// over them of dq[idx * stride] * d q_idx / d s_c (force.py:28-133).
 __device__ float invariant_grad_one(const DescTables &t, const float *s, const float *dq,
                                     int stride, int c) {
     float w = 0.0f;
@@ -243,80 +243,27 @@ __device__ float invariant_grad_one(const DescTables &t, const float *s, const f
     return w;
 }
 
-// dE/ds of one channel: W[c] += sum_L dq_L * dq_L/ds_c  (force.py:28-133).
-__device__ void invariant_gradient(const DescTables &t, const float *s, const float *dq,
-                                   int stride, float *W) {
-    int idx = 0;
-    for (int L = 1; L <= t.l_max; ++L) {
-        int st = L * L - 1;
-        float g = dq[stride * idx++];
-        for (int c = 0; c <= 2 * L; ++c)
-            W[st + c] += g * ((c == 0 ? 2.0f : 4.0f) * t.c3b[st + c] * s[st + c]);
-    }
-    if (t.has_q[0]) {
-        const float *c = t.c4b;
-        float g = dq[stride * idx++];
-        float s20 = s[3], s21r = s[4], s21i = s[5], s22r = s[6], s22i = s[7];
-        W[3] += g * (3.0f * c[0] * s20 * s20 + c[1] * (s21r * s21r + s21i * s21i) +
-                     c[2] * (s22r * s22r + s22i * s22i));
-        W[4] += g * (2.0f * c[1] * s20 * s21r - 2.0f * c[3] * s22r * s21r + c[4] * s21i * s22i);
-        W[5] += g * (2.0f * c[1] * s20 * s21i + 2.0f * c[3] * s22r * s21i + c[4] * s21r * s22i);
-        W[6] += g * (2.0f * c[2] * s20 * s22r + c[3] * (s21i * s21i - s21r * s21r));
-        W[7] += g * (2.0f * c[2] * s20 * s22i + c[4] * s21r * s21i);
-    }
-    if (t.has_q[1]) {
-        const float *c = t.c5b;
-        float g = dq[stride * idx++];
-        float s0 = s[0], s1 = s[1], s2 = s[2];
-        float a = s0 * s0, b = s1 * s1 + s2 * s2;
-        float factor = c[1] * a + 2.0f * c[2] * b;
-        W[0] += g * (2.0f * s0 * (2.0f * c[0] * a + c[1] * b));
-        W[1] += g * 2.0f * s1 * factor;
-        W[2] += g * 2.0f * s2 * factor;
-    }
-    if (t.has_q[2]) {
-        const float *c = t.c4b2;
-        float g = dq[stride * idx++];
-        float a = s[0], b = s[1], cc = s[2], d = s[3], e = s[4], f = s[5], gg = s[6], h = s[7];
-        W[0] += g * (2.0f * c[0] * a * d + c[1] * (b * e + cc * f));
-        W[1] += g * (c[1] * a * e + 2.0f * c[2] * d * b + 2.0f * c[3] * gg * b + c[4] * cc * h);
-        W[2] += g * (c[1] * a * f + 2.0f * c[2] * d * cc - 2.0f * c[3] * gg * cc + c[4] * b * h);
-        W[3] += g * (c[0] * a * a + c[2] * (b * b + cc * cc));
-        W[4] += g * c[1] * a * b;
-        W[5] += g * c[1] * a * cc;
-        W[6] += g * c[3] * (b * b - cc * cc);
-        W[7] += g * c[4] * b * cc;
-    }
-    for (int w = 0; w < 3; ++w) {
-        if (!t.has_q[3 + w]) continue;
-        float g = dq[stride * idx++];
-        const float *co = t.cubic_coef + w * kMaxCubic;
-        const int *ix = t.cubic_idx + w * kMaxCubic * 3;
-        for (int k = 0; k < t.cubic_n[w]; ++k) {
-            int a = ix[3 * k], b = ix[3 * k + 1], c = ix[3 * k + 2];
-            float gc = g * co[k];
-            W[a] += gc * (s[b] * s[c]);
-            W[b] += gc * (s[a] * s[c]);
-            W[c] += gc * (s[a] * s[b]);
-        }
-    }
-}
-
-// WL[n * nlm + c] += dE/ds_c of channel n for every (n, c).  Without the
-// cubic invariants one lane forms one output; with them one lane takes a
-// channel and scatters each term's three partial derivatives (the per-output
-// form would walk a long derivative list per lane).
+// WL[n * nlm + c] += dE/ds_c of channel n for every (n, c): one output per
+// lane for the order and four/five-body invariants, then one channel per
+// lane for the cubic invariants (their unrolled term lists read the moments
+// from registers and update the row at constant offsets).
 __device__ void invariant_gradient_all(const DescTables &t, const float *sL, const float *dq,
                                        float *WL, int lane) {
     const int na = t.na, nlm = t.nlm;
-    if (t.has_q[3] || t.has_q[4] || t.has_q[5]) {
-        for (int n = lane; n < na; n += kWave)
-            invariant_gradient(t, sL + n * nlm, dq + n, na, WL + n * nlm);
-        return;
-    }
     for (int o = lane; o < na * nlm; o += kWave) {
         const int n = o / nlm, c = o - n * nlm;
         WL[o] += invariant_grad_one(t, sL + n * nlm, dq + n, na, c);
+    }
+    if (!(t.has_q[3] || t.has_q[4] || t.has_q[5])) return;
+    __syncthreads();
+    for (int n = lane; n < na; n += kWave) {
+        float sr[kCubicComps];
+        cubic_moments(sL + n * nlm, nlm, sr);
+        float *w = WL + n * nlm;
+        int idx = t.l_max + t.has_q[0] + t.has_q[1] + t.has_q[2];
+        if (t.has_q[3]) cubic_grad<0>(sr, dq[n + na * idx++], w, nlm);
+        if (t.has_q[4]) cubic_grad<1>(sr, dq[n + na * idx++], w, nlm);
+        if (t.has_q[5]) cubic_grad<2>(sr, dq[n + na * idx++], w, nlm);
     }
 }
 

@@ -13,7 +13,6 @@ constexpr int kMaxNa = 16;    // angular descriptor channels
 constexpr int kMaxKa = 24;    // angular basis size
 constexpr int kMaxL = 8;      // l_max
 constexpr int kMaxLm = kMaxL * (kMaxL + 2);
-constexpr int kMaxCubic = 64; // terms of one cubic invariant
 
 // Descriptor constants and coefficient tables (device pointers).
 struct DescTables {
@@ -31,9 +30,6 @@ struct DescTables {
     const float *c4b;             // [5]
     const float *c5b;             // [3]
     const float *c4b2;            // [5]
-    const float *cubic_coef;      // [3][kMaxCubic]  q123, q233, q134
-    const int *cubic_idx;         // [3][kMaxCubic][3]
-    int cubic_n[3];
 };
 
 // ZBL (rune/mobius/zbl.py:92-141).

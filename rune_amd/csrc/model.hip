@@ -21,46 +21,6 @@ namespace rune {
 namespace {
 thread_local std::string g_last_error;
 
-struct CubicTerm {
-    int coef, sign, a, b, c;
-};
-// Cubic invariant term lists (coefficient index into C4B_123/233/134, sign,
-// component indices), in the order of rune/mobius/descriptor.py:141-196.
-const CubicTerm kQ123[] = {
-    {6, 1, 12, 2, 4}, {6, -1, 11, 2, 5}, {6, 1, 1, 11, 4}, {6, 1, 1, 12, 5}, {5, 1, 0, 11, 6},
-    {5, 1, 0, 12, 7}, {3, 1, 14, 2, 6}, {3, -1, 13, 2, 7}, {3, 1, 1, 13, 6}, {3, 1, 1, 14, 7},
-    {4, 1, 10, 0, 5}, {4, 1, 0, 4, 9},  {1, 1, 10, 2, 3}, {1, 1, 0, 3, 8},  {1, 1, 1, 3, 9},
-    {0, 1, 10, 2, 6}, {0, -1, 10, 1, 7}, {0, -1, 2, 7, 9}, {0, -1, 1, 6, 9}, {2, -1, 2, 5, 8},
-    {2, -1, 1, 4, 8}};
-const CubicTerm kQ233[] = {
-    {0, 1, 3, 8, 8},    {1, 1, 10, 10, 3},  {1, 1, 3, 9, 9},    {2, -1, 10, 10, 6},
-    {2, 1, 6, 9, 9},    {3, 1, 4, 8, 9},    {3, 1, 10, 5, 8},   {4, -1, 13, 13, 3},
-    {4, -1, 14, 14, 3}, {5, -1, 14, 7, 9},  {5, -1, 13, 6, 9},  {5, -1, 10, 14, 6},
-    {5, 1, 10, 13, 7},  {6, 1, 10, 7, 9},   {7, -1, 11, 6, 8},  {7, -1, 12, 7, 8},
-    {8, 1, 11, 4, 9},   {8, 1, 12, 5, 9},   {8, 1, 10, 12, 4},  {8, -1, 10, 11, 5},
-    {9, 1, 12, 14, 4},  {9, 1, 11, 14, 5},  {9, 1, 13, 11, 4},  {9, -1, 13, 12, 5}};
-const CubicTerm kQ134[] = {
-    {0, -1, 10, 15, 2}, {0, -1, 1, 15, 9},  {1, 1, 0, 15, 8},   {2, -1, 1, 13, 18},
-    {2, -1, 1, 14, 19}, {2, -1, 2, 14, 18}, {2, 1, 2, 13, 19},  {3, -1, 10, 18, 2},
-    {3, 1, 1, 10, 19},  {3, 1, 1, 18, 9},   {3, 1, 2, 19, 9},   {4, 1, 1, 16, 8},
-    {4, 1, 2, 17, 8},   {5, 1, 0, 10, 17},  {5, 1, 0, 16, 9},   {5, -1, 1, 11, 16},
-    {5, -1, 1, 12, 17}, {5, -1, 2, 12, 16}, {5, 1, 2, 11, 17},  {6, 1, 1, 13, 22},
-    {6, 1, 1, 14, 23},  {6, -1, 2, 14, 22}, {6, 1, 2, 13, 23},  {7, 1, 0, 11, 18},
-    {7, 1, 0, 12, 19},  {8, 1, 0, 13, 20},  {8, 1, 0, 14, 21},  {9, 1, 1, 11, 20},
-    {9, 1, 1, 12, 21},  {9, -1, 2, 12, 20}, {9, 1, 2, 11, 21}};
-// C4B_123 / C4B_233 / C4B_134 (rune/mobius/descriptor.py:107-139).
-const double kC123[] = {-0.008418146349617, -0.016836292699234, -0.033672585398469,
-                        -0.042090731748086, -0.067345170796937, -0.084181463496172,
-                        -0.168362926992344};
-const double kC233[] = {0.008572620635186, 0.009644198214584, 0.019288396429168,
-                        0.025717861905558, 0.026789439484956, 0.032147327381947,
-                        0.038576792858337, 0.128589309527790, 0.192883964291685,
-                        0.321473273819474};
-const double kC134[] = {0.003645164295772, 0.004860219061029, 0.006075273826286,
-                        0.018225821478859, 0.024301095305146, 0.036451642957719,
-                        0.042526916784005, 0.072903285915437, 0.085053833568010,
-                        0.255161500704030};
-
 std::string str(const char *p) { return p ? std::string(p) : std::string(); }
 }  // namespace
 
@@ -182,25 +142,6 @@ static void pack_descriptor(ModelImpl &m, Packer &pk, std::map<std::string, size
     off["c4b"] = pk.put(m.tensor("descriptor.angular.C4B"));
     off["c5b"] = pk.put(m.tensor("descriptor.angular.C5B"));
     off["c4b2"] = pk.put(m.tensor("descriptor.angular.C4B2"));
-    std::vector<float> coef(3 * kMaxCubic, 0.0f);
-    std::vector<float> idxf(3 * kMaxCubic * 3, 0.0f);  // stored as int bits
-    const CubicTerm *lists[3] = {kQ123, kQ233, kQ134};
-    const int counts[3] = {int(sizeof(kQ123) / sizeof(CubicTerm)),
-                           int(sizeof(kQ233) / sizeof(CubicTerm)),
-                           int(sizeof(kQ134) / sizeof(CubicTerm))};
-    const double *cvals[3] = {kC123, kC233, kC134};
-    for (int w = 0; w < 3; ++w) {
-        m.desc.cubic_n[w] = counts[w];
-        for (int k = 0; k < counts[w]; ++k) {
-            const CubicTerm &t = lists[w][k];
-            coef[w * kMaxCubic + k] = float(double(t.sign) * cvals[w][t.coef]);
-            int ids[3] = {t.a, t.b, t.c};
-            for (int q = 0; q < 3; ++q)
-                std::memcpy(&idxf[(w * kMaxCubic + k) * 3 + q], &ids[q], sizeof(int));
-        }
-    }
-    off["cubic_coef"] = pk.put(coef);
-    off["cubic_idx"] = pk.put(idxf);
     if (c.zbl_mode != RUNE_ZBL_NONE) {
         const auto &zn = m.tensor("zbl.atomic_numbers");
         std::vector<float> zp(zn.size());
@@ -305,8 +246,6 @@ static void finalize(ModelImpl &m) {
     d.c4b = P("c4b");
     d.c5b = P("c5b");
     d.c4b2 = P("c4b2");
-    d.cubic_coef = P("cubic_coef");
-    d.cubic_idx = reinterpret_cast<const int *>(P("cubic_idx"));
     ZblTables &z = m.zbl;
     if (m.cfg.zbl_mode != RUNE_ZBL_NONE) {
         z.z = P("zbl_z");
