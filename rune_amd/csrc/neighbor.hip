@@ -12,6 +12,8 @@
 #include <cstring>
 #include <sstream>
 
+#include <type_traits>
+
 #include "nlist.hpp"
 
 #pragma clang fp contract(off)
@@ -202,6 +204,19 @@ __device__ inline void key_shift(uint64_t key, int *S) {
 // 0's insertion sort in global memory.
 constexpr int kWaveKeys = 1024;
 
+// LDS keys per wave for rows of at most `cap` keys (the neighbour limit):
+// rows that cannot exceed 128 or 256 keys take the smaller arrays, which
+// keeps more waves resident per CU; launch(std::integral_constant<int, KW>).
+template <typename F>
+void by_key_lds(int cap, F &&launch) {
+    if (cap <= 128)
+        launch(std::integral_constant<int, 128>{});
+    else if (cap <= 256)
+        launch(std::integral_constant<int, 256>{});
+    else
+        launch(std::integral_constant<int, kWaveKeys>{});
+}
+
 __device__ inline void wave_fence() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -209,8 +224,9 @@ __device__ inline void wave_fence() {
 }
 
 // Counts of centre i (and the overflow flag), then its keys sorted ascending:
-// by rank in LDS when they all fit there (kl holds the first kWaveKeys keys),
+// by rank in LDS when they all fit there (kl holds the first KW keys),
 // else by lane 0's insertion sort in global memory.
+template <int KW>
 __device__ inline void finish_centre(int i, int lane, int cu, int cr, int ca, int max_r, int max_a,
                                      int cap, const uint64_t *kl, uint64_t *out,
                                      int32_t *cnt_union, int32_t *cnt_r, int32_t *cnt_a,
@@ -222,7 +238,7 @@ __device__ inline void finish_centre(int i, int lane, int cu, int cr, int ca, in
         if (cr > max_r || ca > max_a || cu > cap) atomicOr(error_flag, 1);
     }
     if (cu > cap) return;
-    if (cu <= kWaveKeys) {
+    if (cu <= KW) {
         for (int a = lane; a < cu; a += kWave) {
             const uint64_t x = kl[a];
             int rank = 0;
@@ -244,13 +260,14 @@ __device__ inline void finish_centre(int i, int lane, int cu, int cr, int ca, in
     }
 }
 
+template <int KW>
 __global__ void __launch_bounds__(256) enumerate_flat(
     int n, const double *pos, const int32_t *sptr, int nstruct, const Geo *geo,
     const int32_t *atom_wrap, const int32_t *atom_cell, const int32_t *bin_start,
     const int32_t *bin_atoms, double rc2_r, double rc2_a, double rc2_max, int max_r, int max_a,
     int cap, int32_t *cnt_union, int32_t *cnt_r, int32_t *cnt_a, int32_t *error_flag,
     uint64_t *keys) {
-    __shared__ uint64_t kl[4][kWaveKeys];
+    __shared__ uint64_t kl[4][KW];
     __shared__ int cst[4][kWave], cbg[4][kWave], cT[4][kWave][3];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int i = blockIdx.x * 4 + wave;
@@ -333,7 +350,7 @@ __global__ void __launch_bounds__(256) enumerate_flat(
                 const int slot = cu + __popcll(bp & below);
                 const uint64_t key = make_key((in_r && in_a) ? 0 : 1, j, S);
                 if (slot < cap) out[slot] = key;
-                if (slot < kWaveKeys) kl[wave][slot] = key;
+                if (slot < KW) kl[wave][slot] = key;
             }
             cu += __popcll(bp);
             cr += __popcll(__ballot(pass && in_r));
@@ -341,7 +358,7 @@ __global__ void __launch_bounds__(256) enumerate_flat(
         }
         wave_fence();
     }
-    finish_centre(i, lane, cu, cr, ca, max_r, max_a, cap, kl[wave], out, cnt_union, cnt_r, cnt_a,
+    finish_centre<KW>(i, lane, cu, cr, ca, max_r, max_a, cap, kl[wave], out, cnt_union, cnt_r, cnt_a,
                   error_flag);
 }
 
@@ -350,12 +367,13 @@ __global__ void __launch_bounds__(256) enumerate_flat(
 // taken 64 at a time with the same exact fp64 test and key packing as
 // enumerate_flat, so the centre's row of `keys` comes out identical to a
 // fresh enumeration whenever the candidates include every member.
+template <int KW>
 __global__ void __launch_bounds__(256) refilter_wave(
     int n, const double *pos, const int32_t *sptr, int nstruct, const Geo *geo,
     const uint64_t *cand, int capc, const int32_t *cand_cnt, double rc2_r, double rc2_a,
     double rc2_max, int max_r, int max_a, int cap, int32_t *cnt_union, int32_t *cnt_r,
     int32_t *cnt_a, int32_t *error_flag, uint64_t *keys) {
-    __shared__ uint64_t kl[4][kWaveKeys];
+    __shared__ uint64_t kl[4][KW];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int i = blockIdx.x * 4 + wave;
     if (i >= n) return;
@@ -384,14 +402,14 @@ __global__ void __launch_bounds__(256) refilter_wave(
             const int slot = cu + __popcll(bp & below);
             const uint64_t key = make_key((in_r && in_a) ? 0 : 1, j, S);
             if (slot < cap) out[slot] = key;
-            if (slot < kWaveKeys) kl[wave][slot] = key;
+            if (slot < KW) kl[wave][slot] = key;
         }
         cu += __popcll(bp);
         cr += __popcll(__ballot(pass && in_r));
         ca += __popcll(__ballot(pass && in_a));
     }
     wave_fence();
-    finish_centre(i, lane, cu, cr, ca, max_r, max_a, cap, kl[wave], out, cnt_union, cnt_r, cnt_a,
+    finish_centre<KW>(i, lane, cu, cr, ca, max_r, max_a, cap, kl[wave], out, cnt_union, cnt_r, cnt_a,
                   error_flag);
 }
 
@@ -525,18 +543,19 @@ __global__ void fill_in(int64_t e, const int32_t *nbr, const int32_t *tptr, int3
 // Each atom's transposed records in ascending record order, and the centre
 // of each (tctr[t] = ctr[tidx[t]]): one atom per wave, ranked in LDS (record
 // ids are distinct, so each value's rank is the number of smaller ones); an
-// atom with more than kWaveKeys falls back to lane 0's insertion sort in
-// global memory.
+// atom with more than KW falls back to lane 0's insertion sort in global
+// memory.
+template <int KW>
 __global__ void __launch_bounds__(256) sort_in(int n, const int32_t *tptr, int32_t *tidx,
                                                const int32_t *ctr, int32_t *tctr) {
-    __shared__ int32_t kl[4][kWaveKeys];
+    __shared__ int32_t kl[4][KW];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int a = blockIdx.x * 4 + wave;
     if (a >= n) return;
     int32_t *k = tidx + tptr[a];
     int32_t *kc = tctr + tptr[a];
     const int c = tptr[a + 1] - tptr[a];
-    if (c <= kWaveKeys) {
+    if (c <= KW) {
         for (int p = lane; p < c; p += kWave) kl[wave][p] = k[p];
         wave_fence();
         for (int p = lane; p < c; p += kWave) {
@@ -747,9 +766,10 @@ struct Work {
 
 // indeg and cursor: n + 1 counters each, cleared by the caller (inside its
 // one clearing of the builder's counters); `counted`: indeg already holds
-// the in-degrees (counted while the records were written).
+// the in-degrees (counted while the records were written); `cap`: the
+// largest in-degree expected (larger ones take a slower sort, still exact).
 void build_transpose(rune_nlist *nl, int32_t *indeg, int32_t *cursor, int32_t *scan_tmp,
-                     bool counted, hipStream_t s) {
+                     bool counted, int cap, hipStream_t s) {
     int n = int(nl->n_atoms);
     int64_t e = nl->n_records;
     nl->tptr.reserve(sizeof(int32_t) * (n + 1));
@@ -763,9 +783,11 @@ void build_transpose(rune_nlist *nl, int32_t *indeg, int32_t *cursor, int32_t *s
                            nl->nbr.as<int32_t>(), nl->tptr.as<int32_t>(), cursor,
                            nl->tidx.as<int32_t>());
         nl->tctr.reserve(sizeof(int32_t) * std::max<int64_t>(e, 1));
-        hipLaunchKernelGGL(sort_in, dim3(ceil_div(n, 4)), dim3(256), 0, s, n,
-                           nl->tptr.as<int32_t>(), nl->tidx.as<int32_t>(),
-                           nl->ctr.as<int32_t>(), nl->tctr.as<int32_t>());
+        by_key_lds(cap, [&](auto kw) {
+            hipLaunchKernelGGL(sort_in<decltype(kw)::value>, dim3(ceil_div(n, 4)), dim3(256), 0,
+                               s, n, nl->tptr.as<int32_t>(), nl->tidx.as<int32_t>(),
+                               nl->ctr.as<int32_t>(), nl->tctr.as<int32_t>());
+        });
     } else {
         nl->tctr.reserve(sizeof(int32_t));
     }
@@ -953,11 +975,13 @@ static void build_lists(rune_nlist *nl, int64_t n_atoms, const double *d_positio
     }
     if (skin == 0.0) {
         if (n > 0)
-            hipLaunchKernelGGL(enumerate_flat, dim3(ceil_div(n, 4)), dim3(256), 0, s, n,
-                               d_positions, sptr, n_structures, w.geo, w.atom_wrap, w.atom_cell,
-                               w.bin_start, w.bin_atoms, rc2_r, rc2_a, rc2, max_radial,
-                               max_angular, cap, w.cnt_union, w.cnt_r, w.cnt_a, w.flag,
-                               nl->keys.as<uint64_t>());
+            by_key_lds(cap, [&](auto kw) {
+                hipLaunchKernelGGL(enumerate_flat<decltype(kw)::value>, dim3(ceil_div(n, 4)),
+                                   dim3(256), 0, s, n, d_positions, sptr, n_structures, w.geo,
+                                   w.atom_wrap, w.atom_cell, w.bin_start, w.bin_atoms, rc2_r,
+                                   rc2_a, rc2, max_radial, max_angular, cap, w.cnt_union,
+                                   w.cnt_r, w.cnt_a, w.flag, nl->keys.as<uint64_t>());
+            });
     } else {
         if (search) {
             // candidates within rc + skin, all of class 0 (sorted by (j, S));
@@ -967,12 +991,15 @@ static void build_lists(rune_nlist *nl, int64_t n_atoms, const double *d_positio
             for (int attempt = 0;; ++attempt) {
                 nl->cand_keys.reserve(8 * size_t(std::max(n, 1)) * size_t(nl->cand_cap));
                 if (n > 0)
-                    hipLaunchKernelGGL(enumerate_flat, dim3(ceil_div(n, 4)), dim3(256), 0, s, n,
-                                       d_positions, sptr, n_structures, w.geo, w.atom_wrap,
-                                       w.atom_cell, w.bin_start, w.bin_atoms, rb2, rb2, rb2,
-                                       nl->cand_cap, nl->cand_cap, nl->cand_cap,
-                                       nl->cand_cnt.as<int32_t>(), w.cnt_r, w.cnt_a, w.flag,
-                                       nl->cand_keys.as<uint64_t>());
+                    by_key_lds(nl->cand_cap, [&](auto kw) {
+                        hipLaunchKernelGGL(enumerate_flat<decltype(kw)::value>,
+                                           dim3(ceil_div(n, 4)), dim3(256), 0, s, n, d_positions,
+                                           sptr, n_structures, w.geo, w.atom_wrap, w.atom_cell,
+                                           w.bin_start, w.bin_atoms, rb2, rb2, rb2, nl->cand_cap,
+                                           nl->cand_cap, nl->cand_cap,
+                                           nl->cand_cnt.as<int32_t>(), w.cnt_r, w.cnt_a, w.flag,
+                                           nl->cand_keys.as<uint64_t>());
+                    });
                 RUNE_HIP_CHECK(hipGetLastError());
                 int32_t over = 0;
                 RUNE_HIP_CHECK(hipMemcpyAsync(&over, w.flag, 4, hipMemcpyDeviceToHost, s));
@@ -993,12 +1020,14 @@ static void build_lists(rune_nlist *nl, int64_t n_atoms, const double *d_positio
                                               hipMemcpyDeviceToDevice, s));
         }
         if (n > 0)
-            hipLaunchKernelGGL(refilter_wave, dim3(ceil_div(n, 4)), dim3(256), 0, s, n,
-                               d_positions, sptr, n_structures, w.geo,
-                               nl->cand_keys.as<uint64_t>(), nl->cand_cap,
-                               nl->cand_cnt.as<int32_t>(), rc2_r, rc2_a, rc2, max_radial,
-                               max_angular, cap, w.cnt_union, w.cnt_r, w.cnt_a, w.flag,
-                               nl->keys.as<uint64_t>());
+            by_key_lds(cap, [&](auto kw) {
+                hipLaunchKernelGGL(refilter_wave<decltype(kw)::value>, dim3(ceil_div(n, 4)),
+                                   dim3(256), 0, s, n, d_positions, sptr, n_structures, w.geo,
+                                   nl->cand_keys.as<uint64_t>(), nl->cand_cap,
+                                   nl->cand_cnt.as<int32_t>(), rc2_r, rc2_a, rc2, max_radial,
+                                   max_angular, cap, w.cnt_union, w.cnt_r, w.cnt_a, w.flag,
+                                   nl->keys.as<uint64_t>());
+            });
     }
     exclusive_scan(w.cnt_union, nl->ptr.as<int32_t>(), n, w.scan_tmp, s);
     int32_t *words = nl->readback.get();
@@ -1030,7 +1059,7 @@ static void build_lists(rune_nlist *nl, int64_t n_atoms, const double *d_positio
                            nl->ctr.as<int32_t>(), w.indeg);
     }
     RUNE_HIP_CHECK(hipGetLastError());
-    build_transpose(nl, w.indeg, tcur, w.scan_tmp, true, s);
+    build_transpose(nl, w.indeg, tcur, w.scan_tmp, true, cap, s);
     // processing order: atoms bin by bin, bins in Morton order (kept from the
     // last binning when the candidates are reused; it only orders the work,
     // so a list of fewer than kOrderMinAtoms atoms, which fits in L2 either
@@ -1211,7 +1240,7 @@ extern "C" int rune_nlist_from_padded(rune_nlist *nl, int64_t n_atoms, const flo
                                nl->shift.as<int32_t>(), nl->vec.as<float4>(),
                                nl->ctr.as<int32_t>());
         RUNE_HIP_CHECK(hipGetLastError());
-        build_transpose(nl, indeg, tcur, scan_tmp, false, s);
+        build_transpose(nl, indeg, tcur, scan_tmp, false, kWaveKeys, s);
         if (n_records) *n_records = e;
     });
 }
