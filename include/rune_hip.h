@@ -268,11 +268,15 @@ int rune_model_descriptor_extrema(rune_model *model, const rune_nlist *nl,
 /* Bytes of device workspace the handle currently holds. */
 int64_t rune_model_workspace_bytes(const rune_model *model);
 
-/* Phase timing.  When enabled, rune_model_compute records a HIP event on its
- * stream at every phase boundary (no synchronisation inside the call; the last
- * 256 calls are kept).  rune_model_timing_read waits for those events and
- * returns the summed milliseconds per phase and the number of calls.
- * (No counterpart in the reference; it feeds the roofline measurement.) */
+/* Phase timing.  rune_model_timing(model, mode): mode 1 makes
+ * rune_model_compute record a HIP event on its stream at every phase boundary
+ * (no synchronisation inside the call; the last 256 calls are kept) and
+ * bracket every kernel-group launch (below); mode 2 brackets the group
+ * launches only (no phase events, so a timed loop carries no per-phase
+ * instrumentation); mode 0 turns both off.  rune_model_timing_read waits for
+ * the phase events and returns the summed milliseconds per phase and the
+ * number of calls.  (No counterpart in the reference; it feeds the roofline
+ * measurement.) */
 enum {
     RUNE_PHASE_DESCRIPTOR = 0,   /* K2 descriptor forward                       */
     RUNE_PHASE_DENSE_FWD = 1,    /* input projection + residual blocks           */
@@ -288,7 +292,7 @@ int rune_model_timing(rune_model *model, int32_t enable);
 int rune_model_timing_read(rune_model *model, double *ms_per_phase, int64_t *calls);
 
 /* Kernel-group timing (no counterpart in the reference; it feeds the roofline
- * measurement).  While timing is enabled, every launch of a group is bracketed
+ * measurement).  While timing is on (mode 1 or 2), every launch of a group is bracketed
  * by two HIP events on the launch stream.  rune_model_timing_groups waits for
  * them and returns, per group, the summed milliseconds and the number of
  * launches since timing was enabled. */

@@ -423,8 +423,9 @@ class NativeModel:
     PHASES = ("descriptor", "dense_fwd", "message_fwd", "readout", "message_bwd", "dense_bwd",
               "reverse", "forces")
 
-    def timing(self, enable=True):
-        check(library().rune_model_timing(self._h, int(enable)))
+    def timing(self, enable=True, phases=True):
+        """Kernel-group spans (and, with ``phases``, per-phase events) on or off."""
+        check(library().rune_model_timing(self._h, 0 if not enable else (1 if phases else 2)))
 
     def timing_read(self):
         """Summed milliseconds per phase over the recorded calls, and the call count."""

@@ -402,7 +402,7 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
         return;
     }
     hipEvent_t *ev = nullptr;
-    if (m.timing && !fixed) {
+    if (m.timing == 1 && !fixed) {
         if (m.events.empty()) {
             m.events.resize(size_t(kTimingRing) * (RUNE_N_PHASES + 1));
             for (auto &e : m.events) RUNE_HIP_CHECK(hipEventCreate(&e));
@@ -469,7 +469,7 @@ ModelImpl::~ModelImpl() {
 }
 
 int ModelImpl::span_begin(int group, hipStream_t s) {
-    if (!timing || span_n >= kMaxSpans) return -1;
+    if (timing == 0 || span_n >= kMaxSpans) return -1;
     while (span_ev.size() < 2 * (span_n + 1)) {
         hipEvent_t e;
         RUNE_HIP_CHECK(hipEventCreate(&e));
@@ -734,8 +734,8 @@ extern "C" int rune_model_compute_static(rune_model *model, const rune_nlist *nl
         // no timing events here (creating them is a runtime allocation)
         struct Untimed {
             ModelImpl &m;
-            bool was;
-            explicit Untimed(ModelImpl &x) : m(x), was(x.timing) { m.timing = false; }
+            int was;
+            explicit Untimed(ModelImpl &x) : m(x), was(x.timing) { m.timing = 0; }
             ~Untimed() { m.timing = was; }
         } untimed(*model);
         compute(*model, nl, d_types, compute_forces, compute_virial, d_energies, d_energy,
@@ -876,7 +876,8 @@ extern "C" int64_t rune_model_workspace_bytes(const rune_model *model) {
 extern "C" int rune_model_timing(rune_model *model, int32_t enable) {
     return guarded([&] {
         RUNE_REQUIRE(model, RUNE_ERR_ARGUMENT, "null model");
-        model->timing = enable != 0;
+        RUNE_REQUIRE(enable >= 0 && enable <= 2, RUNE_ERR_ARGUMENT, "timing mode is 0, 1 or 2");
+        model->timing = enable;
         model->timed_calls = 0;
         model->span_n = 0;
     });

@@ -127,7 +127,7 @@ struct ModelImpl {
     hipEvent_t type_event = nullptr;
     bool type_pending = false;   // type_event recorded, verdict not yet read
     // phase timing ring (events recorded on the launch stream)
-    bool timing = false;
+    int timing = 0;   // 0 off, 1 phase events and kernel-group spans, 2 spans only
     std::vector<hipEvent_t> events;       // kTimingRing x (RUNE_N_PHASES + 1)
     int64_t timed_calls = 0;
     // kernel-group spans: events 2k, 2k + 1 bracket launch k of group span_grp[k]

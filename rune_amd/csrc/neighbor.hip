@@ -680,6 +680,8 @@ Geo make_geo(const double *cell_in, const int32_t *pbc, double rc, double *th) {
     return g;
 }
 
+constexpr double kDenseBin = 12.0;
+
 // Bin frame of one structure.  Periodic directions tile the cell with nb
 // bins; open directions cover exactly the bins that hold atoms, from the
 // extent [flo, fhi] of the atoms' fractional coordinates (an atom outside
@@ -690,6 +692,16 @@ Geo make_geo(const double *cell_in, const int32_t *pbc, double rc, double *th) {
 void fit_bins(Geo &g, const double *th, double rc, int n_atoms, const double *flo,
               const double *fhi, int bin_offset, int atom_begin) {
     const int64_t cap = std::max<int64_t>(64, 4 * int64_t(n_atoms));
+    // dense periodic cells (on average kDenseBin atoms or more per bin of the
+    // cutoff's width) take bins of half that width: the 5x5x5 stencil then
+    // proposes about 1.7x fewer candidates than the 3x3x3 one
+    if (g.pbc[0] && g.pbc[1] && g.pbc[2] &&
+        double(n_atoms) >= kDenseBin * double(g.nb[0]) * double(g.nb[1]) * double(g.nb[2])) {
+        for (int d = 0; d < 3; ++d) {
+            const double nb = std::floor(2.0 * th[d] / (rc * (1.0 + 1e-9)));
+            g.nb[d] = int(std::max(1.0, std::min(nb, 1024.0)));
+        }
+    }
     for (;;) {
         double total = 1.0;
         for (int d = 0; d < 3; ++d) {
