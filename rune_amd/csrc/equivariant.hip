@@ -345,6 +345,7 @@ __device__ inline float lane_get(float v, int q) {
 
 // Radial-basis weights held in registers; a longer basis reads the rest from L2.
 constexpr int kRbRegs = 17;
+constexpr int kRcStride = 20;   // LDS row of a record's radial basis when ldrb <= 20
 
 template <int DMC>
 struct EdgeCols {
@@ -431,9 +432,18 @@ __device__ inline void stage_record(const EqArgs &a, int e, float *Yc, float *Rc
 #pragma unroll
     for (int k = 0; k < NQ; ++k) Yc[q * LY + k] = y[k];
     if (Rc) {
+        // rows of kRcStride floats (zero past ldrb) when the basis fits, so
+        // the readers use constant offsets; else rows of ldrb
         const float4 *rb = reinterpret_cast<const float4 *>(a.rb + size_t(e) * a.ldrb);
-        for (int k = 0; k < a.ldrb / 4; ++k)
-            reinterpret_cast<float4 *>(Rc + q * a.ldrb)[k] = rb[k];
+        if (a.ldrb <= kRcStride) {
+#pragma unroll
+            for (int k = 0; k < kRcStride / 4; ++k)
+                reinterpret_cast<float4 *>(Rc + q * kRcStride)[k] =
+                    4 * k < a.ldrb ? rb[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        } else {
+            for (int k = 0; k < a.ldrb / 4; ++k)
+                reinterpret_cast<float4 *>(Rc + q * a.ldrb)[k] = rb[k];
+        }
     }
 }
 
@@ -470,6 +480,7 @@ __global__ void __launch_bounds__(kBlock) k_eq_edge_nbr(EqArgs a) {
 #pragma unroll
     for (int u = 0; u < DMC; ++u) Bj[u] = a.node[size_t(j) * a.NP + D + col.dl[u]];
     const int tb = a.r.tptr[j], te = a.r.tptr[j + 1];
+    const bool fixed_rc = LR <= kRcStride;
     for (int t0 = tb; t0 < te; t0 += kWave) {
         const int cnt = min(kWave, te - t0);
         int me = 0, mp = 0;
@@ -497,22 +508,55 @@ __global__ void __launch_bounds__(kBlock) k_eq_edge_nbr(EqArgs a) {
             float acc[DMC];
 #pragma unroll
             for (int u = 0; u < DMC; ++u) acc[u] = 0.0f;
+            if constexpr (NQ % 4 == 0) {
+                // 16-byte rows (LY = NQ + 4), constant offsets
+                const float4 *y4 = reinterpret_cast<const float4 *>(Yc + q * LY);
 #pragma unroll
-            for (int k = 0; k < NQ; ++k) {
-                const float y = Yc[q * LY + k];
+                for (int k4 = 0; k4 < NQ / 4; ++k4) {
+                    const float4 y = y4[k4];
 #pragma unroll
-                for (int u = 0; u < DMC; ++u) acc[u] += y * Q[k][u];
+                    for (int u = 0; u < DMC; ++u) {
+                        acc[u] += y.x * Q[4 * k4][u];
+                        acc[u] += y.y * Q[4 * k4 + 1][u];
+                        acc[u] += y.z * Q[4 * k4 + 2][u];
+                        acc[u] += y.w * Q[4 * k4 + 3][u];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < NQ; ++k) {
+                    const float y = Yc[q * LY + k];
+#pragma unroll
+                    for (int u = 0; u < DMC; ++u) acc[u] += y * Q[k][u];
+                }
             }
+            if (fixed_rc) {
+                const float *rq = Rc + q * kRcStride;
 #pragma unroll
-            for (int k = 0; k < kRbRegs; ++k) {
-                const float r = Rc[q * LR + min(k, LR - 1)];
+                for (int k = 0; k < kRbRegs; ++k) {
+                    const float r = rq[k];
 #pragma unroll
-                for (int u = 0; u < DMC; ++u) acc[u] += r * wr[k][u];
-            }
-            for (int k = kRbRegs; k < kb; ++k) {
-                const float r = Rc[q * LR + k];
+                    for (int u = 0; u < DMC; ++u) acc[u] += r * wr[k][u];
+                }
+                for (int k = kRbRegs; k < kb; ++k) {
+                    const float r = rq[k];
 #pragma unroll
-                for (int u = 0; u < DMC; ++u) acc[u] += r * a.wrb[size_t(k) * D + col.dl[u]];
+                    for (int u = 0; u < DMC; ++u)
+                        acc[u] += r * a.wrb[size_t(k) * D + col.dl[u]];
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < kRbRegs; ++k) {
+                    const float r = Rc[q * LR + min(k, LR - 1)];
+#pragma unroll
+                    for (int u = 0; u < DMC; ++u) acc[u] += r * wr[k][u];
+                }
+                for (int k = kRbRegs; k < kb; ++k) {
+                    const float r = Rc[q * LR + k];
+#pragma unroll
+                    for (int u = 0; u < DMC; ++u)
+                        acc[u] += r * a.wrb[size_t(k) * D + col.dl[u]];
+                }
             }
             const bool on = lane_get(mf, q) != 0.0f;
 #pragma unroll
@@ -2037,7 +2081,7 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
                 // per-wave record rows, or (prologue) the state rows plus one
                 // order's weight chunk
                 const int pro = ceil_div(kWaves * cn4 + C * kWave * dmc, kWaves);
-                a.wlds = std::max({cn4, kWave * (ly + p.ldrb), pro});
+                a.wlds = std::max({cn4, kWave * (ly + std::max(p.ldrb, kRcStride)), pro});
                 const size_t lds_n = sizeof(float) * kWaves * a.wlds;
                 EQ_LAUNCH_D(k_eq_edge_nbr, lq, dmc, egrid, dim3(kBlock), lds_n, s, a);
             }
