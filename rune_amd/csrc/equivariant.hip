@@ -75,7 +75,7 @@ struct EqArgs {
     const float *mixw;        // [lq, C, C]
     float *mixst;             // [N, C*nq] channel-mixed dir_in
     int act;                  // activation of the edge MLP
-    int wlds;                 // LDS floats per wave of the edge-MLP kernels
+    int wlds;                 // LDS floats per wave of the edge-MLP kernels (multiple of 4)
     const int32_t *pair;      // [E] pair type index
     const float *pair_proj;   // [T*T, D]
     const float *wpc, *wpn;   // [lq*C, D] probe weights (neighbour side signed)
@@ -177,6 +177,26 @@ __device__ inline void load_row(float (&v)[NQ], const float *__restrict__ p) {
     } else {
 #pragma unroll
         for (int k = 0; k < NQ; ++k) v[k] = p[k];
+    }
+}
+
+// Row r of a staged record array (row stride LY floats, 16-byte aligned rows
+// when NQ % 4 == 0) into registers: 16-byte LDS reads at constant offsets.
+template <int NQ, int LY>
+__device__ inline void lds_row(float (&v)[NQ], const float *base, int r) {
+    if constexpr (NQ % 4 == 0 && LY % 4 == 0) {
+        const float4 *p = reinterpret_cast<const float4 *>(base + r * LY);
+#pragma unroll
+        for (int q = 0; q < NQ / 4; ++q) {
+            const float4 t = p[q];
+            v[4 * q] = t.x;
+            v[4 * q + 1] = t.y;
+            v[4 * q + 2] = t.z;
+            v[4 * q + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) v[k] = base[r * LY + k];
     }
 }
 
@@ -618,11 +638,13 @@ __global__ void __launch_bounds__(kBlock) k_eq_edge_centre(EqArgs a) {
             float acc[DMC];
 #pragma unroll
             for (int u = 0; u < DMC; ++u) acc[u] = 0.0f;
+            {
+                float y[NQ];
+                lds_row<NQ, LY>(y, Yc, q);
 #pragma unroll
-            for (int k = 0; k < NQ; ++k) {
-                const float y = Yc[q * LY + k];
+                for (int k = 0; k < NQ; ++k)
 #pragma unroll
-                for (int u = 0; u < DMC; ++u) acc[u] += y * Q[k][u];
+                    for (int u = 0; u < DMC; ++u) acc[u] += y[k] * Q[k][u];
             }
             const bool on = lane_get(mf, q) != 0.0f;
 #pragma unroll
@@ -706,8 +728,7 @@ __global__ void __launch_bounds__(kBlock, 2) k_eq_aggregate(EqArgs a) {
             if (fc != 0.0f) {
                 if (ln.act) {
                     float Y[NQ];
-#pragma unroll
-                    for (int k = 0; k < NQ; ++k) Y[k] = Yc[(q0 + ln.slot) * LY + k];
+                    lds_row<NQ, LY>(Y, Yc, q0 + ln.slot);
 #pragma unroll
                     for (int L = 1; L <= LQ; ++L)
 #pragma unroll
@@ -881,8 +902,7 @@ __global__ void __launch_bounds__(kBlock) k_eq_pair_dir(EqArgs a) {
                 float *dg = a.dgg + size_t(e) * NG + G + ln.c;
                 if (on) {
                     float Y[NQ];
-#pragma unroll
-                    for (int k = 0; k < NQ; ++k) Y[k] = Yc[q * LY + k];
+                    lds_row<NQ, LY>(Y, Yc, q);
 #pragma unroll
                     for (int L = 1; L <= LQ; ++L) {
                         const int st = L * L - 1;
@@ -2081,14 +2101,15 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
                 // per-wave record rows, or (prologue) the state rows plus one
                 // order's weight chunk
                 const int pro = ceil_div(kWaves * cn4 + C * kWave * dmc, kWaves);
-                a.wlds = std::max({cn4, kWave * (ly + std::max(p.ldrb, kRcStride)), pro});
+                // a multiple of 4 floats: the record rows are read as 16-byte vectors
+                a.wlds = (std::max({cn4, kWave * (ly + std::max(p.ldrb, kRcStride)), pro}) + 3) & ~3;
                 const size_t lds_n = sizeof(float) * kWaves * a.wlds;
                 EQ_LAUNCH_D(k_eq_edge_nbr, lq, dmc, egrid, dim3(kBlock), lds_n, s, a);
             }
             {
                 Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
                 const int pro = ceil_div(kWaves * cn4 + C * kWave * dmc, kWaves);
-                a.wlds = std::max({cn4, kWave * ly, pro});
+                a.wlds = (std::max({cn4, kWave * ly, pro}) + 3) & ~3;
                 const size_t lds_c = sizeof(float) * kWaves * a.wlds;
                 EQ_LAUNCH_D(k_eq_edge_centre, lq, dmc, egrid, dim3(kBlock), lds_c, s, a);
             }
