@@ -80,7 +80,13 @@ __device__ inline void store_stage(const float4 (&r)[kRows * 8 / 256], float *S,
 // embedding, residual, gathered rows; then the pre-activation store, the
 // activation (act2 from column act_split on) and the activation derivative.
 // Out-of-range elements load from clamped indices and store nothing.
-template <int WM, int WN, int WMW>
+// EK selects the activation at compile time for the common epilogues (the
+// others keep the run-time choice): kEpiGate sigmoid before column act_split
+// and tanh from it (the gate logits), kEpiSilu SiLU, kEpiDsilu the product
+// with SiLU'(U) and no activation.
+constexpr int kEpiAny = 0, kEpiGate = 1, kEpiSilu = 2, kEpiDsilu = 3;
+
+template <int WM, int WN, int WMW, int EK = kEpiAny>
 __device__ inline void tile_epilogue(floatx4 (&acc)[WM][WN], int M, int N,
                                      float *__restrict__ C, int ldc, const Epilogue &ep,
                                      int m0, int n0) {
@@ -125,11 +131,23 @@ __device__ inline void tile_epilogue(floatx4 (&acc)[WM][WN], int M, int N,
                 if (row >= M || col >= N) continue;
                 float t = x[a][v][b];
                 if (ep.pre) ep.pre[size_t(row) * ep.ldp + col] = t;
-                if (ep.act_split >= 0 && col >= ep.act_split)
-                    t = act_f(ep.act2, t);
-                else if (ep.act >= 0)
-                    t = act_f(ep.act, t);
-                if (ep.dact_from) t *= act_d(ep.dact, du[a][v][b]);
+                if constexpr (EK == kEpiGate) {
+                    // tanh(t) = 2 sigmoid(2t) - 1: one logistic per element
+                    const bool th = col >= ep.act_split;
+                    const float sg = sigmoid_fast(th ? 2.0f * t : t);
+                    t = th ? 2.0f * sg - 1.0f : sg;
+                } else if constexpr (EK == kEpiSilu) {
+                    t = t * sigmoid_fast(t);
+                } else if constexpr (EK == kEpiDsilu) {
+                    const float uu = du[a][v][b], sg = sigmoid_fast(uu);
+                    t *= sg * (1.0f + uu * (1.0f - sg));
+                } else {
+                    if (ep.act_split >= 0 && col >= ep.act_split)
+                        t = act_f(ep.act2, t);
+                    else if (ep.act >= 0)
+                        t = act_f(ep.act, t);
+                    if (ep.dact_from) t *= act_d(ep.dact, du[a][v][b]);
+                }
                 C[size_t(row) * ldc + col] = t;
             }
         }
@@ -146,7 +164,7 @@ __device__ inline void tile_epilogue(floatx4 (&acc)[WM][WN], int M, int N,
 // Batched launches (gridDim.y > 1) offset A, C by z times their batch strides
 // and Bt by sb times z, or times L(z) - 1 (L the harmonic order of component z)
 // when the batches share one weight block per order.
-template <int WM, int WN, int WMW, bool kVec, bool kActA = false>
+template <int WM, int WN, int WMW, bool kVec, bool kActA = false, int EK = kEpiAny>
 __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *__restrict__ A,
                                               int lda, const float *__restrict__ Bt, int ldb,
                                               float *__restrict__ C, int ldc, Epilogue ep,
@@ -226,7 +244,7 @@ __global__ void __launch_bounds__(256) k_gemm(int M, int N, int K, const float *
         }
         __syncthreads();
     }
-    tile_epilogue<WM, WN, WMW>(acc, M, N, C, ldc, ep, m0, n0);
+    tile_epilogue<WM, WN, WMW, EK>(acc, M, N, C, ldc, ep, m0, n0);
 }
 
 // One output element of the fused epilogue (the terms of tile_epilogue in the
@@ -483,7 +501,28 @@ static void launch_gemm(bool vec, int M, int N, int K, const float *A, int lda, 
     if (blocks > 0x7fffffff || bt.count > 65535)
         throw Error(RUNE_ERR_ARGUMENT, "gemm: problem too large");
     const dim3 grid(unsigned(blocks), unsigned(bt.count));
-    if (vec && ep.a_act >= 0)
+    // compile-time activation for the common epilogues (vector operands,
+    // activation not applied to A)
+    int ek = kEpiAny;
+    if (ep.a_act < 0 && vec) {
+        if (ep.act == kActSigmoid && ep.act_split >= 0 && ep.act2 == RUNE_ACT_TANH &&
+            !ep.dact_from)
+            ek = kEpiGate;
+        else if (ep.act == RUNE_ACT_SILU && ep.act_split < 0 && !ep.dact_from)
+            ek = kEpiSilu;
+        else if (ep.act < 0 && ep.act_split < 0 && ep.dact_from && ep.dact == RUNE_ACT_SILU)
+            ek = kEpiDsilu;
+    }
+    if (ek == kEpiGate)
+        hipLaunchKernelGGL((k_gemm<WM, WN, WMW, true, false, kEpiGate>), grid, dim3(256), 0, s,
+                           M, N, K, A, lda, Bt, ldb, C, ldc, ep, nbn, bt);
+    else if (ek == kEpiSilu)
+        hipLaunchKernelGGL((k_gemm<WM, WN, WMW, true, false, kEpiSilu>), grid, dim3(256), 0, s,
+                           M, N, K, A, lda, Bt, ldb, C, ldc, ep, nbn, bt);
+    else if (ek == kEpiDsilu)
+        hipLaunchKernelGGL((k_gemm<WM, WN, WMW, true, false, kEpiDsilu>), grid, dim3(256), 0, s,
+                           M, N, K, A, lda, Bt, ldb, C, ldc, ep, nbn, bt);
+    else if (vec && ep.a_act >= 0)
         hipLaunchKernelGGL((k_gemm<WM, WN, WMW, true, true>), grid, dim3(256), 0, s, M, N, K, A,
                            lda, Bt, ldb, C, ldc, ep, nbn, bt);
     else if (ep.a_act >= 0)
