@@ -647,11 +647,21 @@ __global__ void __launch_bounds__(kBlock) k_eq_edge_centre(EqArgs a) {
                     for (int u = 0; u < DMC; ++u) acc[u] += y[k] * Q[k][u];
             }
             const bool on = lane_get(mf, q) != 0.0f;
+            float v[DMC], h[DMC];
+#pragma unroll
+            for (int u = 0; u < DMC; ++u) v[u] = (A[u] + X[0][u]) + (on ? acc[u] : 0.0f);
+            // one uniform branch per record for the activation (SiLU inline)
+            if (act == RUNE_ACT_SILU) {
+#pragma unroll
+                for (int u = 0; u < DMC; ++u) h[u] = v[u] * sigmoid_fast(v[u]);
+            } else {
+#pragma unroll
+                for (int u = 0; u < DMC; ++u) h[u] = act_f(act, v[u]);
+            }
 #pragma unroll
             for (int u = 0; u < DMC; ++u) {
-                const float v = (A[u] + X[0][u]) + (on ? acc[u] : 0.0f);
-                a.ue[size_t(e) * ldd + col.d[u]] = v;
-                a.eh[size_t(e) * ldd + col.d[u]] = act_f(act, v);
+                a.ue[size_t(e) * ldd + col.d[u]] = v[u];
+                a.eh[size_t(e) * ldd + col.d[u]] = h[u];
             }
 #pragma unroll
             for (int f = 0; f + 1 < kPf; ++f) copy(X[f], X[f + 1]);
