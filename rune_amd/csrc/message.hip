@@ -824,8 +824,11 @@ __device__ inline void mp_edge_u(const MpEdgeArgs &a, const float *Wx, const MpT
     }
 }
 
+// Register budgets measured on C3: the forward at 4 waves per SIMD (no
+// spill) and the reverse at 3 (four spilled registers) beat the compiler's
+// unbounded choices (3 and 2 waves); the reverse at 4 spills 60 and loses.
 template <int DB, int GB, int ACT>
-__global__ void __launch_bounds__(256) k_mp_edge_forward(MpEdgeArgs a) {
+__global__ void __launch_bounds__(256, 4) k_mp_edge_forward(MpEdgeArgs a) {
     extern __shared__ float lds[];
     float *Wx = lds;                      // [D][KP]
     float *Wg = Wx + a.D * a.KP;          // [16 GB][D], zero rows past NG
@@ -873,7 +876,7 @@ __global__ void __launch_bounds__(256) k_mp_edge_forward(MpEdgeArgs a) {
 }
 
 template <int DB, int GB, int ACT>
-__global__ void __launch_bounds__(256) k_mp_edge_reverse(MpEdgeArgs a) {
+__global__ void __launch_bounds__(256, 3) k_mp_edge_reverse(MpEdgeArgs a) {
     extern __shared__ float lds[];
     float *Wx = lds;                      // [D][KP]
     float *WgT = Wx + a.D * a.KP;         // [D][16 GB], zero columns past NG
