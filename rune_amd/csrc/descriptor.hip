@@ -247,6 +247,7 @@ __device__ float invariant_grad_one(const DescTables &t, const float *s, const f
 // lane for the order and four/five-body invariants, then one channel per
 // lane for the cubic invariants (their unrolled term lists read the moments
 // from registers and update the row at constant offsets).
+template <bool kRegCubic = false>
 __device__ void invariant_gradient_all(const DescTables &t, const float *sL, const float *dq,
                                        float *WL, int lane) {
     const int na = t.na, nlm = t.nlm;
@@ -259,11 +260,21 @@ __device__ void invariant_gradient_all(const DescTables &t, const float *sL, con
     for (int n = lane; n < na; n += kWave) {
         float sr[kCubicComps];
         cubic_moments(sL + n * nlm, nlm, sr);
-        float *w = WL + n * nlm;
+        // kRegCubic: accumulate in registers (no LDS read-modify-write chain,
+        // more registers: the variant for grids too small to fill the chip)
+        float wr[kCubicComps];
+#pragma unroll
+        for (int c = 0; c < kCubicComps; ++c) wr[c] = 0.0f;
+        float *w = kRegCubic ? wr : WL + n * nlm;
         int idx = t.l_max + t.has_q[0] + t.has_q[1] + t.has_q[2];
         if (t.has_q[3]) cubic_grad<0>(sr, dq[n + na * idx++], w, nlm);
         if (t.has_q[4]) cubic_grad<1>(sr, dq[n + na * idx++], w, nlm);
         if (t.has_q[5]) cubic_grad<2>(sr, dq[n + na * idx++], w, nlm);
+        if constexpr (kRegCubic) {
+#pragma unroll
+            for (int c = 0; c < kCubicComps; ++c)
+                if (c < nlm) WL[n * nlm + c] += wr[c];
+        }
     }
 }
 
@@ -411,7 +422,7 @@ __device__ inline void zbl_pair(const ZblTables &z, int ti, int tj, float d, flo
     de = 0.5f * (dscr * cut + scr * dcut);
 }
 
-template <int KR, int KA, int NA>
+template <int KR, int KA, int NA, bool kRegCubic = false>
 __global__ void __launch_bounds__(kWave) k_descriptor_reverse(
     DescTables t, ZblTables z, Records r, const int32_t *types, const float *dq, int ldq,
     const float *moments, const float *dmom, const float4 *g_direct, float *energies,
@@ -434,7 +445,7 @@ __global__ void __launch_bounds__(kWave) k_descriptor_reverse(
             WL[o] = dmom ? dmom[size_t(i) * nout + o] : 0.0f;
         }
         __syncthreads();
-        invariant_gradient_all(t, sL, dqL + t.nr, WL, lane);
+        invariant_gradient_all<kRegCubic>(t, sL, dqL + t.nr, WL, lane);
         __syncthreads();
     }
     float zsum = 0.0f;
@@ -832,6 +843,10 @@ bool descriptor_fits_registers(const DescTables &t) {
 // of 140 / 145, so 7 / 5 waves per SIMD instead of 3) for the models that
 // fit them, the OAM and NEP models among them.
 constexpr int kCompactKr = 20, kCompactKa = 16, kCompactNa = 12, kCompactOut = 5;
+// Up to this many centres (a few waves per SIMD at most) the reverse kernel
+// keeps the cubic-invariant gradients in registers: its wave latency is the
+// kernel time there, and the extra registers cost nothing.
+constexpr int kSmallDescAtoms = 8192;
 bool descriptor_compact(const DescTables &t) {
     return t.nr <= kMaxNr && t.kr <= kCompactKr && t.ka <= kCompactKa && t.na <= kCompactNa &&
            t.na * t.nlm <= kCompactOut * kWave;
@@ -886,7 +901,11 @@ void descriptor_reverse(const DescTables &t, const ZblTables &z, const Records &
         return;
     }
     size_t lds = sizeof(float) * (t.Q + 2 * t.na * t.nlm);
-    if (descriptor_compact(t))
+    if (descriptor_compact(t) && r.n_atoms <= kSmallDescAtoms)
+        hipLaunchKernelGGL((k_descriptor_reverse<kCompactKr, kCompactKa, kCompactNa, true>),
+                           dim3(r.n_atoms), dim3(kWave), lds, s, t, z, r, types, dq, ldq, moments,
+                           dmom, g_direct, energies, g, want_grad);
+    else if (descriptor_compact(t))
         hipLaunchKernelGGL((k_descriptor_reverse<kCompactKr, kCompactKa, kCompactNa>),
                            dim3(r.n_atoms), dim3(kWave), lds, s, t, z, r, types, dq, ldq, moments,
                            dmom, g_direct, energies, g, want_grad);
