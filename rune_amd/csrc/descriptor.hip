@@ -281,15 +281,15 @@ __device__ void invariant_gradient_all(const DescTables &t, const float *sL, con
 // KR / KA: basis values of a lane's record, NR: radial channels, NO: moment
 // outputs per lane (register arrays sized for the model, so the compact
 // instantiation keeps occupancy up).
-template <int KR, int KA, int NR, int NO>
+template <int KR, int KA, int NR, int NO, int CH = kWave>
 __global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Records r,
                                                               const int32_t *types, float *q,
                                                               int ldq, float *moments) {
     extern __shared__ float lds[];
     const int nlm = t.nlm, na = t.na, nout = na * nlm;
-    float *gnL = lds;                          // [64][na+1]
-    float *bL = gnL + kWave * (na + 1);        // [64][nlm+1]
-    float *sL = bL + kWave * (nlm + 1);        // [na*nlm]
+    float *gnL = lds;                          // [CH][na+1]
+    float *bL = gnL + CH * (na + 1);           // [CH][nlm+1]
+    float *sL = lds;                           // [na*nlm], after the record rounds
     const int i = blockIdx.x;
     const int lane = threadIdx.x;
     const int ti = types[i];
@@ -319,15 +319,16 @@ __global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Reco
         if (lane == 0) q[size_t(i) * ldq + n] = v;
     }
 
-    // angular moments s[n][lm] = sum_e gn[e][n] b[e][lm]
+    // angular moments s[n][lm] = sum_e gn[e][n] b[e][lm], CH records (lanes)
+    // per round
     float acc[NO];
 #pragma unroll
     for (int j = 0; j < NO; ++j) acc[j] = 0.0f;
-    for (int base = ab; base < ae; base += kWave) {
+    for (int base = ab; base < ae; base += CH) {
         int e = base + lane;
         float *gl = gnL + lane * (na + 1);
         float *bl = bL + lane * (nlm + 1);
-        if (e < ae) {
+        if (lane < CH && e < ae) {
             float4 v = r.vec[e];
             int tj = types[r.nbr[e]];
             float f[KA] = {};
@@ -351,12 +352,12 @@ __global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Reco
                     }
                 }
             }
-        } else {
+        } else if (lane < CH) {
             for (int n = 0; n < na; ++n) gl[n] = 0.0f;
             for (int c = 0; c < nlm; ++c) bl[c] = 0.0f;
         }
         __syncthreads();
-        int cnt = min(kWave, ae - base);
+        int cnt = min(CH, ae - base);
 #pragma unroll
         for (int j = 0; j < NO; ++j) {
             int o = lane + kWave * j;
@@ -860,8 +861,8 @@ static void allow_lds(const void *kernel, size_t lds) {
                                            int(lds)));
 }
 
-void descriptor_forward(const DescTables &t, const Records &r, const int32_t *types, float *q,
-                        int ldq, float *moments, hipStream_t s) {
+void descriptor_forward(const DescTables &t, const Records &r, int64_t n_records,
+                        const int32_t *types, float *q, int ldq, float *moments, hipStream_t s) {
     if (r.n_atoms == 0) return;
     if (!descriptor_fits_registers(t)) {
         const int kmax = std::max(t.kr, t.ka);
@@ -873,8 +874,19 @@ void descriptor_forward(const DescTables &t, const Records &r, const int32_t *ty
         RUNE_HIP_CHECK(hipGetLastError());
         return;
     }
-    size_t lds = sizeof(float) * (kWave * (t.na + 1) + kWave * (t.nlm + 1) + t.na * t.nlm);
-    if (descriptor_compact(t))
+    // LDS rows for `ch` angular records per round (the moment row reuses
+    // them afterwards).  Half-wave rounds halve the LDS of a block, so twice
+    // as many blocks fit a CU; they pay when a centre has at most 32 angular
+    // records, estimated from the mean record count and the cutoff volumes.
+    const double ratio = t.rc_a < t.rc_r ? double(t.rc_a) / t.rc_r : 1.0;
+    const double ang = double(n_records) / r.n_atoms * ratio * ratio * ratio;
+    const int ch = descriptor_compact(t) && ang <= 32.0 ? 32 : kWave;
+    const size_t lds = sizeof(float) * std::max<size_t>(size_t(ch) * (t.na + t.nlm + 2),
+                                                        size_t(t.na) * t.nlm);
+    if (descriptor_compact(t) && ch == 32)
+        hipLaunchKernelGGL((k_descriptor_forward<kCompactKr, kCompactKa, kMaxNr, kCompactOut, 32>),
+                           dim3(r.n_atoms), dim3(kWave), lds, s, t, r, types, q, ldq, moments);
+    else if (descriptor_compact(t))
         hipLaunchKernelGGL((k_descriptor_forward<kCompactKr, kCompactKa, kMaxNr, kCompactOut>),
                            dim3(r.n_atoms), dim3(kWave), lds, s, t, r, types, q, ldq, moments);
     else

@@ -62,8 +62,9 @@ struct Records {
 };
 
 // ---- descriptor (descriptor.hip) ----
-void descriptor_forward(const DescTables &t, const Records &r, const int32_t *types, float *q,
-                        int ldq, float *moments, hipStream_t s);
+// n_records (the record count) only steers the launch shape.
+void descriptor_forward(const DescTables &t, const Records &r, int64_t n_records,
+                        const int32_t *types, float *q, int ldq, float *moments, hipStream_t s);
 // dq: [N, ldq]; dmom: [N, na*nlm] or null; g_direct: [E] or null (added);
 // energies: ZBL energies added when zbl.mode != NONE; g: [E] output.
 void descriptor_reverse(const DescTables &t, const ZblTables &z, const Records &r,

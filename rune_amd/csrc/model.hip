@@ -415,7 +415,7 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     };
     // ---- forward ----
     mark(0);
-    descriptor_forward(d, r, types, q, ldq, mom, s);
+    descriptor_forward(d, r, E, types, q, ldq, mom, s);
     mark(1);
     const float4 *g_direct = nullptr;
     const float *dmom = nullptr;
@@ -854,7 +854,7 @@ extern "C" int rune_model_descriptor_extrema(rune_model *model, const rune_nlist
         RUNE_REQUIRE(hflag == 0, RUNE_ERR_TYPE, "atom type outside [0, n_types)");
         float *q = reinterpret_cast<float *>(base + o_q);
         if (N > 0)
-            descriptor_forward(d, records_of(nl), d_types, q, ldq,
+            descriptor_forward(d, records_of(nl), nl->n_records, d_types, q, ldq,
                                reinterpret_cast<float *>(base + o_s), s);
         hipLaunchKernelGGL(k_column_extrema, dim3(m.Q), dim3(256), 0, s, N, q, ldq, d_q_min,
                            d_q_max, int(accumulate != 0));
