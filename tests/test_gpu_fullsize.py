@@ -61,6 +61,29 @@ def test_c4_neighbor_list_bit_exact(c4):
     np.testing.assert_array_equal(out["view"][:, 3] - out["view"][:, 2], counts_a)
 
 
+@pytest.mark.parametrize("make", [lambda: W.fcc_alloy(seed=3),
+                                  lambda: W.amorphous(seed=6, n_atoms=40_000)],
+                         ids=["c3_19652", "amorphous_40000"])
+def test_mid_size_neighbor_list_bit_exact(make):
+    """Neighbour lists of the C3 cell (19,652 atoms) and a 40,000-atom
+    amorphous cell bit for bit against the oracle's builder: atom counts
+    above the single-workgroup scan (16,384), below C4's."""
+    from rune_amd import _native as N
+    s = make()
+    print("mid-size cell:", len(s), "atoms", flush=True)
+    ref = ONB.build(s.positions, s.cell, s.pbc, 6.0, 5.0)
+    nl = N.NeighborList().build(torch.as_tensor(s.positions, device="cuda"), [0, len(s)],
+                                [s.cell], [s.pbc], 6.0, 5.0, 819, 819)
+    out = {k: v.cpu().numpy() for k, v in nl.export().items()}
+    assert nl.n_records == len(ref["neighbor"])
+    np.testing.assert_array_equal(out["ptr"], ref["ptr"])
+    np.testing.assert_array_equal(out["nbr"], ref["neighbor"])
+    np.testing.assert_array_equal(out["shift"], ref["shift"])
+    np.testing.assert_array_equal(out["vec"][:, :3], ref["vec32"])
+    counts_a = np.bincount(ref["center"][ref["angular_mask"]], minlength=len(s))
+    np.testing.assert_array_equal(out["view"][:, 3] - out["view"][:, 2], counts_a)
+
+
 def _cluster(s, i, radius):
     """Atoms within ``radius`` of atom i (minimum image of a cubic cell), atom i
     first, as a non-periodic structure."""
