@@ -433,6 +433,9 @@ __global__ void __launch_bounds__(kWave) k_descriptor_reverse(
     float *dqL = lds;              // [Q]
     float *sL = dqL + t.Q;         // [na*nlm]
     float *WL = sL + nout;         // [na*nlm]
+    // channel-major copy of WL, NA rows per channel (zero past na), 16-byte
+    // aligned: each record reads a channel's weights with NA / 4 vector loads
+    float *WT = lds + ((t.Q + 2 * nout + 3) & ~3);   // [nlm][NA]
     const int i = blockIdx.x;
     const int lane = threadIdx.x;
     const int ti = types[i];
@@ -447,6 +450,11 @@ __global__ void __launch_bounds__(kWave) k_descriptor_reverse(
         }
         __syncthreads();
         invariant_gradient_all<kRegCubic>(t, sL, dqL + t.nr, WL, lane);
+        __syncthreads();
+        for (int o = lane; o < nlm * NA; o += kWave) {
+            const int c = o / NA, n = o - c * NA;
+            WT[o] = n < na ? WL[n * nlm + c] : 0.0f;
+        }
         __syncthreads();
     }
     float zsum = 0.0f;
@@ -501,12 +509,18 @@ __global__ void __launch_bounds__(kWave) k_descriptor_reverse(
             // one angular channel c with basis value b and gradient (bx, by, bz)
             auto channel = [&](float b, float bx, float by, float bz) {
                 float wsum = 0.0f, wsump = 0.0f;
+                const float4 *w4 = reinterpret_cast<const float4 *>(WT + c * NA);
 #pragma unroll
-                for (int n = 0; n < NA; ++n) {
-                    if (n >= na) break;
-                    float w = WL[n * nlm + c];
-                    wsum += w * gn[n];
-                    wsump += w * gnp[n];
+                for (int q = 0; q < NA / 4; ++q) {
+                    const float4 w = w4[q];
+                    wsum += w.x * gn[4 * q];
+                    wsump += w.x * gnp[4 * q];
+                    wsum += w.y * gn[4 * q + 1];
+                    wsump += w.y * gnp[4 * q + 1];
+                    wsum += w.z * gn[4 * q + 2];
+                    wsump += w.z * gnp[4 * q + 2];
+                    wsum += w.w * gn[4 * q + 3];
+                    wsump += w.w * gnp[4 * q + 3];
                 }
                 rs += wsump * b;
                 dx += wsum * bx;
@@ -912,7 +926,9 @@ void descriptor_reverse(const DescTables &t, const ZblTables &z, const Records &
         RUNE_HIP_CHECK(hipGetLastError());
         return;
     }
-    size_t lds = sizeof(float) * (t.Q + 2 * t.na * t.nlm);
+    static_assert(kCompactNa % 4 == 0 && kMaxNa % 4 == 0, "channel-major rows of 4-float vectors");
+    const int na_pad = descriptor_compact(t) ? kCompactNa : kMaxNa;
+    const size_t lds = sizeof(float) * (((t.Q + 2 * t.na * t.nlm + 3) & ~3) + size_t(na_pad) * t.nlm);
     if (descriptor_compact(t) && r.n_atoms <= kSmallDescAtoms)
         hipLaunchKernelGGL((k_descriptor_reverse<kCompactKr, kCompactKa, kCompactNa, true>),
                            dim3(r.n_atoms), dim3(kWave), lds, s, t, z, r, types, dq, ldq, moments,
