@@ -1430,36 +1430,30 @@ static MpEdgeArgs mp_edge_args(ModelImpl &m, MessagePlan &p, const MessageWeight
     return a;
 }
 
-float *messages_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Records &r,
-                        const int32_t *types, const float *moments, float *h, hipStream_t s,
-                        bool keep) {
+// The record-only forward work of the MP blocks: the edge features (basis,
+// cutoff, pair index; message.py:108-110) and every block's edge MLP (gate
+// logits from the features and the pair row, message.py:160, :178), none of
+// which reads a node state.
+static void mp_record_forward(ModelImpl &m, MessagePlan &p, const Records &r,
+                              const int32_t *types, hipStream_t s) {
     const rune_model_config &c = m.cfg;
-    if (c.family != RUNE_FAMILY_MOBIUS || c.message_layers == 0) return h;
-    if (c.message_mode == RUNE_MESSAGE_EQUIVARIANT)
-        return equivariant_forward(m, p, lp, r, types, moments, h, s, keep);
-    const int N = p.N, H = c.hidden_dim, D = c.message_dim, act = c.activation;
+    const int D = c.message_dim, act = c.activation;
     const int64_t E = p.E;
-    (void)keep;
     {
         Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
         edge_prep(m, p, r, types, s, nullptr, nullptr, 0, 0);
     }
-    float *cur = h;
-    for (int b = 0; b < c.message_layers; ++b) {
+    for (int b = 0; b < c.message_layers && E > 0; ++b) {
         const MessageWeights &w = m.msg[b];
         const BlockBuffers &bb = p.blocks[b];
-        Epilogue e0;
-        e0.rms_out = p.at(bb.rin);   // input RMSNorm, formed by the GEMM
-        e0.rms_eps = float(c.norm_eps);
-        gemm(N, w.NP, H, cur, H, w.node_f, H, p.at(bb.vs), w.NP, e0, s);
         bool fused = false;
-        if (E > 0) {
+        {
             Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
             MpEdgeArgs ea = mp_edge_args(m, p, w, E);
             ea.gv = p.at(bb.gv);
             fused = mp_edge_fused(ea, false, s);
         }
-        if (E > 0 && !fused) {
+        if (!fused) {
             Epilogue e1;
             e1.gtab[0] = w.pair_proj;
             e1.gidx[0] = reinterpret_cast<const int32_t *>(p.at(p.i_pair));
@@ -1478,6 +1472,41 @@ float *messages_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Recor
                 gemm(int(E), w.NG, D, p.at(bb.ue), D, w.gate, D, p.at(bb.gv), w.NG, e2, s);
             }
         }
+    }
+    RUNE_HIP_CHECK(hipGetLastError());
+}
+
+bool messages_records_ahead(ModelImpl &m, MessagePlan &p, const Records &r,
+                            const int32_t *types, hipStream_t s) {
+    const rune_model_config &c = m.cfg;
+    if (c.family != RUNE_FAMILY_MOBIUS || c.message_layers == 0 ||
+        c.message_mode == RUNE_MESSAGE_EQUIVARIANT || !m.side)
+        return false;
+    RUNE_HIP_CHECK(hipEventRecord(m.fork_ev, s));
+    RUNE_HIP_CHECK(hipStreamWaitEvent(m.side, m.fork_ev, 0));
+    p.records_ready = true;   // set first: a failed launch below still joins
+    mp_record_forward(m, p, r, types, m.side);
+    return true;
+}
+
+float *messages_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Records &r,
+                        const int32_t *types, const float *moments, float *h, hipStream_t s,
+                        bool keep) {
+    const rune_model_config &c = m.cfg;
+    if (c.family != RUNE_FAMILY_MOBIUS || c.message_layers == 0) return h;
+    if (c.message_mode == RUNE_MESSAGE_EQUIVARIANT)
+        return equivariant_forward(m, p, lp, r, types, moments, h, s, keep);
+    const int N = p.N, H = c.hidden_dim, D = c.message_dim, act = c.activation;
+    (void)keep;
+    if (!p.records_ready) mp_record_forward(m, p, r, types, s);
+    float *cur = h;
+    for (int b = 0; b < c.message_layers; ++b) {
+        const MessageWeights &w = m.msg[b];
+        const BlockBuffers &bb = p.blocks[b];
+        Epilogue e0;
+        e0.rms_out = p.at(bb.rin);   // input RMSNorm, formed by the GEMM
+        e0.rms_eps = float(c.norm_eps);
+        gemm(N, w.NP, H, cur, H, w.node_f, H, p.at(bb.vs), w.NP, e0, s);
         MpArgs a = mp_args(m, p, r, b);
         {
             Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);

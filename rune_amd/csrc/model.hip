@@ -232,6 +232,11 @@ static void finalize(ModelImpl &m) {
         *m.type_flag_host = 0;
     }
     if (!m.type_event) RUNE_HIP_CHECK(hipEventCreateWithFlags(&m.type_event, hipEventDisableTiming));
+    if (!m.side && m.cfg.family == RUNE_FAMILY_MOBIUS && m.cfg.message_layers > 0) {
+        RUNE_HIP_CHECK(hipStreamCreateWithFlags(&m.side, hipStreamNonBlocking));
+        RUNE_HIP_CHECK(hipEventCreateWithFlags(&m.fork_ev, hipEventDisableTiming));
+        RUNE_HIP_CHECK(hipEventCreateWithFlags(&m.join_ev, hipEventDisableTiming));
+    }
     const float *base = m.weights.as<float>();
     auto P = [&](const std::string &k) -> const float * {
         auto it = off.find(k);
@@ -414,6 +419,25 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
         if (ev) RUNE_HIP_CHECK(hipEventRecord(ev[k], s));
     };
     // ---- forward ----
+    // the message blocks' record-only work runs on the side stream beside the
+    // descriptor and the local network; the launch stream waits for it before
+    // the blocks (and, whatever happens in between, before compute returns)
+    struct SideJoin {
+        ModelImpl &m;
+        hipStream_t s;
+        bool armed = false;
+        hipError_t join() {
+            if (!armed) return hipSuccess;
+            armed = false;
+            hipError_t e = hipEventRecord(m.join_ev, m.side);
+            return e == hipSuccess ? hipStreamWaitEvent(s, m.join_ev, 0) : e;
+        }
+        ~SideJoin() { (void)join(); }
+    } side_join{m, s};
+    if (m.cfg.family == RUNE_FAMILY_MOBIUS) {
+        side_join.armed = true;
+        side_join.armed = messages_records_ahead(m, mp, r, types, s);
+    }
     mark(0);
     descriptor_forward(d, r, E, types, q, ldq, mom, s);
     mark(1);
@@ -430,6 +454,7 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     } else {
         float *h = local_forward(m, lp, N, q, ldq, types, s);
         mark(2);
+        RUNE_HIP_CHECK(side_join.join());
         h = messages_forward(m, mp, lp, r, types, mom, h, s, grad);
         mark(3);
         float *dh = grad ? lp.dh_a : nullptr;
@@ -462,6 +487,10 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
 }
 
 ModelImpl::~ModelImpl() {
+    if (side) (void)hipStreamSynchronize(side);
+    if (side) (void)hipStreamDestroy(side);
+    if (fork_ev) (void)hipEventDestroy(fork_ev);
+    if (join_ev) (void)hipEventDestroy(join_ev);
     if (type_event) (void)hipEventDestroy(type_event);
     if (type_flag_host) (void)hipHostFree(type_flag_host);
     for (auto &e : events) (void)hipEventDestroy(e);

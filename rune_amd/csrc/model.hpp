@@ -82,6 +82,7 @@ struct MessagePlan {
     size_t o_gd = 0, o_dmom = 0;
     int ldrb = 0;
     int ld_edge = 0;              // EQ: row stride of the per-record [E, D] arrays
+    bool records_ready = false;   // record-only forward work already enqueued (side stream)
     int i_rb = -1, i_fc = -1, i_tfc = -1, i_pair = -1, i_dv = -1, i_harm = -1, i_dharm = -1, i_zero = -1;
     int i_dfc = -1, i_drb = -1, i_rbd = -1;
     std::vector<BlockBuffers> blocks;
@@ -126,6 +127,10 @@ struct ModelImpl {
     int32_t *type_flag_host = nullptr;
     hipEvent_t type_event = nullptr;
     bool type_pending = false;   // type_event recorded, verdict not yet read
+    // side stream (default priority) for the record-only work of the message
+    // blocks, forked from and joined back into the launch stream by events
+    hipStream_t side = nullptr;
+    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
     // phase timing ring (events recorded on the launch stream)
     int timing = 0;   // 0 off, 1 phase events and kernel-group spans, 2 spans only
     std::vector<hipEvent_t> events;       // kTimingRing x (RUNE_N_PHASES + 1)
@@ -164,6 +169,10 @@ void define_expected_messages(ModelImpl &m);
 void pack_messages(ModelImpl &m, Packer &pk, std::map<std::string, size_t> &off);
 void bind_messages(ModelImpl &m, const PackedLookup &P);
 MessagePlan plan_messages(ModelImpl &m, Arena &ar, int N, int64_t E);
+// Enqueues the message blocks' record-only forward work (no node state read)
+// on m.side after an event on s; false when the model has none to move.
+bool messages_records_ahead(ModelImpl &m, MessagePlan &p, const Records &r,
+                            const int32_t *types, hipStream_t s);
 float *messages_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Records &r,
                         const int32_t *types, const float *moments, float *h, hipStream_t s,
                         bool keep);
