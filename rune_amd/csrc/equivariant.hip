@@ -1405,9 +1405,15 @@ __global__ void __launch_bounds__(kBlock, 2) k_eq_edge_adj(EqArgs a) {
     }
 }
 
-__global__ void k_gather_f(int64_t E, const int32_t *idx, const float *src, float *dst) {
+// dst[t] = src[idx[t]] for t < E; also clears z0[0, E) and z1[0, n1).
+__global__ void k_gather_f(int64_t E, const int32_t *idx, const float *src, float *dst,
+                           float *z0, float *z1, int n1) {
     int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (t < E) dst[t] = src[idx[t]];
+    if (t < E) {
+        dst[t] = src[idx[t]];
+        z0[t] = 0.0f;
+    }
+    if (t < n1) z1[t] = 0.0f;
 }
 
 // Reverse of the direction encoder: dE/ds[i, n, k] = scale[k] sum_c
@@ -2060,6 +2066,26 @@ static EqArgs eq_args(ModelImpl &m, MessagePlan &p, const Records &r, int b) {
     return a;
 }
 
+// The record-only forward work of the EQ blocks: edge features and
+// harmonics, the cutoff of every transposed record, and the clearing of the
+// dE/dfc accumulators and the zero row (no node state read).  dE/dY needs no
+// clearing: the first reverse block writes every row.
+void equivariant_record_forward(ModelImpl &m, MessagePlan &p, const Records &r,
+                                const int32_t *types, hipStream_t s) {
+    const rune_model_config &c = m.cfg;
+    const int lq = c.equivariant_l_max, nq = lq * (lq + 2);
+    const int64_t E = p.E;
+    {
+        Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+        edge_prep(m, p, r, types, s, p.at(p.i_harm), m.harm_scale, lq, nq);
+    }
+    Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
+    hipLaunchKernelGGL(k_gather_f, dim3(ceil_div(std::max<int64_t>(E, 128), 256)), dim3(256), 0,
+                       s, E, r.tidx, p.at(p.i_fc), p.at(p.i_tfc), p.at(p.i_dfc), p.at(p.i_zero),
+                       128);
+    RUNE_HIP_CHECK(hipGetLastError());
+}
+
 float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Records &r,
                            const int32_t *types, const float *moments, float *h, hipStream_t s,
                            bool keep) {
@@ -2070,20 +2096,7 @@ float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Re
     const int lq = c.equivariant_l_max, C = c.equivariant_channels, nq = lq * (lq + 2);
     const int64_t E = p.E;
     const int atom_grid = ceil_div(N, kWaves), mix_grid = std::max(1, std::min(ceil_div(N, 4), 4096));
-    {
-        Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
-        edge_prep(m, p, r, types, s, p.at(p.i_harm), m.harm_scale, lq, nq);
-    }
-    if (E > 0) {
-        {
-            Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
-            hipLaunchKernelGGL(k_gather_f, dim3(ceil_div(E, 256)), dim3(256), 0, s, E, r.tidx,
-                               p.at(p.i_fc), p.at(p.i_tfc));
-        }
-        // dE/dY needs no clearing: the first reverse block writes every row
-        RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_zero), 0, 4 * 128, s));
-        RUNE_HIP_CHECK(hipMemsetAsync(p.at(p.i_dfc), 0, 4 * size_t(E), s));
-    }
+    if (!p.records_ready) equivariant_record_forward(m, p, r, types, s);
     {
         const int wrow = (std::max(m.desc.na * m.desc.nlm, C * nq) + 3) & ~3;
         const size_t lds = sizeof(float) * (size_t(lq) * C * m.desc.na + 4 * size_t(wrow));

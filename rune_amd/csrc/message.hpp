@@ -78,6 +78,8 @@ void define_expected_equivariant(ModelImpl &m);
 void pack_equivariant(ModelImpl &m, Packer &pk, std::map<std::string, size_t> &off);
 void bind_equivariant(ModelImpl &m, const PackedLookup &P);
 MessagePlan plan_equivariant(ModelImpl &m, Arena &ar, int N, int64_t E);
+void equivariant_record_forward(ModelImpl &m, MessagePlan &p, const Records &r,
+                                const int32_t *types, hipStream_t s);
 float *equivariant_forward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Records &r,
                            const int32_t *types, const float *moments, float *h, hipStream_t s,
                            bool keep);
