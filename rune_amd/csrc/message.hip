@@ -81,6 +81,7 @@ __global__ void __launch_bounds__(256) k_edge_prep(EdgePrepArgs a) {
         a.fc[e] = fc;
         a.pair[e] = a.types[i] * a.n_types + a.types[a.r.nbr[e]];
         a.dv[e] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (a.dd) a.dd[e] = 0.0f;
         if (a.harm) {
             // normalised real harmonics Y = b(r_hat) * scale (descriptor.py:643-648)
             float *y = yL + t * nq;
@@ -133,12 +134,14 @@ __global__ void k_edge_rb_backward(int64_t E, Records r, const float *fc, const 
     dv[e].w += acc;
 }
 
-// g_direct = dE/dd * u + (I - u u^T) dE/du / d
-__global__ void k_edge_direct(int64_t E, Records r, const float4 *dv, float4 *g) {
+// g_direct = dE/dd * u + (I - u u^T) dE/du / d, dE/dd = dv.w (+ dd)
+__global__ void k_edge_direct(int64_t E, Records r, const float4 *dv, const float *dd,
+                              float4 *g) {
     int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (e >= E) return;
     float4 v = r.vec[e];
     float4 a = dv[e];
+    if (dd) a.w += dd[e];
     float inv = 1.0f / fmaxf(v.w, 1.0e-12f);
     float ux = v.x * inv, uy = v.y * inv, uz = v.z * inv;
     float proj = a.x * ux + a.y * uy + a.z * uz;
@@ -779,6 +782,7 @@ struct MpEdgeArgs {
     const float *fc;       // [E] cosine cutoff (0: record outside the message list)
     const float4 *vec;     // [E] record vectors
     float4 *dv;            // [E] dE/dd accumulated in .w (dv.w += sum_k drb_k f_k'(d))
+    float *dd;             // [E] or null: the accumulator of that sum instead of dv.w
     float cutoff;          // message_cutoff
 };
 
@@ -1034,7 +1038,12 @@ __global__ void __launch_bounds__(256, 3) k_mp_edge_reverse(MpEdgeArgs a) {
         }
         part += __shfl_xor(part, 16, 64);
         part += __shfl_xor(part, 32, 64);
-        if (live && g == 0 && a.fc[e] != 0.0f) a.dv[e].w += part;
+        if (live && g == 0 && a.fc[e] != 0.0f) {
+            if (a.dd)
+                a.dd[e] += part;
+            else
+                a.dv[e].w += part;
+        }
     }
 }
 
@@ -1297,7 +1306,12 @@ MessagePlan plan_messages(ModelImpl &m, Arena &ar, int N, int64_t E) {
     p.i_pair = p.add(ar, 4 * e);
     p.i_dv = p.add(ar, 16 * e);
     // the fused edge MLP keeps pre-activations and their adjoints in registers
-    const size_t ed = mp_edge_fusable(D, NG, c.message_basis_size) ? 1 : e;
+    const bool fusable = mp_edge_fusable(D, NG, c.message_basis_size);
+    const size_t ed = fusable ? 1 : e;
+    // the fused edge reverses run on the side stream: each block keeps its gate
+    // adjoints, and their dE/dd goes to its own accumulator
+    const bool side = fusable && m.side;
+    if (side) p.i_dd = p.add(ar, 4 * e);
     for (int b = 0; b < L; ++b) {
         BlockBuffers bb;
         bb.h_out = p.add(ar, 4 * n * H);
@@ -1305,6 +1319,7 @@ MessagePlan plan_messages(ModelImpl &m, Arena &ar, int N, int64_t E) {
         bb.vs = p.add(ar, 4 * n * NP);
         bb.ue = p.add(ar, 4 * ed * D);
         bb.gv = p.add(ar, 4 * e * NG);
+        if (side) bb.dgv = p.add(ar, 4 * e * NG);
         bb.msg = p.add(ar, 4 * n * H);
         bb.rm = p.add(ar, 4 * n);
         bb.vsum = p.add(ar, 4 * n * 3 * std::max(vc, 1));
@@ -1346,6 +1361,7 @@ void edge_prep(ModelImpl &m, MessagePlan &p, const Records &r, const int32_t *ty
     a.fc = p.at(p.i_fc);
     a.pair = reinterpret_cast<int32_t *>(p.at(p.i_pair));
     a.dv = reinterpret_cast<float4 *>(p.at(p.i_dv));
+    a.dd = p.i_dd >= 0 ? p.at(p.i_dd) : nullptr;
     a.harm = harm;
     a.scale = scale;
     a.lq = lq;
@@ -1376,7 +1392,8 @@ void edge_rb_backward(ModelImpl &m, MessagePlan &p, const Records &r, const floa
 void edge_direct(MessagePlan &p, const Records &r, hipStream_t s) {
     if (p.E == 0) return;
     hipLaunchKernelGGL(k_edge_direct, dim3(edge_grid(p.E)), dim3(256), 0, s, p.E, r,
-                       reinterpret_cast<const float4 *>(p.at(p.i_dv)), p.g_direct);
+                       reinterpret_cast<const float4 *>(p.at(p.i_dv)),
+                       p.i_dd >= 0 ? p.at(p.i_dd) : nullptr, p.g_direct);
     RUNE_HIP_CHECK(hipGetLastError());
 }
 
@@ -1403,7 +1420,7 @@ static MpArgs mp_args(ModelImpl &m, MessagePlan &p, const Records &r, int b) {
     a.duin = p.at(p.t_duin);
     a.dmsg = p.at(p.t_dmsg);
     a.dvsum = p.at(p.t_dvsum);
-    a.dgv = p.at(p.t_dgv);
+    a.dgv = bb.dgv >= 0 ? p.at(bb.dgv) : p.at(p.t_dgv);
     a.dv = reinterpret_cast<float4 *>(p.at(p.i_dv));
     a.dvs = p.at(p.t_dvs);
     a.cutoff = float(c.message_cutoff);
@@ -1546,6 +1563,7 @@ float *messages_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Reco
     const int N = p.N, H = c.hidden_dim, D = c.message_dim, act = c.activation;
     const int64_t E = p.E;
     float *cur = dh;
+    bool tail_side = false;   // edge reverses enqueued on the side stream
     for (int b = c.message_layers - 1; b >= 0; --b) {
         const MessageWeights &w = m.msg[b];
         const BlockBuffers &bb = p.blocks[b];
@@ -1584,17 +1602,28 @@ float *messages_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Reco
         }
         RUNE_HIP_CHECK(hipGetLastError());
         if (E > 0) {
+            // the edge reverse feeds only the geometric derivative, so with a
+            // block-owned dgv it runs on the side stream beside the node chain
+            hipStream_t es = s;
+            if (bb.dgv >= 0) {
+                RUNE_HIP_CHECK(hipEventRecord(m.fork_ev, s));
+                RUNE_HIP_CHECK(hipStreamWaitEvent(m.side, m.fork_ev, 0));
+                es = m.side;
+                tail_side = true;
+            }
             bool fused = false;
             {
-                Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
+                Span sp(m, RUNE_GROUP_EDGE_GEMM, es);
                 MpEdgeArgs ea = mp_edge_args(m, p, w, E);
-                ea.dgv = p.at(p.t_dgv);
+                ea.dgv = a.dgv;
                 ea.fc = p.at(p.i_fc);
                 ea.vec = r.vec;
                 ea.dv = reinterpret_cast<float4 *>(p.at(p.i_dv));
+                ea.dd = bb.dgv >= 0 ? p.at(p.i_dd) : nullptr;
                 ea.cutoff = float(c.message_cutoff);
-                fused = mp_edge_fused(ea, true, s);
+                fused = mp_edge_fused(ea, true, es);
             }
+            RUNE_REQUIRE(fused || es == s, RUNE_ERR_STATE, "internal: unfused side reverse");
             if (!fused) {
                 Epilogue e2;
                 e2.dact_from = p.at(bb.ue);
@@ -1623,9 +1652,17 @@ float *messages_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const Reco
         rms_backward(N, H, hin, H, p.at(bb.rin), p.at(p.t_dz), H, cur, H, next, H, s);
         cur = next;
     }
+    // the direct edge gradient after the last reverse (and after every
+    // contribution of the node chain to dv)
+    hipStream_t ts = s;
+    if (tail_side) {
+        RUNE_HIP_CHECK(hipEventRecord(m.fork_ev, s));
+        RUNE_HIP_CHECK(hipStreamWaitEvent(m.side, m.fork_ev, 0));
+        ts = m.side;
+    }
     {
-        Span sp(m, RUNE_GROUP_EDGE_KERNELS, s);
-        edge_direct(p, r, s);
+        Span sp(m, RUNE_GROUP_EDGE_KERNELS, ts);
+        edge_direct(p, r, ts);
     }
     p.g_direct_used = E > 0;
     return cur;

@@ -17,6 +17,7 @@ struct EdgePrepArgs {
     float *fc;             // [E] cosine cutoff, 0 outside the radial list
     int32_t *pair;         // [E] t_i * T + t_j
     float4 *dv;            // [E] zeroed: (dE/du, dE/dd) accumulators
+    float *dd;             // [E] zeroed second dE/dd accumulator, or null
     float *harm;           // EQ: [E, nq] normalised harmonics, or null
     const float *scale;    // [nq] orthonormal scale
     int lq, nq;

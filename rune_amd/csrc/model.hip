@@ -462,9 +462,13 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
                 float(m.cfg.norm_eps), energies, dh, m.cfg.hidden_dim, s);
         mark(4);
         if (grad) {
+            // the message blocks leave work that feeds only the descriptor
+            // reverse on the side stream; joined after the local network
+            side_join.armed = m.side != nullptr;
             dh = messages_backward(m, mp, lp, r, types, mom, dh, s);
             mark(5);
             local_backward(m, lp, N, dh, dq, ldq, s);
+            RUNE_HIP_CHECK(side_join.join());
             g_direct = mp.g_direct_used ? mp.g_direct : nullptr;
             dmom = mp.dmom_used ? mp.dmom : nullptr;
         } else {

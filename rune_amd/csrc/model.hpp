@@ -69,6 +69,7 @@ struct BlockBuffers {
     int vsum = -1, mixed = -1, uin = -1, u1 = -1, z1 = -1;
     int dir_in = -1, dir_out = -1, mixstate = -1;   // EQ angular states
     int q = -1;                                      // EQ per-atom edge-MLP factors
+    int dgv = -1;   // MP: this block's gate adjoints, when its edge reverse runs on the side stream
 };
 
 struct MessagePlan {
@@ -83,6 +84,7 @@ struct MessagePlan {
     int ldrb = 0;
     int ld_edge = 0;              // EQ: row stride of the per-record [E, D] arrays
     bool records_ready = false;   // record-only forward work already enqueued (side stream)
+    int i_dd = -1;                // MP: [E] dE/dd of the edge reverses run on the side stream
     int i_rb = -1, i_fc = -1, i_tfc = -1, i_pair = -1, i_dv = -1, i_harm = -1, i_dharm = -1, i_zero = -1;
     int i_dfc = -1, i_drb = -1, i_rbd = -1;
     std::vector<BlockBuffers> blocks;
