@@ -59,6 +59,28 @@ def test_neighbor_list_bit_exact(name, rc):
     np.testing.assert_array_equal(out["view"][:, 3] - out["view"][:, 2], counts_a)
 
 
+def test_neighbor_list_dense_rows_after_sparse_build():
+    """One list handle rebuilt from a sparse system (8 records per centre) to
+    dense ones (160-183 records per centre, cutoffs beyond half the cell, so
+    several images of an atom): every list bit for bit the oracle's."""
+    from rune_amd import _native as N
+    nl = N.NeighborList()
+    cases = [(SMALL["si8"](), (3.8, 3.5)),
+             (W.amorphous(seed=25, n_atoms=200), (8.0, 7.0)),
+             (W.amorphous(seed=26, n_atoms=200), (8.0, 7.0))]
+    for s, rc in cases:
+        ref = ONB.build(s.positions, s.cell, s.pbc, rc[0], rc[1])
+        nl.build(torch.as_tensor(s.positions, device="cuda"), [0, len(s)], [s.cell], [s.pbc],
+                 rc[0], rc[1], 100000, 100000)
+        out = {k: v.cpu().numpy() for k, v in nl.export().items()}
+        print("rows", np.diff(ref["ptr"]).max(), "records", len(ref["neighbor"]), flush=True)
+        assert nl.n_records == len(ref["neighbor"])
+        np.testing.assert_array_equal(out["ptr"], ref["ptr"])
+        np.testing.assert_array_equal(out["nbr"], ref["neighbor"])
+        np.testing.assert_array_equal(out["shift"], ref["shift"])
+        np.testing.assert_array_equal(out["vec"][:, :3], ref["vec32"])
+
+
 def _oracle(p, w, s, types, dtype):
     nl = ONB.build(s.positions, s.cell, s.pbc, p["rcut_radial"], p["rcut_angular"])
     sp = ONB.split(nl)
