@@ -2188,7 +2188,6 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
     // rows of one batch, and its record ids
     const int adj_wlds = kAdjBatch * ((16 * ntc + 4) + (16 * mt + 4) + (nq + 1) + 1);
     float *cur = dh;
-    bool drb_side = false;   // a dE/drb product is enqueued on the side stream
     const float *ddir_out = nullptr;   // the last block's states feed only its invariants
     float *ddir_in = p.at(p.t_ddir0);
     for (int b = c.message_layers - 1; b >= 0; --b) {
@@ -2228,12 +2227,6 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         }
         RUNE_HIP_CHECK(hipGetLastError());
         if (E > 0) {
-            // due is rewritten below: the previous block's dE/drb product on
-            // the side stream must have read it
-            if (drb_side) {
-                RUNE_HIP_CHECK(hipEventRecord(m.join_ev, m.side));
-                RUNE_HIP_CHECK(hipStreamWaitEvent(s, m.join_ev, 0));
-            }
             // due = (dE/dgates) gate^T * act'(u), zero in the padding columns
             Epilogue e2;
             e2.dact_from = p.at(bb.ue);
@@ -2244,25 +2237,16 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
                 gemm(int(E), ldd, w.NG, p.at(p.t_dgv), w.NG, w.gate_Tp, w.NG, p.at(p.t_due), ldd,
                      e2, s);
             }
-            // dE/drb = due W_rb^T, summed over the blocks: it feeds only the
-            // geometric derivative, so it runs on the side stream beside the
-            // edge adjoints
-            hipStream_t ds = s;
-            if (m.side) {
-                RUNE_HIP_CHECK(hipEventRecord(m.fork_ev, s));
-                RUNE_HIP_CHECK(hipStreamWaitEvent(m.side, m.fork_ev, 0));
-                ds = m.side;
-                drb_side = true;
-            }
+            // dE/drb = due W_rb^T, summed over the blocks
             Epilogue e3;
             if (b != c.message_layers - 1) {
                 e3.residual = p.at(p.i_drb);
                 e3.ldr = p.ldrb;
             }
             {
-                Span sp(m, RUNE_GROUP_EDGE_GEMM, ds);
+                Span sp(m, RUNE_GROUP_EDGE_GEMM, s);
                 gemm(int(E), kb, D, p.at(p.t_due), ldd, w.edge_rbT, D, p.at(p.i_drb), p.ldrb, e3,
-                     ds);
+                     s);
             }
         }
         a.wlds = adj_wlds;
@@ -2295,14 +2279,7 @@ float *equivariant_backward(ModelImpl &m, MessagePlan &p, LocalPlan &lp, const R
         ddir_out = ddir_in;
         ddir_in = (ddir_in == p.at(p.t_ddir0)) ? p.at(p.t_ddir1) : p.at(p.t_ddir0);
     }
-    // ddir_out now holds dE/d(encoder output).  The rest feeds only the
-    // descriptor reverse: on the side stream, beside the local network's
-    // reverse (the caller joins before the descriptor reverse).
-    if (m.side) {
-        RUNE_HIP_CHECK(hipEventRecord(m.fork_ev, s));
-        RUNE_HIP_CHECK(hipStreamWaitEvent(m.side, m.fork_ev, 0));
-        s = m.side;
-    }
+    // ddir_out now holds dE/d(encoder output)
     {
         const int wrow = (std::max(m.desc.na * m.desc.nlm, C * nq) + 3) & ~3;
         const size_t lds = sizeof(float) * (size_t(lq) * C * m.desc.na + 4 * size_t(wrow));

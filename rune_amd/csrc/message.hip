@@ -1496,14 +1496,13 @@ static void mp_record_forward(ModelImpl &m, MessagePlan &p, const Records &r,
 bool messages_records_ahead(ModelImpl &m, MessagePlan &p, const Records &r,
                             const int32_t *types, hipStream_t s) {
     const rune_model_config &c = m.cfg;
-    if (c.family != RUNE_FAMILY_MOBIUS || c.message_layers == 0 || !m.side) return false;
+    if (c.family != RUNE_FAMILY_MOBIUS || c.message_layers == 0 ||
+        c.message_mode == RUNE_MESSAGE_EQUIVARIANT || !m.side)
+        return false;
     RUNE_HIP_CHECK(hipEventRecord(m.fork_ev, s));
     RUNE_HIP_CHECK(hipStreamWaitEvent(m.side, m.fork_ev, 0));
     p.records_ready = true;   // set first: a failed launch below still joins
-    if (c.message_mode == RUNE_MESSAGE_EQUIVARIANT)
-        equivariant_record_forward(m, p, r, types, m.side);
-    else
-        mp_record_forward(m, p, r, types, m.side);
+    mp_record_forward(m, p, r, types, m.side);
     return true;
 }
 

@@ -232,7 +232,10 @@ static void finalize(ModelImpl &m) {
         *m.type_flag_host = 0;
     }
     if (!m.type_event) RUNE_HIP_CHECK(hipEventCreateWithFlags(&m.type_event, hipEventDisableTiming));
-    if (!m.side && m.cfg.family == RUNE_FAMILY_MOBIUS && m.cfg.message_layers > 0) {
+    // the side stream serves the MP blocks (EQ keeps one stream: overlapping
+    // its heavier record kernels gained 0.3 % and stretched their durations)
+    if (!m.side && m.cfg.family == RUNE_FAMILY_MOBIUS && m.cfg.message_layers > 0 &&
+        m.cfg.message_mode != RUNE_MESSAGE_EQUIVARIANT) {
         RUNE_HIP_CHECK(hipStreamCreateWithFlags(&m.side, hipStreamNonBlocking));
         RUNE_HIP_CHECK(hipEventCreateWithFlags(&m.fork_ev, hipEventDisableTiming));
         RUNE_HIP_CHECK(hipEventCreateWithFlags(&m.join_ev, hipEventDisableTiming));
