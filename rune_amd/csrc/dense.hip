@@ -1,6 +1,7 @@
 // Dense per-atom layers: fp32 MFMA GEMM with fused epilogues, RMSNorm rows,
 // the Möbius element-head readout and the NEP per-element MLP.
 #include <cmath>
+#include <cstdlib>
 
 #include "activation.hpp"
 #include "kernels.hpp"
@@ -490,6 +491,14 @@ static bool narrow_tile(int N) { return ceil_div(N, 32) * 32 < ceil_div(N, 64) *
 // Below this many 64-row tiles (one per CU) a launch cannot fill the chip and
 // the small-grid kernel, with K split over the waves of a block, is used.
 constexpr int64_t kSmallGemmBlocks = 256;
+// Rows from which a product takes the 64x96 tile (see gemm_any); the
+// environment variable RUNE_TALL_ROWS overrides it (tests run that tile on
+// small systems with it).
+constexpr int64_t kTallRows = 2000000;
+static int64_t tall_rows() {
+    const char *v = std::getenv("RUNE_TALL_ROWS");
+    return v && *v ? std::max<int64_t>(1, std::atoll(v)) : kTallRows;
+}
 
 template <int WM, int WN, int WMW = 2>
 static void launch_gemm(bool vec, int M, int N, int K, const float *A, int lda, const float *Bt,
@@ -583,7 +592,15 @@ static void gemm_any(int M, int N, int K, const float *A, int lda, const float *
             e.row_scale = ep.rms_out;
             e.rms_out = nullptr;
         }
-        if (narrow_tile(N))
+        // very tall products (the per-record GEMMs of large cells): 64x96
+        // tiles when they pad N no more than the default tile, so a block does
+        // 1.5-3x the work behind one prologue and epilogue (4 waves per SIMD
+        // instead of 5-8; measured on C4, N = 264 and 192: -0.3 ms each; at
+        // 0.6 M rows slightly slower)
+        const int pad = narrow_tile(N) ? ceil_div(N, 32) * 32 : ceil_div(N, 64) * 64;
+        if (int64_t(M) >= tall_rows() && bt.count == 1 && N > 128 && ceil_div(N, 96) * 96 <= pad)
+            launch_gemm<1, 6, 4>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, e, bt, s);
+        else if (narrow_tile(N))
             launch_gemm<1, 2, 4>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, e, bt, s);
         else
             launch_gemm<2, 2, 2>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, e, bt, s);

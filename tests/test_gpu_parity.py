@@ -336,6 +336,18 @@ def test_eq_model_matches_oracle(name):
     check_against_oracle("eq", out, s, ev.types_of(s.numbers))
 
 
+@pytest.mark.parametrize("name", ["fcc108", "amo200"])
+def test_eq_model_with_tall_product_tiles_matches_oracle(name, monkeypatch):
+    """The 64x96 tile the per-record GEMMs of cells with millions of records
+    take (gate product N = 264, its transpose N = 192), run here on small
+    cells by lowering the row threshold."""
+    monkeypatch.setenv("RUNE_TALL_ROWS", "1")
+    ev, p = _evaluator("eq")
+    s = _structures()[name]
+    out = ev.evaluate(s)
+    check_against_oracle("eq", out, s, ev.types_of(s.numbers))
+
+
 def _check_small(model):
     from rune_amd import _native as N
     from rune_amd.api import Evaluator
