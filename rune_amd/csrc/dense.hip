@@ -593,13 +593,14 @@ static void gemm_any(int M, int N, int K, const float *A, int lda, const float *
             e.rms_out = nullptr;
         }
         // very tall products (the per-record GEMMs of large cells): 64x96
-        // tiles when they pad N no more than the default tile, so a block does
-        // 1.5-3x the work behind one prologue and epilogue (4 waves per SIMD
-        // instead of 5-8; measured on C4, N = 264 and 192: -0.3 ms each; at
-        // 0.6 M rows slightly slower)
+        // tiles (2 x 2 waves of 32 x 48) when they pad N no more than the
+        // default tile, so a block does 1.5-3x the work behind one prologue
+        // and epilogue (5 waves per SIMD; measured on C4, N = 264 / 192:
+        // -0.9 / -0.3 ms per launch pair; 1 x 4 waves of 16 x 96 gained half
+        // as much, 128 x 96 lost 4 ms; at 0.6 M rows no gain)
         const int pad = narrow_tile(N) ? ceil_div(N, 32) * 32 : ceil_div(N, 64) * 64;
         if (int64_t(M) >= tall_rows() && bt.count == 1 && N > 128 && ceil_div(N, 96) * 96 <= pad)
-            launch_gemm<1, 6, 4>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, e, bt, s);
+            launch_gemm<2, 3, 2>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, e, bt, s);
         else if (narrow_tile(N))
             launch_gemm<1, 2, 4>(vec, M, N, K, A, lda, Bt, ldb, C, ldc, e, bt, s);
         else
