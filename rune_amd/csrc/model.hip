@@ -347,6 +347,7 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
     const int64_t E = nl->n_records;
     const bool grad = want_f || want_w;
     Records r = records_of(nl);
+    nl->order_wanted = m.cfg.family == RUNE_FAMILY_MOBIUS && m.cfg.message_layers > 0;
     const DescTables &d = m.desc;
     const int ldq = (m.Q + 3) & ~3;
     const int nmom = d.na * d.nlm;

@@ -1076,7 +1076,7 @@ static void build_lists(rune_nlist *nl, int64_t n_atoms, const double *d_positio
     // last binning when the candidates are reused; it only orders the work,
     // so a list of fewer than kOrderMinAtoms atoms, which fits in L2 either
     // way, keeps the index order and saves the launches)
-    if (binned && n < kOrderMinAtoms) {
+    if (binned && (n < kOrderMinAtoms || !nl->order_wanted)) {
         nl->has_order = false;
     } else if (binned) {
         nl->order.reserve(4 * size_t(std::max(n, 1)));

@@ -32,6 +32,11 @@ struct rune_nlist {
     // for lists made from padded tensors
     rune::DeviceBuffer order;    // int32 [N]
     bool has_order = false;
+    // whether the last model that read this list walks atoms in the processing
+    // order (the message blocks do; the descriptor and force kernels do not):
+    // a build computes the order only then (without it the walks take index
+    // order, with identical results)
+    mutable bool order_wanted = true;
     std::vector<int32_t> h_perm; // host Morton ranks of the bins
     // skin reuse (rune_nlist_update): candidates within max(rc) + skin of the
     // last search, the positions it saw, and what else it depended on
