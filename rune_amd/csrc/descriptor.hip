@@ -380,6 +380,122 @@ __global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Reco
     invariants_all(t, sL, q + size_t(i) * ldq + t.nr, lane);
 }
 
+// Two centres per wave (lanes 0-31 centre 2b, lanes 32-63 centre 2b + 1) for
+// sparse lists (at most about 32 records per centre, e.g. NEP on a
+// 13,824-atom cell): the arithmetic of k_descriptor_forward over half-waves,
+// with record rounds of 32 per half, so a launch has half the waves and a
+// wave's lanes are not mostly idle.  Sums over a half-wave stay in it
+// (shuffle offsets below 32).
+template <int KR, int KA, int NR, int NO2>
+__global__ void __launch_bounds__(kWave) k_descriptor_forward_pair(DescTables t, Records r,
+                                                                   const int32_t *types, float *q,
+                                                                   int ldq, float *moments) {
+    extern __shared__ float lds[];
+    constexpr int H = kWave / 2;
+    const int nlm = t.nlm, na = t.na, nout = na * nlm;
+    const int lane = threadIdx.x, half = lane >> 5, hl = lane & (H - 1);
+    const int i = 2 * int(blockIdx.x) + half;
+    const bool valid = i < r.n_atoms;
+    const int ic = valid ? i : r.n_atoms - 1;
+    const int hstride = max(H * (na + nlm + 2), nout);
+    float *gnL = lds + half * hstride;   // [H][na+1]
+    float *bL = gnL + H * (na + 1);      // [H][nlm+1]
+    float *sL = gnL;                     // [na*nlm], after the record rounds
+    const int ti = types[ic];
+    const int rb = r.view[4 * ic], re = valid ? r.view[4 * ic + 1] : rb;
+    const int ab = r.view[4 * ic + 2], ae = valid ? r.view[4 * ic + 3] : ab;
+
+    // radial channels
+    float qr[NR];
+#pragma unroll
+    for (int n = 0; n < NR; ++n) qr[n] = 0.0f;
+    for (int e = rb + hl; e < re; e += H) {
+        float4 v = r.vec[e];
+        int tj = types[r.nbr[e]];
+        float f[KR] = {};
+        chebyshev<KR>(v.w, t.rc_r, t.kr, f);
+        const float *row = t.c_radial + size_t(ti * t.n_types + tj) * t.nr * t.kr4;
+#pragma unroll
+        for (int n = 0; n < NR; ++n) {
+            if (n >= t.nr) break;
+            qr[n] += row_dot<KR>(row + n * t.kr4, t.kr4, f);
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < NR; ++n) {
+        if (n >= t.nr) break;
+        float v = qr[n];
+#pragma unroll
+        for (int off = H / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+        if (hl == 0 && valid) q[size_t(i) * ldq + n] = v;
+    }
+
+    // angular moments, rounds of H records per half (as many rounds as the
+    // larger of the two centres needs)
+    float acc[NO2];
+#pragma unroll
+    for (int j = 0; j < NO2; ++j) acc[j] = 0.0f;
+    const int cnt_a = ae - ab;
+    const int rounds_to = max(cnt_a, __shfl_xor(cnt_a, H, kWave));
+    for (int base = 0; base < rounds_to; base += H) {
+        const int e = ab + base + hl;
+        float *gl = gnL + hl * (na + 1);
+        float *bl = bL + hl * (nlm + 1);
+        if (e < ae) {
+            float4 v = r.vec[e];
+            int tj = types[r.nbr[e]];
+            float f[KA] = {};
+            chebyshev<KA>(v.w, t.rc_a, t.ka, f);
+            const float *row = t.c_angular + size_t(ti * t.n_types + tj) * t.na * t.ka4;
+            for (int n = 0; n < na; ++n) gl[n] = row_dot<KA>(row + n * t.ka4, t.ka4, f);
+            float inv = 1.0f / fmaxf(v.w, 1.0e-12f);
+            const float ux = v.x * inv, uy = v.y * inv, uz = v.z * inv;
+            int idx = 0;
+            for (int L = 1; L <= t.l_max; ++L) {
+                float wr = 1.0f, wi = 0.0f;   // (x + iy)^n1
+                for (int n1 = 0; n1 <= L; ++n1) {
+                    float zf, zfp;
+                    zpoly(t, L, n1, uz, zf, zfp);
+                    if (n1 == 0) {
+                        bl[idx++] = zf;
+                    } else {
+                        next_w(ux, uy, wr, wi);
+                        bl[idx++] = zf * wr;
+                        bl[idx++] = zf * wi;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        const int cnt = max(0, min(H, cnt_a - base));
+#pragma unroll
+        for (int j = 0; j < NO2; ++j) {
+            int o = hl + H * j;
+            if (o >= nout) break;
+            int n = o / nlm, c = o - n * nlm;
+            float a = 0.0f;
+            for (int k = 0; k < cnt; ++k) a += gnL[k * (na + 1) + n] * bL[k * (nlm + 1) + c];
+            acc[j] += a;
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < NO2; ++j) {
+        int o = hl + H * j;
+        if (o >= nout) break;
+        sL[o] = acc[j];
+        if (valid) moments[size_t(i) * nout + o] = acc[j];
+    }
+    __syncthreads();
+    if (valid) {
+        float *out = q + size_t(i) * ldq + t.nr;
+        for (int o = hl; o < na * t.num_L; o += H) {
+            const int idx = o / na, n = o - idx * na;
+            out[o] = invariant_one(t, sL + n * nlm, idx);
+        }
+    }
+}
+
 __device__ inline void zbl_pair(const ZblTables &z, int ti, int tj, float d, float &e,
                                 float &de) {
     const float K = 14.399645f;
@@ -862,6 +978,9 @@ constexpr int kCompactKr = 20, kCompactKa = 16, kCompactNa = 12, kCompactOut = 5
 // keeps the cubic-invariant gradients in registers: its wave latency is the
 // kernel time there, and the extra registers cost nothing.
 constexpr int kSmallDescAtoms = 8192;
+// From this many centres (more than one round of one-centre waves) a sparse
+// list takes the two-centres-per-wave kernels.
+constexpr int kPairDescAtoms = 8192;
 bool descriptor_compact(const DescTables &t) {
     return t.nr <= kMaxNr && t.kr <= kCompactKr && t.ka <= kCompactKa && t.na <= kCompactNa &&
            t.na * t.nlm <= kCompactOut * kWave;
@@ -897,7 +1016,23 @@ void descriptor_forward(const DescTables &t, const Records &r, int64_t n_records
     const int ch = descriptor_compact(t) && ang <= 32.0 ? 32 : kWave;
     const size_t lds = sizeof(float) * std::max<size_t>(size_t(ch) * (t.na + t.nlm + 2),
                                                         size_t(t.na) * t.nlm);
-    if (descriptor_compact(t) && ch == 32)
+    // sparse lists on grids of more than one round of waves: two centres per
+    // wave (rounds of 32 records per half)
+    const double mean = double(n_records) / r.n_atoms;
+    if (descriptor_compact(t) && mean <= 32.0 && r.n_atoms >= kPairDescAtoms) {
+        const size_t hstride = std::max<size_t>(size_t(kWave / 2) * (t.na + t.nlm + 2),
+                                                size_t(t.na) * t.nlm);
+        const dim3 grid((r.n_atoms + 1) / 2);
+        const size_t plds = sizeof(float) * 2 * hstride;
+        if (t.na * t.nlm <= kCompactOut * kWave / 2)   // moments per half-lane
+            hipLaunchKernelGGL((k_descriptor_forward_pair<kCompactKr, kCompactKa, kMaxNr,
+                                                          kCompactOut>),
+                               grid, dim3(kWave), plds, s, t, r, types, q, ldq, moments);
+        else
+            hipLaunchKernelGGL((k_descriptor_forward_pair<kCompactKr, kCompactKa, kMaxNr,
+                                                          2 * kCompactOut>),
+                               grid, dim3(kWave), plds, s, t, r, types, q, ldq, moments);
+    } else if (descriptor_compact(t) && ch == 32)
         hipLaunchKernelGGL((k_descriptor_forward<kCompactKr, kCompactKa, kMaxNr, kCompactOut, 32>),
                            dim3(r.n_atoms), dim3(kWave), lds, s, t, r, types, q, ldq, moments);
     else if (descriptor_compact(t))
