@@ -247,17 +247,17 @@ __device__ float invariant_grad_one(const DescTables &t, const float *s, const f
 // lane for the order and four/five-body invariants, then one channel per
 // lane for the cubic invariants (their unrolled term lists read the moments
 // from registers and update the row at constant offsets).
-template <bool kRegCubic = false>
+template <bool kRegCubic = false, int STEP = kWave>
 __device__ void invariant_gradient_all(const DescTables &t, const float *sL, const float *dq,
                                        float *WL, int lane) {
     const int na = t.na, nlm = t.nlm;
-    for (int o = lane; o < na * nlm; o += kWave) {
+    for (int o = lane; o < na * nlm; o += STEP) {
         const int n = o / nlm, c = o - n * nlm;
         WL[o] += invariant_grad_one(t, sL + n * nlm, dq + n, na, c);
     }
     if (!(t.has_q[3] || t.has_q[4] || t.has_q[5])) return;
     __syncthreads();
-    for (int n = lane; n < na; n += kWave) {
+    for (int n = lane; n < na; n += STEP) {
         float sr[kCubicComps];
         cubic_moments(sL + n * nlm, nlm, sr);
         // kRegCubic: accumulate in registers (no LDS read-modify-write chain,
@@ -539,42 +539,50 @@ __device__ inline void zbl_pair(const ZblTables &z, int ti, int tj, float d, flo
     de = 0.5f * (dscr * cut + scr * dcut);
 }
 
-template <int KR, int KA, int NA, bool kRegCubic = false>
+// P centres per wave (P = 2: lanes 0-31 centre 2b, lanes 32-63 centre 2b + 1,
+// for sparse lists on large grids, as k_descriptor_forward_pair).
+template <int KR, int KA, int NA, bool kRegCubic = false, int P = 1>
 __global__ void __launch_bounds__(kWave) k_descriptor_reverse(
     DescTables t, ZblTables z, Records r, const int32_t *types, const float *dq, int ldq,
     const float *moments, const float *dmom, const float4 *g_direct, float *energies,
     float4 *g, int want_grad) {
     extern __shared__ float lds[];
+    constexpr int H = kWave / P;   // lanes per centre
     const int nlm = t.nlm, na = t.na, nout = na * nlm;
-    float *dqL = lds;              // [Q]
-    float *sL = dqL + t.Q;         // [na*nlm]
-    float *WL = sL + nout;         // [na*nlm]
-    // channel-major copy of WL, NA rows per channel (zero past na), 16-byte
-    // aligned: each record reads a channel's weights with NA / 4 vector loads
-    float *WT = lds + ((t.Q + 2 * nout + 3) & ~3);   // [nlm][NA]
-    const int i = blockIdx.x;
-    const int lane = threadIdx.x;
-    const int ti = types[i];
-    const int rb = r.view[4 * i], re = r.view[4 * i + 1];
-    const int ab = r.view[4 * i + 2], ae = r.view[4 * i + 3];
-    const int eb = r.ptr[i], ee = r.ptr[i + 1];
+    const int half = P == 1 ? 0 : int(threadIdx.x) / H;
+    const int lane = P == 1 ? int(threadIdx.x) : int(threadIdx.x) % H;
+    const int i = P * int(blockIdx.x) + half;
+    const bool valid = P == 1 || i < r.n_atoms;
+    const int ic = P == 1 ? i : (valid ? i : r.n_atoms - 1);
+    // per centre: dq row, moments, their weights, and a channel-major copy of
+    // the weights, NA rows per channel (zero past na), 16-byte aligned: each
+    // record reads a channel's weights with NA / 4 vector loads
+    const int wt_off = (t.Q + 2 * nout + 3) & ~3;
+    float *dqL = P == 1 ? lds : lds + half * (wt_off + NA * nlm);   // [Q]
+    float *sL = dqL + t.Q;                           // [na*nlm]
+    float *WL = sL + nout;                           // [na*nlm]
+    float *WT = dqL + wt_off;                        // [nlm][NA]
+    const int ti = types[ic];
+    const int rb = r.view[4 * ic], re = r.view[4 * ic + 1];
+    const int ab = r.view[4 * ic + 2], ae = r.view[4 * ic + 3];
+    const int eb = r.ptr[ic], ee = valid ? r.ptr[ic + 1] : eb;
     if (want_grad) {
-        for (int k = lane; k < t.Q; k += kWave) dqL[k] = dq[size_t(i) * ldq + k];
-        for (int o = lane; o < nout; o += kWave) {
-            sL[o] = moments[size_t(i) * nout + o];
-            WL[o] = dmom ? dmom[size_t(i) * nout + o] : 0.0f;
+        for (int k = lane; k < t.Q; k += H) dqL[k] = dq[size_t(ic) * ldq + k];
+        for (int o = lane; o < nout; o += H) {
+            sL[o] = moments[size_t(ic) * nout + o];
+            WL[o] = dmom ? dmom[size_t(ic) * nout + o] : 0.0f;
         }
         __syncthreads();
-        invariant_gradient_all<kRegCubic>(t, sL, dqL + t.nr, WL, lane);
+        invariant_gradient_all<kRegCubic, H>(t, sL, dqL + t.nr, WL, lane);
         __syncthreads();
-        for (int o = lane; o < nlm * NA; o += kWave) {
+        for (int o = lane; o < nlm * NA; o += H) {
             const int c = o / NA, n = o - c * NA;
             WT[o] = n < na ? WL[n * nlm + c] : 0.0f;
         }
         __syncthreads();
     }
     float zsum = 0.0f;
-    for (int e = eb + lane; e < ee; e += kWave) {
+    for (int e = eb + lane; e < ee; e += H) {
         float4 v = r.vec[e];
         float d = v.w;
         float inv = 1.0f / fmaxf(d, 1.0e-12f);
@@ -685,8 +693,10 @@ __global__ void __launch_bounds__(kWave) k_descriptor_reverse(
         }
     }
     if (z.mode != RUNE_ZBL_NONE) {
-        float s = wave_sum(zsum);
-        if (lane == 0) energies[i] += s;
+        float s = zsum;
+#pragma unroll
+        for (int off = H / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, kWave);
+        if (lane == 0 && valid) energies[i] += s;
     }
 }
 
@@ -1046,9 +1056,9 @@ void descriptor_forward(const DescTables &t, const Records &r, int64_t n_records
 }
 
 void descriptor_reverse(const DescTables &t, const ZblTables &z, const Records &r,
-                        const int32_t *types, const float *dq, int ldq, const float *moments,
-                        const float *dmom, const float4 *g_direct, float *energies, float4 *g,
-                        int want_grad, hipStream_t s) {
+                        int64_t n_records, const int32_t *types, const float *dq, int ldq,
+                        const float *moments, const float *dmom, const float4 *g_direct,
+                        float *energies, float4 *g, int want_grad, hipStream_t s) {
     if (r.n_atoms == 0) return;
     if (!want_grad && z.mode == RUNE_ZBL_NONE) return;
     if (!descriptor_fits_registers(t)) {
@@ -1064,7 +1074,12 @@ void descriptor_reverse(const DescTables &t, const ZblTables &z, const Records &
     static_assert(kCompactNa % 4 == 0 && kMaxNa % 4 == 0, "channel-major rows of 4-float vectors");
     const int na_pad = descriptor_compact(t) ? kCompactNa : kMaxNa;
     const size_t lds = sizeof(float) * (((t.Q + 2 * t.na * t.nlm + 3) & ~3) + size_t(na_pad) * t.nlm);
-    if (descriptor_compact(t) && r.n_atoms <= kSmallDescAtoms)
+    const double mean = double(n_records) / r.n_atoms;
+    if (descriptor_compact(t) && mean <= 32.0 && r.n_atoms >= kPairDescAtoms)
+        hipLaunchKernelGGL((k_descriptor_reverse<kCompactKr, kCompactKa, kCompactNa, false, 2>),
+                           dim3((r.n_atoms + 1) / 2), dim3(kWave), 2 * lds, s, t, z, r, types, dq,
+                           ldq, moments, dmom, g_direct, energies, g, want_grad);
+    else if (descriptor_compact(t) && r.n_atoms <= kSmallDescAtoms)
         hipLaunchKernelGGL((k_descriptor_reverse<kCompactKr, kCompactKa, kCompactNa, true>),
                            dim3(r.n_atoms), dim3(kWave), lds, s, t, z, r, types, dq, ldq, moments,
                            dmom, g_direct, energies, g, want_grad);

@@ -68,9 +68,9 @@ void descriptor_forward(const DescTables &t, const Records &r, int64_t n_records
 // dq: [N, ldq]; dmom: [N, na*nlm] or null; g_direct: [E] or null (added);
 // energies: ZBL energies added when zbl.mode != NONE; g: [E] output.
 void descriptor_reverse(const DescTables &t, const ZblTables &z, const Records &r,
-                        const int32_t *types, const float *dq, int ldq, const float *moments,
-                        const float *dmom, const float4 *g_direct, float *energies, float4 *g,
-                        int want_grad, hipStream_t s);
+                        int64_t n_records, const int32_t *types, const float *dq, int ldq,
+                        const float *moments, const float *dmom, const float4 *g_direct,
+                        float *energies, float4 *g, int want_grad, hipStream_t s);
 
 // ---- dense layers (dense.hip) ----
 struct Epilogue {

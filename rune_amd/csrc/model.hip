@@ -480,7 +480,7 @@ static void compute(ModelImpl &m, const rune_nlist *nl, const int32_t *types, in
         }
         mark(6);
     }
-    descriptor_reverse(d, m.zbl, r, types, dq, ldq, mom, dmom, g_direct, energies, g,
+    descriptor_reverse(d, m.zbl, r, E, types, dq, ldq, mom, dmom, g_direct, energies, g,
                        grad ? 1 : 0, s);
     mark(7);
     if (grad) forces_and_virial(r, g, forces, atom_virial, s);
