@@ -172,6 +172,33 @@ def test_c2_whole_against_oracle():
     assert_within(out, r64, _nep_oracle(model, s, torch.float32), len(s), f"C2 {len(s)}")
 
 
+def test_c2_odd_atom_count_against_oracle():
+    """The C2 cell without its last atom: 13,823 centres, so the last wave of
+    the two-centres-per-wave descriptor kernels holds one centre."""
+    from rune_amd import _native as N
+    from rune_amd.api import Evaluator
+    from rune_amd.nep.model import seeded_nep
+    model = seeded_nep(seed=0)
+    ev = Evaluator(model.params, model.state_dict(), N.FAMILY_NEP)
+    c2 = W.rocksalt()
+    s = W.Structure(c2.positions[:-1], c2.numbers[:-1], c2.cell)
+    assert len(s) % 2 == 1
+    out = ev.evaluate(s)
+    r64 = _nep_oracle(model, s, torch.float64)
+    assert_within(out, r64, _nep_oracle(model, s, torch.float32), len(s), f"C2-1 {len(s)}")
+
+
+def test_sparse_local_cell_against_oracle():
+    """A 8,193-atom amorphous cell at 0.025 atoms / A^3 (22 records per centre
+    on average, 36 at most) with the Mobius-Local model: the
+    two-centres-per-wave descriptor kernels with every invariant order
+    (cubic ones included), and a last wave holding one centre."""
+    ev, _ = _evaluator("loc")
+    s = W.amorphous(seed=7, n_atoms=8193, density=0.025, dmin=1.8)
+    out = ev.evaluate(s)
+    check_against_oracle("loc", out, s, ev.types_of(s.numbers))
+
+
 def test_c5_batch_cells_against_oracle():
     ev, _ = _evaluator("eq")
     cells = W.small_cells()
