@@ -16,6 +16,7 @@ namespace {
 
 constexpr int kWave = 64;
 constexpr float kPi = 3.14159265358979323846f;
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
 __device__ inline float wave_sum(float v) {
 #pragma unroll
@@ -281,7 +282,10 @@ __device__ void invariant_gradient_all(const DescTables &t, const float *sL, con
 // KR / KA: basis values of a lane's record, NR: radial channels, NO: moment
 // outputs per lane (register arrays sized for the model, so the compact
 // instantiation keeps occupancy up).
-template <int KR, int KA, int NR, int NO, int CH = kWave>
+// kMfma: the moment sums of a round on the matrix cores (na <= 16 channels,
+// nlm <= 32 components): M[n][c] += sum_k gn[k][n] b[k][c] as
+// v_mfma_f32_16x16x4f32 over four records at a time, two 16-column tiles.
+template <int KR, int KA, int NR, int NO, int CH = kWave, bool kMfma = false>
 __global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Records r,
                                                               const int32_t *types, float *q,
                                                               int ldq, float *moments) {
@@ -324,6 +328,8 @@ __global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Reco
     float acc[NO];
 #pragma unroll
     for (int j = 0; j < NO; ++j) acc[j] = 0.0f;
+    floatx4_t mt[2] = {floatx4_t{0.0f, 0.0f, 0.0f, 0.0f}, floatx4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+    const int mr = lane & 15, mg = lane >> 4;   // MFMA operand row / k group
     for (int base = ab; base < ae; base += CH) {
         int e = base + lane;
         float *gl = gnL + lane * (na + 1);
@@ -358,16 +364,46 @@ __global__ void __launch_bounds__(kWave) k_descriptor_forward(DescTables t, Reco
         }
         __syncthreads();
         int cnt = min(CH, ae - base);
+        if constexpr (kMfma) {
+            // lane l feeds A[n = l%16][k] = gn[k][n] and B[k][c = 16 t + l%16] =
+            // b[k][c] for record k = k0 + l/16; zero past na, nlm and cnt
+            for (int k0 = 0; k0 < cnt; k0 += 4) {
+                const int k = k0 + mg;
+                const bool kin = k < cnt;
+                const float av = kin && mr < na ? gnL[k * (na + 1) + mr] : 0.0f;
+                const float b0 = kin && mr < nlm ? bL[k * (nlm + 1) + mr] : 0.0f;
+                const float b1 = kin && 16 + mr < nlm ? bL[k * (nlm + 1) + 16 + mr] : 0.0f;
+                mt[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b0, mt[0], 0, 0, 0);
+                mt[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b1, mt[1], 0, 0, 0);
+            }
+        } else {
 #pragma unroll
-        for (int j = 0; j < NO; ++j) {
-            int o = lane + kWave * j;
-            if (o >= nout) break;
-            int n = o / nlm, c = o - n * nlm;
-            float a = 0.0f;
-            for (int k = 0; k < cnt; ++k) a += gnL[k * (na + 1) + n] * bL[k * (nlm + 1) + c];
-            acc[j] += a;
+            for (int j = 0; j < NO; ++j) {
+                int o = lane + kWave * j;
+                if (o >= nout) break;
+                int n = o / nlm, c = o - n * nlm;
+                float a = 0.0f;
+                for (int k = 0; k < cnt; ++k) a += gnL[k * (na + 1) + n] * bL[k * (nlm + 1) + c];
+                acc[j] += a;
+            }
         }
         __syncthreads();
+    }
+    if constexpr (kMfma) {
+        // accumulator v of lane l is M[n = 4 (l/16) + v][c = 16 t + l%16]
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int n = 4 * mg + v, c = 16 * tt + mr;
+                if (n < na && c < nlm) {
+                    sL[n * nlm + c] = mt[tt][v];
+                    moments[size_t(i) * nout + n * nlm + c] = mt[tt][v];
+                }
+            }
+        __syncthreads();
+        invariants_all(t, sL, q + size_t(i) * ldq + t.nr, lane);
+        return;
     }
 #pragma unroll
     for (int j = 0; j < NO; ++j) {
@@ -1042,7 +1078,15 @@ void descriptor_forward(const DescTables &t, const Records &r, int64_t n_records
             hipLaunchKernelGGL((k_descriptor_forward_pair<kCompactKr, kCompactKa, kMaxNr,
                                                           2 * kCompactOut>),
                                grid, dim3(kWave), plds, s, t, r, types, q, ldq, moments);
-    } else if (descriptor_compact(t) && ch == 32)
+    } else if (descriptor_compact(t) && t.nlm <= 32 && ch == 32)
+        hipLaunchKernelGGL((k_descriptor_forward<kCompactKr, kCompactKa, kMaxNr, kCompactOut, 32,
+                                                 true>),
+                           dim3(r.n_atoms), dim3(kWave), lds, s, t, r, types, q, ldq, moments);
+    else if (descriptor_compact(t) && t.nlm <= 32)
+        hipLaunchKernelGGL((k_descriptor_forward<kCompactKr, kCompactKa, kMaxNr, kCompactOut,
+                                                 kWave, true>),
+                           dim3(r.n_atoms), dim3(kWave), lds, s, t, r, types, q, ldq, moments);
+    else if (descriptor_compact(t) && ch == 32)
         hipLaunchKernelGGL((k_descriptor_forward<kCompactKr, kCompactKa, kMaxNr, kCompactOut, 32>),
                            dim3(r.n_atoms), dim3(kWave), lds, s, t, r, types, q, ldq, moments);
     else if (descriptor_compact(t))
