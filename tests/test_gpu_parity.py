@@ -238,13 +238,15 @@ def test_errors_are_reported():
                  6.0, 5.0, 10, 100)
 
 
-@pytest.mark.parametrize("reps", [2, 11])   # 64 atoms: one checking block; 10,648: a grid
-def test_out_of_range_type_is_reported_and_cleared(reps):
+@pytest.mark.parametrize("model,reps", [("loc", 2), ("loc", 11), ("mp", 3)])
+def test_out_of_range_type_is_reported_and_cleared(model, reps):
     """A type outside [0, n_types) is reported by the device check (the kernels
     read a clamped copy meanwhile), and the next call with valid types is
-    unaffected: bitwise equal to the call before."""
+    unaffected: bitwise equal to the call before.  64 atoms: one checking
+    block; 10,648: a grid; the MP model also runs work on its side stream,
+    which the failed call still joins."""
     from rune_amd import _native as N
-    ev, p = _evaluator("loc")
+    ev, p = _evaluator(model)
     s = W.si_diamond(seed=3, reps=reps)
     types = torch.as_tensor(ev.types_of(s.numbers), device="cuda")
     nl = N.NeighborList().build(torch.as_tensor(s.positions, device="cuda"), [0, len(s)],
